@@ -1,0 +1,160 @@
+/*
+ * qwattn — MI355X (gfx950) full-attention hot path of the qwen4exp / Qwen3-Next engine, as a C ABI.
+ *
+ * The reference engine has no plugin ABI for attention: each backend runs it in a private
+ * `attention(l, n[, pos])` method behind `class Backend` (reference: src/backend.h:9-41). The GPU
+ * backend's body is three dispatches whose push-constant structs carry raw device addresses plus
+ * u32 dims (src/qwen4_vk.cpp:66-69, 937-996). This header exports exactly that work, one entry point
+ * per dispatch plus the state a HIP backend owns around them (KV caches, rope table, split
+ * partials), so a `HipBackend : Backend` can call it from its per-layer loop in the positions of
+ * src/qwen4_vk.cpp:1198/1255, src/vk_backend.cpp:806, src/qwen4_cpu.cpp:108 and
+ * src/cpu_backend.cpp:121.
+ *
+ * Conventions
+ *  - Every pointer argument named `*_dev` or documented as "device" is a device address on the
+ *    context's GPU; `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *  - Every function returns QWATTN_OK (0) or a negative QWATTN_E* code and never throws; the text
+ *    of the last error of a context is returned by qwattn_last_error(ctx).
+ *  - No entry point allocates device memory except qwattn_create, qwattn_kv_alloc and
+ *    qwattn_kv_grow. Launches are asynchronous on `stream`.
+ *  - A context is driven by one host thread at a time (the reference backends are not re-entrant).
+ *
+ * Data layouts (row-major, innermost last)
+ *  - qg   [n][NH][2*D]   projection output, per head the query (first D) then the gate (second D);
+ *                        fp32 or bf16 (`in_dtype`). Reference: q_proj emits 2*NH*D rows,
+ *                        src/qwen4.cpp:112, shaders/qk_norm_rope.comp:26.
+ *  - k, v [n][NKV][D]    projection outputs, same dtype as qg.
+ *  - qn, kn [D] fp32     QK-RMSNorm weights stored as (gamma - 1): the kernel multiplies by (1 + w),
+ *                        as the reference uploads them (src/qwen4_vk.cpp:444-448, qk_norm_rope.comp:33).
+ *  - rope [n_pos][R/2][2] fp32 (cos, sin) of the fp32 angle (float)p * inv_freq[i],
+ *                        inv_freq[i] = (float)(1 / theta^(2i/R)) (src/qwen4_vk.cpp:494-504).
+ *  - K cache [cap][NKV][D] fp16 — the reference's kv16 layout (src/qwen4_vk.cpp:565-574).
+ *  - V cache [cap/8][NKV][D][8] fp16 — position-interleaved in groups of 8: element (p, h, d) sits
+ *                        at ((p/8)*NKV + h)*D*8 + d*8 + p%8. This is the one layout that differs
+ *                        from the reference: it makes each 16-byte load hold 8 consecutive keys of
+ *                        one dim, which is the operand shape of the gfx950 MFMA for P*V. `cap` is a
+ *                        multiple of 8. Prefix copies by whole 8-row groups stay valid, so the
+ *                        reference's grow-by-copy (ensure_kv) carries over unchanged.
+ *  - q    [n][NH][D] fp32 normalized + rotated query (the reference's q_out).
+ *  - out  [n][NH][D] fp32 gated attention output (the reference's att_, input of o_proj).
+ */
+#ifndef QWATTN_H
+#define QWATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWATTN_OK 0
+#define QWATTN_EINVAL -1  /* bad argument (shape, pointer, range) */
+#define QWATTN_EHIP -2    /* a HIP runtime call failed */
+#define QWATTN_ENOMEM -3  /* device allocation failed */
+#define QWATTN_ERANGE -4  /* position/context overflow ("context overflow" in the reference) */
+#define QWATTN_ESTATE -5  /* call out of order (e.g. no KV cache allocated) */
+
+#define QWATTN_F32 0
+#define QWATTN_BF16 1
+#define QWATTN_F16 2
+
+typedef struct qwattn_ctx qwattn_ctx;
+
+/* Attention shape of a model (reference: Q4Config attention fields src/qwen4.h:22-25, loaded and
+ * checked at src/qwen4.cpp:17-21, 37-39; Config src/model.h:15-20). */
+typedef struct qwattn_config {
+    int n_heads;      /* NH: query heads (16 for Qwen3-Next) */
+    int n_kv_heads;   /* NKV: key/value heads (2); NH % NKV == 0 */
+    int head_dim;     /* D: 64 or 256 */
+    int rope_dim;     /* R: rotated leading dims per head, even, <= D */
+    float rope_theta; /* 1e7 */
+    float rms_eps;    /* 1e-6 */
+    int max_ctx;      /* context limit: rope table length (262144 by default, src/main.cpp:313) */
+    int max_tokens;   /* largest n per call (the reference's NMAX = 1024 chunk, src/qwen4_vk.cpp:41) */
+    int max_splits;   /* largest split-KV count (the reference caps at 64, src/qwen4_vk.cpp:976-978) */
+} qwattn_config;
+
+/* Creates a context on `device`: checks the shape, allocates the rope table for max_ctx positions
+ * and the split-KV partials for max_tokens x NH x max_splits rows, and fills the rope table.
+ * Replaces the backend constructor's rope upload (src/qwen4_vk.cpp:494-504) and the partials
+ * buffer (src/qwen4_vk.cpp:540). */
+int qwattn_create(qwattn_ctx** ctx, int device, const qwattn_config* cfg);
+int qwattn_destroy(qwattn_ctx* ctx);
+/* Text of the last error on ctx (or of the last failed qwattn_create when ctx is NULL). */
+const char* qwattn_last_error(const qwattn_ctx* ctx);
+int qwattn_get_config(const qwattn_ctx* ctx, qwattn_config* cfg);
+/* Device address of the context's rope table ([max_ctx][R/2][2] fp32). */
+int qwattn_rope_table(const qwattn_ctx* ctx, const float** rope);
+
+/* Fills a caller-owned table rope[n_pos][R/2][2] on the GPU with the same values as the context's
+ * (reference: the rope loop of upload_weights, src/qwen4_vk.cpp:494-504). */
+int qwattn_fill_rope(qwattn_ctx* ctx, void* stream, float* rope, int n_pos);
+
+/* ---- KV cache owned by the context (reference: alloc_state / ensure_kv, src/qwen4_vk.cpp:565-574,
+ * 657-685) ---- */
+/* Allocates n_slots (one per full-attention layer) K and V caches of `cap` tokens (rounded up to a
+ * multiple of 8, at most max_ctx), zero-filled. Any previous caches are freed. */
+int qwattn_kv_alloc(qwattn_ctx* ctx, int n_slots, int cap);
+/* Grows every slot to hold `tokens` positions: new capacity max(2*cap, tokens), at most max_ctx,
+ * copying each slot's rows; no-op when tokens <= cap. Synchronizes `stream`. Same contract as
+ * ensure_kv: call between passes. */
+int qwattn_kv_grow(qwattn_ctx* ctx, void* stream, int tokens);
+/* Current capacity in tokens and the device addresses of one slot's caches. */
+int qwattn_kv_slot(const qwattn_ctx* ctx, int slot, void** kcache, void** vcache, int* cap);
+
+/* ---- Kernels (one entry point per reference dispatch) ---- */
+
+/* Fused QK-RMSNorm + partial RoPE + KV append (reference: shaders/qk_norm_rope.comp, pipeline
+ * qk_norm_rope_kv16, dispatched at src/qwen4_vk.cpp:968-972 with PcQkRope). For each token t < n at
+ * position p = pos + t and each head: y = x * rsqrt(mean(x^2) + eps) * (1 + w), rotate-half RoPE on
+ * the first R dims from `rope` row p; query heads write q_out[t][h], key heads write K cache row p
+ * and V is copied to V cache row p. `q_dtype` is QWATTN_F32 (the reference's q_out) or QWATTN_F16
+ * (prefill operand: fp16, pre-multiplied by log2(e)/sqrt(D)). `kv_cap` is the caches' capacity;
+ * pos + n must not exceed it. */
+int qwattn_qk_norm_rope_append(qwattn_ctx* ctx, void* stream, const void* qg, const void* k,
+                               const void* v, int in_dtype, const float* qn, const float* kn,
+                               const float* rope, void* kcache, void* vcache, int kv_cap, void* q_out,
+                               int q_dtype, int pos, int n);
+
+/* Split-KV causal GQA attention partials (reference: shaders/attention.comp, pipeline
+ * attention_kv16, dispatched at src/qwen4_vk.cpp:985-988 with PcAttn). Token t attends to keys
+ * [0, pos+t+1); the keys [0, pos+n) are cut into `n_split` chunks (0 = automatic), and each
+ * workgroup serves all NH/NKV query heads of one KV head for one chunk, so every K/V row is read
+ * from HBM once. Requires n * NH/NKV <= 32 (decode n=1, MTP verify n<=4 at NH/NKV=8). Partials
+ * (running max in log2 units, sum, unnormalized o[D]) go to the context's scratch; returns the
+ * split count actually used in *used_splits (may be NULL). */
+int qwattn_attend_partial(qwattn_ctx* ctx, void* stream, const float* q, const void* kcache,
+                          const void* vcache, int kv_cap, int pos, int n, int n_split,
+                          int* used_splits);
+
+/* Log-sum-exp merge of the partials of the last qwattn_attend_partial plus the sigmoid output gate
+ * (reference: shaders/attn_combine.comp, dispatched at src/qwen4_vk.cpp:990-992 with
+ * PcAttnCombine): out[t][h][d] = (sum_z o_z e^{m_z-M}) / (sum_z l_z e^{m_z-M}) * sigmoid(gate),
+ * gate = qg[t][h][D + d]; splits with l = 0 are skipped. */
+int qwattn_combine(qwattn_ctx* ctx, void* stream, const void* qg, int in_dtype, float* out, int n,
+                   int n_split);
+
+/* Causal chunked prefill on MFMA: out = softmax(q K^T / sqrt(D)) V * sigmoid(gate) for n tokens at
+ * positions pos.. pos+n-1 against keys [0, pos+t+1), in one kernel (no split partials). The
+ * reference runs prefill chunks through the same split-K shader (src/qwen4_vk.cpp:974-978); this is
+ * its matrix-core replacement. `q` is QWATTN_F16 pre-scaled (see qwattn_qk_norm_rope_append) or
+ * QWATTN_F32 unscaled (`q_dtype`). */
+int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dtype,
+                          const void* kcache, const void* vcache, int kv_cap, const void* qg,
+                          int in_dtype, float* out, int pos, int n);
+
+/* The whole attention body between the projections, for one full-attention layer `slot` of the
+ * context's caches (reference: the dispatches of Qwen4Vulkan::attention, src/qwen4_vk.cpp:968-992;
+ * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): norm + rope + append,
+ * then split-KV attend + combine for n * NH/NKV <= 32, else the MFMA prefill kernel. `n_split` as in
+ * qwattn_attend_partial. The normalized query goes to a context-owned buffer. */
+int qwattn_layer_attention(qwattn_ctx* ctx, void* stream, int slot, const void* qg, const void* k,
+                           const void* v, int in_dtype, const float* qn, const float* kn, float* out,
+                           int pos, int n, int n_split);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWATTN_H */

@@ -1,0 +1,209 @@
+"""qwattn: the MI355X full-attention hot path of the qwen4exp / Qwen3-Next engine.
+
+Python mirror of the C ABI in include/qwattn.h, used by the tests and bench.py. Device memory and
+streams come from PyTorch (plumbing only); every computation runs in libqwattn.so's HIP kernels.
+There is no fallback: if the library is missing, or a call fails, an error is raised, the way the
+reference backends throw std::runtime_error (src/vk_common.h:19-23, src/qwen4_vk.cpp:304).
+
+The package directory name carries a hyphen, so it is loaded by path (see load_package in
+tests/conftest.py, bench.py and __graft_entry__.py) under the module name `qwattn_amd`.
+"""
+import ctypes
+import os
+
+import torch  # loads the HIP runtime that libqwattn.so then shares
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libqwattn.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "qwattn.h")
+
+OK, EINVAL, EHIP, ENOMEM, ERANGE, ESTATE = 0, -1, -2, -3, -4, -5
+F32, BF16, F16 = 0, 1, 2
+LOG2E = 1.4426950408889634
+
+
+class QwattnError(RuntimeError):
+    """A nonzero status from the C ABI, with qwattn_last_error's text."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"{msg} (status {code})")
+        self.code = code
+
+
+class Config(ctypes.Structure):
+    _fields_ = [("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+                ("rope_dim", ctypes.c_int), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
+                ("max_ctx", ctypes.c_int), ("max_tokens", ctypes.c_int), ("max_splits", ctypes.c_int)]
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+
+def load_library():
+    """Loads libqwattn.so (built by build.py); raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    lib = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "qwattn_create": [ctypes.POINTER(_P), _I, ctypes.POINTER(Config)],
+        "qwattn_destroy": [_P],
+        "qwattn_get_config": [_P, ctypes.POINTER(Config)],
+        "qwattn_rope_table": [_P, ctypes.POINTER(_P)],
+        "qwattn_fill_rope": [_P, _P, _P, _I],
+        "qwattn_kv_alloc": [_P, _I, _I],
+        "qwattn_kv_grow": [_P, _P, _I],
+        "qwattn_kv_slot": [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_I)],
+        "qwattn_qk_norm_rope_append": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I],
+        "qwattn_attend_partial": [_P, _P, _P, _P, _P, _I, _I, _I, _I, ctypes.POINTER(_I)],
+        "qwattn_combine": [_P, _P, _P, _I, _P, _I, _I],
+        "qwattn_attend_prefill": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I],
+        "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
+    }
+    for name, args in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = _I
+    lib.qwattn_last_error.argtypes = [_P]
+    lib.qwattn_last_error.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def header_functions():
+    """Names of the functions include/qwattn.h declares."""
+    import re
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(qwattn_\w+)\s*\(", text, re.M)))
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+def v_rows(vcache, cap, n_kv, d):
+    """[cap/8][NKV][D][8] interleaved V cache -> [cap][NKV][D] rows (a copy)."""
+    return vcache.view(cap // 8, n_kv, d, 8).permute(0, 3, 1, 2).reshape(cap, n_kv, d)
+
+
+def v_interleave(rows):
+    """[cap][NKV][D] rows -> the [cap/8][NKV][D][8] interleaved V cache layout (cap % 8 == 0)."""
+    cap, n_kv, d = rows.shape
+    return rows.view(cap // 8, 8, n_kv, d).permute(0, 2, 3, 1).contiguous().view(-1)
+
+
+class Attention:
+    """One qwattn context: attention shape, rope table, split partials and (optionally) K/V caches."""
+
+    def __init__(self, n_heads, n_kv_heads, head_dim, rope_dim, rope_theta=1e7, rms_eps=1e-6, max_ctx=262144,
+                 max_tokens=2048, max_splits=1024, device=0):
+        self.lib = load_library()
+        self.cfg = Config(n_heads, n_kv_heads, head_dim, rope_dim, rope_theta, rms_eps, max_ctx, max_tokens,
+                          max_splits)
+        self.device = device
+        h = ctypes.c_void_p()
+        rc = self.lib.qwattn_create(ctypes.byref(h), device, ctypes.byref(self.cfg))
+        if rc:
+            raise QwattnError(rc, self.lib.qwattn_last_error(None).decode())
+        self.h = h
+        self.NH, self.NKV, self.D, self.R = n_heads, n_kv_heads, head_dim, rope_dim
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.qwattn_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc:
+            raise QwattnError(rc, self.lib.qwattn_last_error(self.h).decode())
+
+    # ---- state ---------------------------------------------------------------------------------------
+    def rope_table(self):
+        """The context's rope table as a [max_ctx, R/2, 2] float32 tensor view (device memory)."""
+        p = ctypes.c_void_p()
+        self._check(self.lib.qwattn_rope_table(self.h, ctypes.byref(p)))
+        n = self.cfg.max_ctx * (self.R // 2) * 2
+        return _wrap_device_floats(p.value, n, self.device).view(self.cfg.max_ctx, self.R // 2, 2)
+
+    def fill_rope(self, table, n_pos, stream=None):
+        self._check(self.lib.qwattn_fill_rope(self.h, _stream(stream), _ptr(table), n_pos))
+
+    def kv_alloc(self, n_slots, cap):
+        self._check(self.lib.qwattn_kv_alloc(self.h, n_slots, cap))
+
+    def kv_grow(self, tokens, stream=None):
+        self._check(self.lib.qwattn_kv_grow(self.h, _stream(stream), tokens))
+
+    def kv_slot(self, slot):
+        """(K cache [cap, NKV, D] fp16 view, V cache flat fp16 view in the interleaved layout, cap)."""
+        k, v, cap = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int()
+        self._check(self.lib.qwattn_kv_slot(self.h, slot, ctypes.byref(k), ctypes.byref(v), ctypes.byref(cap)))
+        n = cap.value * self.NKV * self.D
+        kc = _wrap_device_halfs(k.value, n, self.device).view(cap.value, self.NKV, self.D)
+        vc = _wrap_device_halfs(v.value, n, self.device)
+        return kc, vc, cap.value
+
+    # ---- kernels -------------------------------------------------------------------------------------
+    def qk_norm_rope_append(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, q_out, pos, n, stream=None):
+        self._check(self.lib.qwattn_qk_norm_rope_append(
+            self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
+            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(q_out), _DT[q_out.dtype], pos, n))
+
+    def attend_partial(self, q, kcache, vcache, kv_cap, pos, n, n_split=0, stream=None):
+        used = ctypes.c_int()
+        self._check(self.lib.qwattn_attend_partial(self.h, _stream(stream), _ptr(q), _ptr(kcache), _ptr(vcache),
+                                                   kv_cap, pos, n, n_split, ctypes.byref(used)))
+        return used.value
+
+    def combine(self, qg, out, n, n_split, stream=None):
+        self._check(self.lib.qwattn_combine(self.h, _stream(stream), _ptr(qg), _DT[qg.dtype], _ptr(out), n, n_split))
+
+    def attend_prefill(self, q, kcache, vcache, kv_cap, qg, out, pos, n, stream=None):
+        self._check(self.lib.qwattn_attend_prefill(self.h, _stream(stream), _ptr(q), _DT[q.dtype], _ptr(kcache),
+                                                   _ptr(vcache), kv_cap, _ptr(qg), _DT[qg.dtype], _ptr(out), pos, n))
+
+    def attend(self, q, kcache, vcache, kv_cap, qg, out, pos, n, n_split=0, stream=None):
+        """Split-KV + combine when n * NH/NKV <= 32, else the prefill kernel (q fp32 unscaled)."""
+        if n * (self.NH // self.NKV) <= 32:
+            used = self.attend_partial(q, kcache, vcache, kv_cap, pos, n, n_split, stream)
+            self.combine(qg, out, n, used, stream)
+        else:
+            self.attend_prefill(q, kcache, vcache, kv_cap, qg, out, pos, n, stream)
+
+    def layer_attention(self, slot, qg, k, v, qn, kn, out, pos, n, n_split=0, stream=None):
+        self._check(self.lib.qwattn_layer_attention(self.h, _stream(stream), slot, _ptr(qg), _ptr(k), _ptr(v),
+                                                    _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(out), pos, n, n_split))
+
+
+class _DeviceArray:
+    """Minimal __cuda_array_interface__ exporter so torch can view library-owned device memory."""
+
+    def __init__(self, ptr, n, typestr):
+        self.__cuda_array_interface__ = {"shape": (n,), "typestr": typestr, "data": (ptr, False), "version": 3,
+                                         "strides": None}
+
+
+def _wrap_device_floats(ptr, n, device):
+    return torch.as_tensor(_DeviceArray(ptr, n, "<f4"), device=f"cuda:{device}")
+
+
+def _wrap_device_halfs(ptr, n, device):
+    return torch.as_tensor(_DeviceArray(ptr, n, "<f2"), device=f"cuda:{device}")

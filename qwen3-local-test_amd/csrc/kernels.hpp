@@ -1,0 +1,59 @@
+// Host-side launchers of the gfx950 kernels (internal to libqwattn; the C ABI in qwattn.cpp checks
+// every shape and pointer before calling these).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qw {
+
+constexpr float kLog2eHost = 1.4426950408889634f;
+
+struct NormRopeArgs {
+    const void* qg;      // [n][NH][2D]
+    const void* k;       // [n][NKV][D]
+    const void* v;       // [n][NKV][D]
+    const float* qn;     // [D], multiplier (1 + w)
+    const float* kn;     // [D]
+    const float* rope;   // [>= pos+n][R/2][2]
+    uint16_t* kcache;    // [cap][NKV][D] fp16
+    uint16_t* vcache;    // [cap/8][NKV][D][8] fp16
+    void* q_out;         // [n][NH][D] fp32, or fp16 pre-scaled by log2(e)/sqrt(D)
+    int pos, n, NH, NKV, R;
+    float eps, q_scale;
+};
+hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int D, int in_dtype, int q_dtype, hipStream_t s);
+
+struct SplitArgs {
+    const float* q;       // [n][NH][D] fp32 (normalized, rotated, not scaled)
+    const uint16_t* kc;   // [cap][NKV][D]
+    const uint16_t* vc;   // [cap/8][NKV][D][8]
+    float* part_o;        // [n*NH][n_split][D]
+    float* part_ml;       // [n*NH][n_split][2]: running max (log2 units), sum
+    int pos, n, NH, NKV, chunk, n_split;
+    float q_scale;        // log2(e) / sqrt(D)
+};
+hipError_t launch_attend_split(const SplitArgs& a, int D, hipStream_t s);
+
+struct CombineArgs {
+    const float* part_o;
+    const float* part_ml;
+    const void* qg;       // gate = qg[t][h][D + d]
+    float* out;           // [n][NH][D]
+    int n, NH, n_split;
+};
+hipError_t launch_combine(const CombineArgs& a, int D, int in_dtype, hipStream_t s);
+
+struct PrefillArgs {
+    const void* q;        // [n][NH][D]: fp16 pre-scaled, or fp32 unscaled
+    const uint16_t* kc;
+    const uint16_t* vc;
+    const void* qg;       // gate source
+    float* out;           // [n][NH][D]
+    int pos, n, NH, NKV;
+    float q_scale;
+};
+hipError_t launch_prefill(const PrefillArgs& a, int D, int q_dtype, int in_dtype, hipStream_t s);
+
+hipError_t launch_rope_table(float* rope, const float* inv_freq, int n_pos, int R, hipStream_t s);
+
+}  // namespace qw

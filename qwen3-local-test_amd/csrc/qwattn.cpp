@@ -1,0 +1,363 @@
+// C ABI of the MI355X attention hot path (declared in include/qwattn.h).
+//
+// Host-side counterpart of the reference's attention dispatch (src/qwen4_vk.cpp:937-996): it owns
+// what the Vulkan backend owns around the three dispatches — rope table (:494-504), split partials
+// (:540), fp16 K/V caches with grow-by-doubling (:565-574, 657-685) — checks every shape, pointer
+// and range on the host before a kernel is launched (a kernel never sees an out-of-range position),
+// and turns failures into status codes plus qwattn_last_error text instead of exceptions.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/qwattn.h"
+#include "kernels.hpp"
+
+struct qwattn_ctx {
+    int device = 0;
+    int n_cu = 0;
+    qwattn_config cfg{};
+    float* inv_freq = nullptr;   // [R/2]
+    float* rope = nullptr;       // [max_ctx][R/2][2]
+    float* part_o = nullptr;     // [split_rows][max_splits][D]
+    float* part_ml = nullptr;    // [split_rows][max_splits][2]
+    float* q32 = nullptr;        // [max_tokens][NH][D] layer-path query (fp32)
+    void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
+    int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
+    int last_splits = 0;         // split count of the last qwattn_attend_partial
+    int last_n = 0;
+    std::vector<uint16_t*> kc, vc;
+    int kv_cap = 0;
+    std::string err;
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+int fail(qwattn_ctx* c, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf;
+    else g_create_err = buf;
+    return code;
+}
+
+// Makes the context's device current for the duration of a call and restores the caller's.
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+#define HIP_TRY(c, expr)                                                                             \
+    do {                                                                                             \
+        hipError_t e_ = (expr);                                                                      \
+        if (e_ != hipSuccess) return fail((c), QWATTN_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+
+int check_shape(qwattn_ctx* c, const qwattn_config& g) {
+    if (g.n_heads <= 0 || g.n_kv_heads <= 0 || g.n_heads % g.n_kv_heads)
+        return fail(c, QWATTN_EINVAL, "unsupported attention head counts (%d, %d)", g.n_heads, g.n_kv_heads);
+    if (g.head_dim != 64 && g.head_dim != 128 && g.head_dim != 256)
+        return fail(c, QWATTN_EINVAL, "head_dim %d not supported (64, 128, 256)", g.head_dim);
+    const int dpl = g.head_dim / 64;
+    if (g.rope_dim < 0 || g.rope_dim > g.head_dim || g.rope_dim % 2 || (g.rope_dim / 2) % dpl)
+        return fail(c, QWATTN_EINVAL, "unsupported rope dimension %d", g.rope_dim);
+    const int G = g.n_heads / g.n_kv_heads;
+    if (G > 32 || 128 % G)
+        return fail(c, QWATTN_EINVAL, "GQA group %d not supported (a power of two <= 32)", G);
+    if (g.max_ctx <= 0 || g.max_tokens <= 0 || g.max_splits <= 0 || g.max_ctx > (1 << 26))
+        return fail(c, QWATTN_EINVAL, "bad limits (max_ctx %d, max_tokens %d, max_splits %d)", g.max_ctx, g.max_tokens, g.max_splits);
+    if (!(g.rms_eps >= 0.f) || !(g.rope_theta > 0.f)) return fail(c, QWATTN_EINVAL, "bad eps/theta");
+    return QWATTN_OK;
+}
+
+int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
+    if (n < 1) return fail(c, QWATTN_EINVAL, "n = %d", n);
+    if (pos < 0) return fail(c, QWATTN_EINVAL, "pos = %d", pos);
+    if (n > c->cfg.max_tokens) return fail(c, QWATTN_EINVAL, "n = %d exceeds max_tokens %d", n, c->cfg.max_tokens);
+    if ((long long)pos + n > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow (%d + %d > %d)", pos, n, c->cfg.max_ctx);
+    if ((long long)pos + n > kv_cap) return fail(c, QWATTN_ERANGE, "context overflow: %d + %d rows exceed the K/V cache capacity %d", pos, n, kv_cap);
+    if (kv_cap % 8) return fail(c, QWATTN_EINVAL, "K/V cache capacity %d is not a multiple of 8", kv_cap);
+    return QWATTN_OK;
+}
+
+// The split chunk: ceil(maxlen / n_split) rounded up to the 32-key tile; n_split 0 = automatic (about
+// two workgroups per CU, at least one 32-key tile per wave).
+void pick_split(const qwattn_ctx* c, int maxlen, int n_split, int* chunk, int* used) {
+    if (n_split <= 0) {
+        const int target = std::max(1, 2 * c->n_cu / c->cfg.n_kv_heads);
+        int ch = (maxlen + target - 1) / target;
+        ch = std::max(128, (ch + 127) / 128 * 128);
+        n_split = (maxlen + ch - 1) / ch;
+    }
+    n_split = std::min(n_split, c->cfg.max_splits);
+    int ch = (maxlen + n_split - 1) / n_split;
+    ch = (ch + 31) / 32 * 32;
+    *chunk = ch;
+    *used = (maxlen + ch - 1) / ch;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qwattn_last_error(const qwattn_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_err.c_str(); }
+
+int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
+    if (!out || !cfg) return fail(nullptr, QWATTN_EINVAL, "null argument");
+    *out = nullptr;
+    int rc = check_shape(nullptr, *cfg);
+    if (rc) return rc;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+        return fail(nullptr, QWATTN_EINVAL, "device %d not available (%d devices)", device, ndev);
+    qwattn_ctx* c = new qwattn_ctx;
+    c->device = device;
+    c->cfg = *cfg;
+    DeviceGuard dg(device);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        delete c;
+        return fail(nullptr, QWATTN_EHIP, "hipGetDeviceProperties failed");
+    }
+    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0) {
+        delete c;
+        return fail(nullptr, QWATTN_EINVAL, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    }
+    c->n_cu = prop.multiProcessorCount;
+    const int NH = cfg->n_heads, NKV = cfg->n_kv_heads, D = cfg->head_dim, R = cfg->rope_dim;
+    c->split_rows = 32 * NKV;
+    const size_t rope_n = (size_t)cfg->max_ctx * std::max(1, R / 2) * 2;
+    const size_t part = (size_t)c->split_rows * cfg->max_splits;
+    const size_t qn = (size_t)cfg->max_tokens * NH * D;
+    bool ok = hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
+              hipMalloc(&c->rope, sizeof(float) * rope_n) == hipSuccess &&
+              hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
+              hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
+              hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess;
+    if (!ok) {
+        qwattn_destroy(c);
+        return fail(nullptr, QWATTN_ENOMEM, "out of device memory creating the context");
+    }
+    // inv_freq[i] = (float)(1 / theta^(2i/R)) in double, as src/qwen4_vk.cpp:499 / src/qwen4_cpu.cpp:38-39
+    std::vector<float> inv(std::max(1, R / 2), 0.f);
+    for (int i = 0; i < R / 2; i++) inv[i] = (float)(1.0 / std::pow((double)cfg->rope_theta, (2.0 * i) / R));
+    if (hipMemcpy(c->inv_freq, inv.data(), sizeof(float) * inv.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
+        hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        qwattn_destroy(c);
+        return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
+    }
+    *out = c;
+    return QWATTN_OK;
+}
+
+int qwattn_destroy(qwattn_ctx* c) {
+    if (!c) return QWATTN_OK;
+    DeviceGuard dg(c->device);
+    (void)hipDeviceSynchronize();
+    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->q32, c->q16})
+        if (p) (void)hipFree(p);
+    for (auto* p : c->kc) (void)hipFree(p);
+    for (auto* p : c->vc) (void)hipFree(p);
+    delete c;
+    return QWATTN_OK;
+}
+
+int qwattn_get_config(const qwattn_ctx* c, qwattn_config* cfg) {
+    if (!c || !cfg) return QWATTN_EINVAL;
+    *cfg = c->cfg;
+    return QWATTN_OK;
+}
+
+int qwattn_rope_table(const qwattn_ctx* c, const float** rope) {
+    if (!c || !rope) return QWATTN_EINVAL;
+    *rope = c->rope;
+    return QWATTN_OK;
+}
+
+int qwattn_fill_rope(qwattn_ctx* c, void* stream, float* rope, int n_pos) {
+    if (!c) return QWATTN_EINVAL;
+    if (!rope || n_pos <= 0) return fail(c, QWATTN_EINVAL, "qwattn_fill_rope: bad table");
+    if (c->cfg.rope_dim == 0) return QWATTN_OK;
+    DeviceGuard dg(c->device);
+    HIP_TRY(c, qw::launch_rope_table(rope, c->inv_freq, n_pos, c->cfg.rope_dim, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+// ---- KV cache ---------------------------------------------------------------------------------------
+
+int qwattn_kv_alloc(qwattn_ctx* c, int n_slots, int cap) {
+    if (!c) return QWATTN_EINVAL;
+    if (n_slots <= 0 || cap <= 0) return fail(c, QWATTN_EINVAL, "qwattn_kv_alloc: %d slots of %d tokens", n_slots, cap);
+    cap = std::min((cap + 7) / 8 * 8, (c->cfg.max_ctx + 7) / 8 * 8);
+    DeviceGuard dg(c->device);
+    for (auto* p : c->kc) (void)hipFree(p);
+    for (auto* p : c->vc) (void)hipFree(p);
+    c->kc.assign(n_slots, nullptr);
+    c->vc.assign(n_slots, nullptr);
+    c->kv_cap = 0;
+    const size_t bytes = (size_t)cap * c->cfg.n_kv_heads * c->cfg.head_dim * 2;
+    for (int s = 0; s < n_slots; s++) {
+        if (hipMalloc(&c->kc[s], bytes) != hipSuccess || hipMalloc(&c->vc[s], bytes) != hipSuccess)
+            return fail(c, QWATTN_ENOMEM, "out of device memory allocating the K/V caches");
+        HIP_TRY(c, hipMemset(c->kc[s], 0, bytes));
+        HIP_TRY(c, hipMemset(c->vc[s], 0, bytes));
+    }
+    HIP_TRY(c, hipDeviceSynchronize());
+    c->kv_cap = cap;
+    return QWATTN_OK;
+}
+
+int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
+    if (!c) return QWATTN_EINVAL;
+    if (c->kc.empty()) return fail(c, QWATTN_ESTATE, "qwattn_kv_grow: no K/V cache allocated");
+    if (tokens <= c->kv_cap) return QWATTN_OK;
+    if (tokens > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow growing the K/V caches to %d", tokens);
+    long long cap = std::max<long long>(2ll * c->kv_cap, tokens);
+    cap = std::min<long long>(cap, (c->cfg.max_ctx + 7) / 8 * 8);
+    cap = (cap + 7) / 8 * 8;
+    DeviceGuard dg(c->device);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t per = (size_t)c->cfg.n_kv_heads * c->cfg.head_dim * 2;
+    const size_t old_bytes = (size_t)c->kv_cap * per, bytes = (size_t)cap * per;
+    for (size_t i = 0; i < c->kc.size(); i++) {
+        uint16_t* nk = nullptr;
+        uint16_t* nv = nullptr;
+        if (hipMalloc(&nk, bytes) != hipSuccess || hipMalloc(&nv, bytes) != hipSuccess) {
+            if (nk) (void)hipFree(nk);
+            return fail(c, QWATTN_ENOMEM, "out of VRAM growing the K/V caches");
+        }
+        // both layouts keep rows [0, cap) as a prefix (the V interleave groups 8 whole positions)
+        HIP_TRY(c, hipMemsetAsync(nk, 0, bytes, s));
+        HIP_TRY(c, hipMemsetAsync(nv, 0, bytes, s));
+        HIP_TRY(c, hipMemcpyAsync(nk, c->kc[i], old_bytes, hipMemcpyDeviceToDevice, s));
+        HIP_TRY(c, hipMemcpyAsync(nv, c->vc[i], old_bytes, hipMemcpyDeviceToDevice, s));
+        HIP_TRY(c, hipStreamSynchronize(s));
+        (void)hipFree(c->kc[i]);
+        (void)hipFree(c->vc[i]);
+        c->kc[i] = nk;
+        c->vc[i] = nv;
+    }
+    c->kv_cap = (int)cap;
+    return QWATTN_OK;
+}
+
+int qwattn_kv_slot(const qwattn_ctx* c, int slot, void** kcache, void** vcache, int* cap) {
+    if (!c || slot < 0 || slot >= (int)c->kc.size()) return QWATTN_EINVAL;
+    if (kcache) *kcache = c->kc[slot];
+    if (vcache) *vcache = c->vc[slot];
+    if (cap) *cap = c->kv_cap;
+    return QWATTN_OK;
+}
+
+// ---- kernels ----------------------------------------------------------------------------------------
+
+int qwattn_qk_norm_rope_append(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v,
+                               int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
+                               void* vcache, int kv_cap, void* q_out, int q_dtype, int pos, int n) {
+    if (!c) return QWATTN_EINVAL;
+    if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || !q_out || (!rope && c->cfg.rope_dim))
+        return fail(c, QWATTN_EINVAL, "qwattn_qk_norm_rope_append: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    if (q_dtype != QWATTN_F32 && q_dtype != QWATTN_F16) return fail(c, QWATTN_EINVAL, "q_dtype %d", q_dtype);
+    int rc = check_call(c, pos, n, kv_cap);
+    if (rc) return rc;
+    DeviceGuard dg(c->device);
+    const qwattn_config& g = c->cfg;
+    qw::NormRopeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, q_out,
+                       pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, g.rms_eps,
+                       qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+    HIP_TRY(c, qw::launch_qk_norm_rope(a, g.head_dim, in_dtype, q_dtype == QWATTN_F16 ? 1 : 0, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const void* kcache, const void* vcache,
+                          int kv_cap, int pos, int n, int n_split, int* used_splits) {
+    if (!c) return QWATTN_EINVAL;
+    if (!q || !kcache || !vcache) return fail(c, QWATTN_EINVAL, "qwattn_attend_partial: null pointer");
+    int rc = check_call(c, pos, n, kv_cap);
+    if (rc) return rc;
+    const qwattn_config& g = c->cfg;
+    const int G = g.n_heads / g.n_kv_heads;
+    if (n * G > 32)
+        return fail(c, QWATTN_EINVAL, "qwattn_attend_partial: n * NH/NKV = %d > 32 rows (use the prefill kernel)", n * G);
+    int chunk = 0, used = 0;
+    pick_split(c, pos + n, n_split, &chunk, &used);
+    DeviceGuard dg(c->device);
+    qw::SplitArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, c->part_o, c->part_ml, pos, n,
+                    g.n_heads, g.n_kv_heads, chunk, used, qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+    HIP_TRY(c, qw::launch_attend_split(a, g.head_dim, (hipStream_t)stream));
+    c->last_splits = used;
+    c->last_n = n;
+    if (used_splits) *used_splits = used;
+    return QWATTN_OK;
+}
+
+int qwattn_combine(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, float* out, int n, int n_split) {
+    if (!c) return QWATTN_EINVAL;
+    if (!qg || !out) return fail(c, QWATTN_EINVAL, "qwattn_combine: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    if (c->last_splits == 0) return fail(c, QWATTN_ESTATE, "qwattn_combine: no partials (call qwattn_attend_partial first)");
+    if (n != c->last_n || n_split != c->last_splits)
+        return fail(c, QWATTN_EINVAL, "qwattn_combine: n=%d splits=%d do not match the last partials (n=%d splits=%d)", n,
+                    n_split, c->last_n, c->last_splits);
+    DeviceGuard dg(c->device);
+    qw::CombineArgs a{c->part_o, c->part_ml, qg, out, n, c->cfg.n_heads, n_split};
+    HIP_TRY(c, qw::launch_combine(a, c->cfg.head_dim, in_dtype, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtype, const void* kcache,
+                          const void* vcache, int kv_cap, const void* qg, int in_dtype, float* out, int pos, int n) {
+    if (!c) return QWATTN_EINVAL;
+    if (!q || !kcache || !vcache || !qg || !out) return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill: null pointer");
+    if (q_dtype != QWATTN_F32 && q_dtype != QWATTN_F16) return fail(c, QWATTN_EINVAL, "q_dtype %d", q_dtype);
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    int rc = check_call(c, pos, n, kv_cap);
+    if (rc) return rc;
+    const qwattn_config& g = c->cfg;
+    DeviceGuard dg(c->device);
+    qw::PrefillArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, qg, out, pos, n, g.n_heads, g.n_kv_heads,
+                      qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+    HIP_TRY(c, qw::launch_prefill(a, g.head_dim, q_dtype == QWATTN_F16 ? 2 : 0, in_dtype, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg, const void* k, const void* v,
+                           int in_dtype, const float* qn, const float* kn, float* out, int pos, int n, int n_split) {
+    if (!c) return QWATTN_EINVAL;
+    if (slot < 0 || slot >= (int)c->kc.size())
+        return fail(c, QWATTN_ESTATE, "qwattn_layer_attention: slot %d of %d allocated K/V caches", slot, (int)c->kc.size());
+    const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
+    const bool split = n * G <= 32;
+    int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
+                                        c->kv_cap, split ? (void*)c->q32 : c->q16, split ? QWATTN_F32 : QWATTN_F16, pos, n);
+    if (rc) return rc;
+    if (split) {
+        int used = 0;
+        rc = qwattn_attend_partial(c, stream, c->q32, c->kc[slot], c->vc[slot], c->kv_cap, pos, n, n_split, &used);
+        if (rc) return rc;
+        return qwattn_combine(c, stream, qg, in_dtype, out, n, used);
+    }
+    return qwattn_attend_prefill(c, stream, c->q16, QWATTN_F16, c->kc[slot], c->vc[slot], c->kv_cap, qg, in_dtype, out,
+                                 pos, n);
+}
+
+}  // extern "C"

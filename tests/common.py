@@ -1,0 +1,87 @@
+"""Shared helpers of the test suite: package loading, seeded inputs, the parity criterion."""
+import importlib.util
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG_DIR = os.path.join(ROOT, "qwen3-local-test_amd")
+
+# Parity bar on the attention output: max-abs <= 2e-3 and relative <= 1e-2,
+# the relative error measured as ||gpu - ref||_2 / ||ref||_2 (elementwise relative error is
+# ill-conditioned where long-context outputs are close to 0).
+ATOL = 2e-3
+RTOL = 1e-2
+
+
+def load_package():
+    """Imports qwen3-local-test_amd/ (hyphenated, so by path) as the module `qwattn_amd`."""
+    if "qwattn_amd" in sys.modules:
+        return sys.modules["qwattn_amd"]
+    spec = importlib.util.spec_from_file_location("qwattn_amd", os.path.join(PKG_DIR, "__init__.py"),
+                                                  submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["qwattn_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def parity(out, ref, atol=ATOL, rtol=RTOL):
+    """(max_abs, rel_l2, allclose) of out vs ref."""
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    d = out - ref
+    max_abs = float(np.max(np.abs(d))) if d.size else 0.0
+    rel = float(np.linalg.norm(d) / max(np.linalg.norm(ref), 1e-30))
+    close = bool(np.allclose(out, ref, atol=atol, rtol=rtol))
+    return max_abs, rel, close
+
+
+def assert_parity(out, ref, what="", atol=ATOL, rtol=RTOL):
+    max_abs, rel, close = parity(out, ref, atol, rtol)
+    assert np.all(np.isfinite(out)), f"{what}: non-finite output"
+    assert max_abs <= atol and rel <= rtol, f"{what}: max_abs {max_abs:.3e} rel_l2 {rel:.3e} (allclose {close})"
+    return max_abs, rel
+
+
+class Shape:
+    def __init__(self, NH, NKV, D, R, theta=1e7, eps=1e-6):
+        self.NH, self.NKV, self.D, self.R, self.theta, self.eps = NH, NKV, D, R, theta, eps
+        self.G = NH // NKV
+
+    def __repr__(self):
+        return f"{self.NH}q/{self.NKV}kv/d{self.D}/r{self.R}"
+
+
+TINY = Shape(4, 1, 64, 16)
+TINY_GGUF = Shape(2, 1, 256, 64)    # tests/make_tiny_gguf.py:10, 151 of the reference
+QWEN3_NEXT = Shape(16, 2, 256, 64)  # src/model.h:15-20 of the reference
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def projections(seed, n, s, gamma_sd=0.1):
+    """Seeded projection outputs: qg [n,NH,2D] (query | gate), k, v [n,NKV,D] ~ N(0,1), and QK-norm
+    weights w with gamma = 1 + w, w ~ gamma_sd * N(0,1)."""
+    r = rng(seed)
+    qg = r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32)
+    k = r.standard_normal((n, s.NKV, s.D)).astype(np.float32)
+    v = r.standard_normal((n, s.NKV, s.D)).astype(np.float32)
+    qn = (gamma_sd * r.standard_normal(s.D)).astype(np.float32)
+    kn = (gamma_sd * r.standard_normal(s.D)).astype(np.float32)
+    return qg, k, v, qn, kn
+
+
+def cache_rows(seed, rows, s, heavy_frac=0.0, heavy_scale=8.0):
+    """Seeded fp16 K/V cache rows [rows, NKV, D] ~ N(0,1); a fraction of key rows scaled (post-norm, so
+    the scale survives)."""
+    r = rng(seed)
+    k = r.standard_normal((rows, s.NKV, s.D)).astype(np.float32)
+    v = r.standard_normal((rows, s.NKV, s.D)).astype(np.float32)
+    if heavy_frac > 0:
+        idx = r.choice(rows, size=max(1, int(rows * heavy_frac)), replace=False)
+        k[idx] *= heavy_scale
+    return k.astype(np.float16), v.astype(np.float16)

@@ -1,0 +1,52 @@
+"""The C ABI library: built for gfx950, loads without a GPU, exports every function include/qwattn.h
+declares, and reports a missing GPU as a status code (no compute calls here)."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import common
+
+
+def test_library_exports_every_header_function():
+    qw = common.load_package()
+    lib = qw.load_library()
+    names = qw.header_functions()
+    assert len(names) >= 13
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_exports_match_header_exactly():
+    qw = common.load_package()
+    out = subprocess.run(["nm", "-D", "--defined-only", qw.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = sorted({l.split()[-1] for l in out.splitlines() if " T qwattn_" in l})
+    assert exported == qw.header_functions()
+
+
+def test_code_object_is_gfx950_only():
+    qw = common.load_package()
+    data = open(qw.LIB_PATH, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+    for other in (b"--gfx942", b"--gfx90a", b"--gfx1100"):
+        assert other not in data
+
+
+def test_no_gpu_is_a_status_code():
+    """qwattn_create on a machine without a usable gfx950 returns an error code and text."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    qw = common.load_package()
+    with pytest.raises(qw.QwattnError, match="device 0 not available"):
+        qw.Attention(16, 2, 256, 64)
+
+
+def test_bad_shapes_rejected_before_any_device_call():
+    """Shape checks come first: they fail identically with or without a GPU."""
+    qw = common.load_package()
+    for args, pat in [((16, 3, 256, 64), "head counts"), ((16, 2, 96, 64), "head_dim"),
+                      ((16, 2, 256, 63), "rope dimension"), ((64, 1, 256, 64), "GQA group")]:
+        with pytest.raises(qw.QwattnError, match=pat):
+            qw.Attention(*args)

@@ -1,0 +1,340 @@
+"""GPU parity of every kernel against the CPU oracle, through the C ABI (libqwattn.so).
+
+Inputs are seeded; the oracle reads the same fp16-rounded K/V the GPU reads (the reference CPU path
+keeps fp32 caches, src/qwen4_cpu.cpp:30-32, the GPU path fp16, src/qwen4_vk.cpp:565-574).
+"""
+import numpy as np
+import pytest
+import torch
+
+from common import QWEN3_NEXT, TINY, TINY_GGUF, Shape, assert_parity, cache_rows, projections
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    return t.detach().float().cpu().numpy()
+
+
+def make_ctx(qw, s, max_ctx=8192, max_tokens=2048, max_splits=1024):
+    return qw.Attention(s.NH, s.NKV, s.D, s.R, s.theta, s.eps, max_ctx=max_ctx, max_tokens=max_tokens,
+                        max_splits=max_splits)
+
+
+def gpu_caches(qw, k16, v16, cap):
+    """Caller-owned device caches of capacity cap holding rows [0, len(k16))."""
+    rows, nkv, d = k16.shape
+    kc = torch.zeros((cap, nkv, d), dtype=torch.float16, device=DEV)
+    kc[:rows] = dev(k16)
+    vrows = torch.zeros((cap, nkv, d), dtype=torch.float16, device=DEV)
+    vrows[:rows] = dev(v16)
+    return kc, qw.v_interleave(vrows)
+
+
+# ---- rope table --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("s", [TINY, QWEN3_NEXT], ids=repr)
+def test_rope_table(qw, oracle, s):
+    ctx = make_ctx(qw, s, max_ctx=262144)
+    tab = host(ctx.rope_table())
+    for lo, hi in [(0, 4096), (262144 - 4096, 262144)]:
+        ref = oracle.rope_table(hi, s.R, s.theta)[lo:hi]
+        err = np.abs(tab[lo:hi] - ref).max()
+        assert err <= 1e-6, (lo, hi, err)
+    own = torch.zeros((1000, s.R // 2, 2), device=DEV)
+    ctx.fill_rope(own, 1000)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(own), tab[:1000])
+
+
+# ---- fused QK-norm + rope + append --------------------------------------------------------------------
+
+CASES_NR = [(TINY, 1, 128), (TINY, 37, 5), (TINY_GGUF, 4, 300), (QWEN3_NEXT, 1, 16384), (QWEN3_NEXT, 4, 32768),
+            (QWEN3_NEXT, 64, 1000), (QWEN3_NEXT, 1, 262143)]
+
+
+@pytest.mark.parametrize("s,n,pos", CASES_NR, ids=lambda v: repr(v))
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_qk_norm_rope_append(qw, oracle, s, n, pos, dtype):
+    print(f"norm_rope {s} n={n} pos={pos} {dtype}", flush=True)
+    qg, k, v, qn, kn = projections(11 + n, n, s)
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    qg_d, k_d, v_d = dev(qg).to(tdt), dev(k).to(tdt), dev(v).to(tdt)
+    # the oracle sees exactly the values the GPU reads
+    qg_h, k_h, v_h = host(qg_d), host(k_d), host(v_d)
+    ctx = make_ctx(qw, s, max_ctx=262144)
+    cap = (pos + n + 7) // 8 * 8
+    kc = torch.zeros((cap, s.NKV, s.D), dtype=torch.float16, device=DEV)
+    vc = torch.zeros(cap * s.NKV * s.D, dtype=torch.float16, device=DEV)
+    q_out = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, q_out, pos, n)
+    q16 = torch.zeros((n, s.NH, s.D), dtype=torch.float16, device=DEV)
+    ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, q16, pos, n)
+    torch.cuda.synchronize()
+    rq, rk, rv = oracle.qk_norm_rope(qg_h, k_h, v_h, 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
+    assert np.abs(host(q_out) - rq).max() <= 2e-5 * max(1.0, np.abs(rq).max())
+    # fp16 K rows: within one fp16 rounding step of the oracle's fp32 row
+    gk = host(kc[pos:pos + n])
+    assert np.all(np.abs(gk - rk[pos:pos + n]) <= np.abs(rk[pos:pos + n]) * 2.0 ** -10 + 1e-6)
+    # V is copied: bit-exact fp16 of the input
+    gv = host(qw.v_rows(vc, cap, s.NKV, s.D)[pos:pos + n])
+    assert np.array_equal(gv, v_h.astype(np.float16).astype(np.float32))
+    # rows outside [pos, pos+n) untouched
+    assert float(kc[:pos].abs().max() if pos else 0) == 0.0
+    # fp16 prefill operand = fp16(q * log2(e)/sqrt(D))
+    ref16 = rq * (qw.LOG2E / np.sqrt(s.D))
+    assert np.all(np.abs(host(q16) - ref16) <= np.abs(ref16) * 2.0 ** -10 + 1e-6)
+
+
+# ---- split-KV decode / verify -------------------------------------------------------------------------
+
+def run_split(qw, ctx, q, kc, vc, cap, qg, pos, n, n_split=0):
+    out = torch.zeros((n, ctx.NH, ctx.D), device=DEV)
+    used = ctx.attend_partial(q, kc, vc, cap, pos, n, n_split)
+    ctx.combine(qg, out, n, used)
+    torch.cuda.synchronize()
+    return host(out), used
+
+
+CASES_DEC = [
+    (TINY, 128, 1, 0),
+    (TINY, 0, 1, 0),              # a single key: out = V0 * sigmoid(gate)
+    (TINY, 33, 4, 0),
+    (TINY_GGUF, 300, 1, 3),       # the reference's own tiny shape, 3 splits
+    (TINY_GGUF, 17, 4, 0),
+    (QWEN3_NEXT, 16384, 1, 64),   # BASELINE config 2 with the reference's 64 splits
+    (QWEN3_NEXT, 16384, 1, 0),
+    (QWEN3_NEXT, 31, 1, 0),
+    (QWEN3_NEXT, 32768, 4, 0),    # BASELINE config 3 (MTP verify)
+    (QWEN3_NEXT, 1000, 3, 7),
+    (QWEN3_NEXT, 32768, 1, 0),    # the headline metric's shape
+]
+
+
+@pytest.mark.parametrize("s,pos,n,n_split", CASES_DEC, ids=lambda v: repr(v))
+def test_split_decode_parity(qw, oracle, s, pos, n, n_split):
+    print(f"decode {s} pos={pos} n={n} split={n_split}", flush=True)
+    rows = pos + n
+    cap = (rows + 7) // 8 * 8
+    k16, v16 = cache_rows(100 + pos, rows, s)
+    r = np.random.default_rng(pos + 7)
+    q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
+    qg = r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    out, used = run_split(qw, ctx, dev(q), kc, vc, cap, dev(qg), pos, n, n_split)
+    ref = oracle.attention(q, k16.astype(np.float32), v16.astype(np.float32), pos, qg)
+    assert_parity(out, ref, f"{s} pos={pos} n={n} splits={used}")
+    if pos == 0:
+        sig = 1 / (1 + np.exp(-qg[0, :, s.D:].astype(np.float64)))
+        exp0 = v16[0].astype(np.float64)[np.arange(s.NH) // s.G] * sig
+        assert np.abs(out[0] - exp0).max() <= 1e-6
+
+
+def test_split_peaked_keys(qw, oracle):
+    """1% of the key rows scaled x8 (BASELINE config 5's softmax-range stress) at 16K."""
+    s = QWEN3_NEXT
+    pos, n = 16384, 1
+    rows = pos + n
+    k16, v16 = cache_rows(5, rows, s, heavy_frac=0.01)
+    r = np.random.default_rng(9)
+    q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
+    qg = r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32)
+    ctx = make_ctx(qw, s, max_ctx=rows + 7)
+    cap = (rows + 7) // 8 * 8
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    out, _ = run_split(qw, ctx, dev(q), kc, vc, cap, dev(qg), pos, n, 256)
+    ref = oracle.attention(q, k16.astype(np.float32), v16.astype(np.float32), pos, qg)
+    assert_parity(out, ref, "peaked")
+
+
+def test_split_invariance(qw):
+    """Any split count, including splits that end up empty for some rows, gives the same output."""
+    s = QWEN3_NEXT
+    pos, n = 5000, 4
+    rows = pos + n
+    cap = (rows + 7) // 8 * 8
+    k16, v16 = cache_rows(3, rows, s)
+    r = np.random.default_rng(4)
+    q = dev(r.standard_normal((n, s.NH, s.D)).astype(np.float32))
+    qg = dev(r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32))
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    outs = {sp: run_split(qw, ctx, q, kc, vc, cap, qg, pos, n, sp)[0] for sp in (1, 2, 7, 64, 0, 157, 1024)}
+    base = outs[1]
+    for sp, o in outs.items():
+        assert np.abs(o - base).max() <= 2e-6, sp
+
+
+def test_verify_equals_sequential_decodes(qw):
+    """A 4-token verify pass equals 4 single-token decodes at pos..pos+3 (src/main.cpp:457-460)."""
+    s = QWEN3_NEXT
+    pos, n = 3000, 4
+    rows = pos + n
+    cap = (rows + 7) // 8 * 8
+    k16, v16 = cache_rows(21, rows, s)
+    r = np.random.default_rng(22)
+    q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
+    qg = r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    together, _ = run_split(qw, ctx, dev(q), kc, vc, cap, dev(qg), pos, n)
+    for t in range(n):
+        one, _ = run_split(qw, ctx, dev(q[t:t + 1]), kc, vc, cap, dev(qg[t:t + 1]), pos + t, 1)
+        # the single-token pass carries P's fp16 remainder, the 4-token pass rounds P to fp16 once
+        assert np.abs(one[0] - together[t]).max() <= 2e-5, t
+
+
+# ---- prefill -------------------------------------------------------------------------------------------
+
+CASES_PF = [
+    (TINY, 0, 64),
+    (TINY, 100, 37),
+    (TINY_GGUF, 5, 50),
+    (QWEN3_NEXT, 0, 5),
+    (QWEN3_NEXT, 0, 300),
+    (QWEN3_NEXT, 777, 129),
+    (QWEN3_NEXT, 2048, 2048),
+]
+
+
+@pytest.mark.parametrize("s,pos,n", CASES_PF, ids=lambda v: repr(v))
+def test_prefill_parity(qw, oracle, s, pos, n):
+    """bf16 projections -> fused norm/rope/append (fp16 pre-scaled q) -> MFMA prefill, against the
+    oracle's norm/rope/append and attention on the same values."""
+    print(f"prefill {s} pos={pos} n={n}", flush=True)
+    rows = pos + n
+    cap = (rows + 7) // 8 * 8
+    k16, v16 = cache_rows(40 + pos, pos, s) if pos else (np.zeros((0, s.NKV, s.D), np.float16),) * 2
+    qg, k, v, qn, kn = projections(41 + n, n, s)
+    qg_d, k_d, v_d = dev(qg).to(torch.bfloat16), dev(k).to(torch.bfloat16), dev(v).to(torch.bfloat16)
+    ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=max(n, 1))
+    kc, vc = gpu_caches(qw, k16, v16, cap) if pos else (
+        torch.zeros((cap, s.NKV, s.D), dtype=torch.float16, device=DEV),
+        torch.zeros(cap * s.NKV * s.D, dtype=torch.float16, device=DEV))
+    q16 = torch.zeros((n, s.NH, s.D), dtype=torch.float16, device=DEV)
+    ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, q16, pos, n)
+    out = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.attend_prefill(q16, kc, vc, cap, qg_d, out, pos, n)
+    torch.cuda.synchronize()
+    out = host(out)
+    # oracle on the same inputs; K/V cache rows as the GPU holds them (fp16)
+    rq, _, _ = oracle.qk_norm_rope(host(qg_d), host(k_d), host(v_d), 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
+    kcache = host(kc[:rows])
+    vcache = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
+    qg_h = host(qg_d)
+    # all tokens when small, else a spread of tokens including the first and the last
+    toks = np.arange(n) if n <= 300 else np.unique(np.r_[0, 1, np.linspace(0, n - 1, 48).astype(int), n - 1])
+    for t in toks:
+        ref = oracle.attention(rq[t:t + 1], kcache, vcache, pos + t, qg_h[t:t + 1])
+        assert_parity(out[t:t + 1], ref, f"{s} pos={pos} n={n} token {t}")
+
+
+def test_prefill_equals_decodes(qw):
+    """A prefill chunk gives the same rows as decoding its tokens one at a time (block-causal vs
+    token-causal masks agree)."""
+    s = QWEN3_NEXT
+    pos, n = 200, 70
+    rows = pos + n
+    cap = (rows + 7) // 8 * 8
+    k16, v16 = cache_rows(51, rows, s)
+    r = np.random.default_rng(52)
+    q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
+    qg = dev(r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32))
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    out = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.attend_prefill(dev(q), kc, vc, cap, qg, out, pos, n)
+    torch.cuda.synchronize()
+    pf = host(out)
+    for t in range(0, n, 7):
+        one, _ = run_split(qw, ctx, dev(q[t:t + 1]), kc, vc, cap, qg[t:t + 1], pos + t, 1)
+        # prefill rounds q and p to fp16, decode keeps them at ~fp32: compare at the parity bar
+        assert_parity(pf[t:t + 1], one, f"token {t}")
+
+
+# ---- the whole layer body through context-owned caches -------------------------------------------------
+
+def test_layer_attention_prefill_then_decode(qw, oracle):
+    """qwattn_layer_attention over a prefill chunk then decode steps, with cache growth in between,
+    against the oracle's norm/rope/cache/attention sequence (fp32 inputs)."""
+    s = QWEN3_NEXT
+    ctx = make_ctx(qw, s, max_ctx=4096, max_tokens=512)
+    ctx.kv_alloc(2, 64)  # forces growth: 64 -> 512 -> ...
+    n0 = 300
+    ref_k = np.zeros((4096, s.NKV, s.D), np.float32)
+    ref_v = np.zeros((4096, s.NKV, s.D), np.float32)
+    pos = 0
+    for step, n in enumerate([n0, 1, 1, 4, 1]):
+        qg, k, v, qn, kn = projections(70 + step, n, s)
+        ctx.kv_grow(pos + n)
+        out = torch.zeros((n, s.NH, s.D), device=DEV)
+        ctx.layer_attention(1, dev(qg), dev(k), dev(v), dev(qn), dev(kn), out, pos, n)
+        torch.cuda.synchronize()
+        rq, rk, rv = oracle.qk_norm_rope(qg, k, v, 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
+        ref_k[pos:pos + n] = rk[pos:pos + n].astype(np.float16)
+        ref_v[pos:pos + n] = rv[pos:pos + n].astype(np.float16)
+        ref = oracle.attention(rq, ref_k[:pos + n], ref_v[:pos + n], pos, qg)
+        assert_parity(host(out), ref, f"step {step} pos={pos} n={n}")
+        pos += n
+    kc, vc, cap = ctx.kv_slot(1)
+    assert cap >= pos
+    assert np.array_equal(host(qw.v_rows(vc, cap, s.NKV, s.D)[:pos]), ref_v[:pos])
+
+
+def test_rollback_is_position_reset(qw, oracle):
+    """accept(2) after a 4-token verify: the next step equals a run that never saw drafts 3-4 (the
+    reference rolls attention back by resetting pos_, src/qwen4_vk.cpp:286-300)."""
+    s = QWEN3_NEXT
+    ctx = make_ctx(qw, s, max_ctx=2048, max_tokens=512)
+    ctx.kv_alloc(1, 2048)
+    base = 500
+    qg0, k0, v0, qn, kn = projections(90, base, s)
+    out = torch.zeros((base, s.NH, s.D), device=DEV)
+    ctx.layer_attention(0, dev(qg0), dev(k0), dev(v0), dev(qn), dev(kn), out, 0, base)
+    # verify pass of 1 + 3 drafts, keep 2
+    qg1, k1, v1, _, _ = projections(91, 4, s)
+    out4 = torch.zeros((4, s.NH, s.D), device=DEV)
+    ctx.layer_attention(0, dev(qg1), dev(k1), dev(v1), dev(qn), dev(kn), out4, base, 4)
+    pos = base + 2
+    qg2, k2, v2, _, _ = projections(92, 1, s)
+    out1 = torch.zeros((1, s.NH, s.D), device=DEV)
+    ctx.layer_attention(0, dev(qg2), dev(k2), dev(v2), dev(qn), dev(kn), out1, pos, 1)
+    torch.cuda.synchronize()
+    # a context that only ever saw the 2 kept tokens
+    ctx2 = make_ctx(qw, s, max_ctx=2048, max_tokens=512)
+    ctx2.kv_alloc(1, 2048)
+    o = torch.zeros((base, s.NH, s.D), device=DEV)
+    ctx2.layer_attention(0, dev(qg0), dev(k0), dev(v0), dev(qn), dev(kn), o, 0, base)
+    o2 = torch.zeros((2, s.NH, s.D), device=DEV)
+    ctx2.layer_attention(0, dev(qg1[:2]), dev(k1[:2]), dev(v1[:2]), dev(qn), dev(kn), o2, base, 2)
+    o1 = torch.zeros((1, s.NH, s.D), device=DEV)
+    ctx2.layer_attention(0, dev(qg2), dev(k2), dev(v2), dev(qn), dev(kn), o1, pos, 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out1), host(o1))
+    assert np.abs(host(out4)[:2] - host(o2)).max() <= 2e-5
+
+
+def test_errors_are_status_codes(qw):
+    s = QWEN3_NEXT
+    ctx = make_ctx(qw, s, max_ctx=1024, max_tokens=64)
+    kc = torch.zeros((1024, s.NKV, s.D), dtype=torch.float16, device=DEV)
+    vc = torch.zeros(1024 * s.NKV * s.D, dtype=torch.float16, device=DEV)
+    q = torch.zeros((8, s.NH, s.D), device=DEV)
+    with pytest.raises(qw.QwattnError, match="context overflow") as e:
+        ctx.attend_partial(q, kc, vc, 1024, 1024, 1)
+    assert e.value.code == qw.ERANGE
+    with pytest.raises(qw.QwattnError, match="> 32 rows"):
+        ctx.attend_partial(q, kc, vc, 1024, 10, 8)
+    with pytest.raises(qw.QwattnError, match="slot"):
+        ctx.layer_attention(0, q, q, q, q, q, q, 0, 1)
+    with pytest.raises(qw.QwattnError, match="not a multiple of 8"):
+        ctx.attend_partial(q, kc, vc, 1020, 0, 1)
+    with pytest.raises(qw.QwattnError):
+        qw.Attention(16, 3, 256, 64)
