@@ -12,8 +12,24 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "liboracle.so")
-REF_LIB = os.path.join(HERE, "_ref", "libref.so")
+
+
+def _host_has_avx512():
+    """The v4 builds need AVX-512 F/BW/DQ/VL/CD; otherwise the AVX2 (x86-64-v3) builds are loaded."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512dq", "avx512vl", "avx512cd"} <= flags
+    except OSError:
+        pass
+    return False
+
+
+_SUFFIX = "" if _host_has_avx512() else "_v3"
+LIB = os.path.join(HERE, f"liboracle{_SUFFIX}.so")
+REF_LIB = os.path.join(HERE, "_ref", f"libref{_SUFFIX}.so")
 REF_SRC = "/root/reference/src/cpu_kernels.cpp"
 
 _F = ctypes.POINTER(ctypes.c_float)

@@ -154,10 +154,15 @@ def test_split_peaked_keys(qw, oracle):
     assert_parity(out, ref, "peaked")
 
 
-def test_split_invariance(qw):
-    """Any split count, including splits that end up empty for some rows, gives the same output."""
+@pytest.mark.parametrize("n", [1, 4])
+def test_split_invariance(qw, n):
+    """Any split count, including splits that end up empty for some rows, gives the same output.
+
+    Tolerance: the single-token pass keeps the query and P at ~fp32 accuracy (fp16 hi + lo parts), so
+    splits agree to fp32 rounding; the 4-token pass rounds P to fp16 once (relative 2^-11 per weight),
+    so splits that see different running maxima agree to about 1e-3 of the output's scale."""
     s = QWEN3_NEXT
-    pos, n = 5000, 4
+    pos = 5000
     rows = pos + n
     cap = (rows + 7) // 8 * 8
     k16, v16 = cache_rows(3, rows, s)
@@ -168,8 +173,9 @@ def test_split_invariance(qw):
     kc, vc = gpu_caches(qw, k16, v16, cap)
     outs = {sp: run_split(qw, ctx, q, kc, vc, cap, qg, pos, n, sp)[0] for sp in (1, 2, 7, 64, 0, 157, 1024)}
     base = outs[1]
+    tol = 2e-6 if n == 1 else 1e-3 * np.abs(base).max()
     for sp, o in outs.items():
-        assert np.abs(o - base).max() <= 2e-6, sp
+        assert np.abs(o - base).max() <= tol, sp
 
 
 def test_verify_equals_sequential_decodes(qw):
