@@ -62,69 +62,91 @@ class Workload:
 
     def __init__(self, qw, name, pos, n, slots, n_split=0, in_dtype="f32", heavy_frac=0.0, seed=0):
         import torch
-        self.torch = torch
         self.name, self.pos, self.n, self.slots, self.n_split = name, pos, n, slots, n_split
         rows = pos + n
-        self.cap = (rows + 7) // 8 * 8
+        self.cap = (rows + 31) // 32 * 32
         self.att = qw.Attention(NH, NKV, D, R, THETA, EPS, max_ctx=self.cap, max_tokens=max(n, 1),
                                 max_splits=1024)
         self.att.kv_alloc(slots, self.cap)
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
+        self.slot_views = []
         for s in range(slots):
-            kc, vc, _ = self.att.kv_slot(s)
+            kc, vc, cap = self.att.kv_slot(s)
             kc.normal_(generator=g)
             vc.normal_(generator=g)
             if heavy_frac > 0:  # post-norm cache rows scaled x8 (softmax-range stress)
+                krows = qw.k_rows(kc, cap, NKV, D)
                 idx = torch.randperm(rows, device="cuda", generator=g)[:max(1, int(rows * heavy_frac))]
-                kc[idx] *= 8.0
+                krows[idx] *= 8.0
+                kc.copy_(qw.k_block(krows))
+                del krows
+            self.slot_views.append((kc, vc, cap))
         dt = torch.float32 if in_dtype == "f32" else torch.bfloat16
         self.qg = torch.randn((n, NH, 2 * D), device="cuda", generator=g).to(dt)
         self.k = torch.randn((n, NKV, D), device="cuda", generator=g).to(dt)
         self.v = torch.randn((n, NKV, D), device="cuda", generator=g).to(dt)
         self.qn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.kn = 0.1 * torch.randn(D, device="cuda", generator=g)
-        self.split = n * (NH // NKV) <= 32
-        self.q = torch.zeros((n, NH, D), device="cuda", dtype=torch.float32 if self.split else torch.float16)
+        self.split = n * (NH // NKV) <= 32 and n <= 8
+        self.q = None if self.split else torch.zeros((n, NH, D), device="cuda", dtype=torch.float16)
         self.out = torch.zeros((n, NH, D), device="cuda")
         self.rope = self.att.rope_table()
         self.used = None
 
-    def step(self, slot, ev=None):
-        """One attention body on layer cache `slot`; records ev[0..3] around the kernels when given."""
+    def step(self, slot):
+        """One attention layer body on layer cache `slot` through the layer entry point."""
+        self.att.layer_attention(slot, self.qg, self.k, self.v, self.qn, self.kn, self.out, self.pos, self.n,
+                                 self.n_split)
+
+    def step_events(self, slot, ev):
+        """The same kernels through the per-dispatch entry points, with HIP events around each kernel."""
         a = self.att
-        kc, vc, cap = a.kv_slot(slot)
-        if ev:
-            ev[0].record()
-        a.qk_norm_rope_append(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.q, self.pos,
-                              self.n)
-        if ev:
-            ev[1].record()
+        kc, vc, cap = self.slot_views[slot]
+        ev[0].record()
         if self.split:
-            self.used = a.attend_partial(self.q, kc, vc, cap, self.pos, self.n, self.n_split)
-            if ev:
-                ev[2].record()
+            self.used = a.decode_partial(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.pos,
+                                         self.n, self.n_split)
+            ev[1].record()
             a.combine(self.qg, self.out, self.n, self.used)
         else:
+            a.qk_norm_rope_append(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.q,
+                                  self.pos, self.n)
+            ev[1].record()
             a.attend_prefill(self.q, kc, vc, cap, self.qg, self.out, self.pos, self.n)
-            if ev:
-                ev[2].record()
-        if ev:
-            ev[3].record()
+        ev[2].record()
 
     def close(self):
+        self.slot_views = []
         self.att.close()
 
 
+_SLEEP_PER_MS = None
+
+
+def gpu_sleep(ms):
+    """Keeps the stream busy for about `ms` milliseconds, so that the launches queued behind it start
+    back to back and their HIP events time the kernels, not the host's launch latency."""
+    import torch
+    global _SLEEP_PER_MS
+    if _SLEEP_PER_MS is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        e0.record()
+        torch.cuda._sleep(1_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_PER_MS = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(ms * _SLEEP_PER_MS))
+
+
 def run_workload(wl, steps, warmup, graph):
-    """Times `steps` steps (rotating over the slots) by wall clock, then the same steps with HIP events
-    around every kernel. Returns a dict of timings in microseconds."""
+    """Times `steps` layer steps (rotating over the slots) by wall clock, then the same kernels with
+    HIP events around each one. Returns timings in microseconds."""
     import torch
     for i in range(max(warmup, wl.slots)):
         wl.step(i % wl.slots)
     torch.cuda.synchronize()
-    ref_out = None
-    g = None
     if graph:
         # one graph holds one step per slot; replaying it runs `slots` steps
         wl.step(0)
@@ -143,8 +165,7 @@ def run_workload(wl, steps, warmup, graph):
         for _ in range(2):
             g.replay()
         torch.cuda.synchronize()
-        # the last step of the graph runs slot slots-1; re-run slot 0 eagerly and compare with the output
-        # recorded before capture so a replay that computes something else is caught
+        # a replay that computed something else than the eager step would show here
         wl.step(0)
         torch.cuda.synchronize()
         if not torch.equal(wl.out, ref_out):
@@ -156,6 +177,7 @@ def run_workload(wl, steps, warmup, graph):
             g.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        del g
     else:
         timed_steps = steps
         torch.cuda.synchronize()
@@ -165,28 +187,28 @@ def run_workload(wl, steps, warmup, graph):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
 
-    # per-kernel durations: HIP events on the stream the library launches on (torch's current stream)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    for i in range(steps):
-        wl.step(i % wl.slots, evs[i])
+    # per-kernel durations: HIP events on the stream the library launches on (torch's current stream),
+    # queued behind a GPU sleep in batches of 16 steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for b0 in range(0, steps, 16):
+        gpu_sleep(2.0)
+        for i in range(b0, min(steps, b0 + 16)):
+            wl.step_events(i % wl.slots, evs[i])
     torch.cuda.synchronize()
-    k_norm = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
-    k_attn = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
-    k_comb = [e[2].elapsed_time(e[3]) * 1e3 for e in evs]
-    k_all = [e[0].elapsed_time(e[3]) * 1e3 for e in evs]
-    ok = bool(torch.isfinite(wl.out).all())
-    if not ok:
+    k_first = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
+    k_second = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
+    k_all = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
+    if not bool(torch.isfinite(wl.out).all()):
         raise RuntimeError(f"{wl.name}: non-finite attention output")
-    return {
-        "timed_steps": timed_steps,
-        "us_per_step": wall / timed_steps * 1e6,
-        "us_norm_rope": statistics.mean(k_norm),
-        "us_attend": statistics.mean(k_attn),
-        "us_attend_median": statistics.median(k_attn),
-        "us_combine": statistics.mean(k_comb),
-        "us_kernels": statistics.mean(k_all),
-        "splits": wl.used,
-    }
+    r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all)}
+    if wl.split:
+        r.update({"kernel": "k_decode (fused norm+rope+append+split attend)", "us_main": statistics.mean(k_first),
+                  "us_main_median": statistics.median(k_first), "us_combine": statistics.mean(k_second),
+                  "splits": wl.used})
+    else:
+        r.update({"kernel": "k_prefill", "us_norm_rope": statistics.mean(k_first), "us_main": statistics.mean(k_second),
+                  "us_main_median": statistics.median(k_second)})
+    return r
 
 
 def cpu_info():
@@ -269,11 +291,13 @@ def main():
     only = set(filter(None, args.only.split(",")))
 
     configs = [
-        # name, pos, n, slots, n_split, in_dtype, heavy_frac
+        # name, pos, n, slots, n_split (0 = one workgroup per CU), in_dtype, heavy_frac
         ("decode_32k", 32768, 1, args.slots, 0, "f32", 0.0),
+        ("decode_16k", 16384, 1, args.slots, 0, "f32", 0.0),
         ("decode_16k_64splits", 16384, 1, args.slots, 64, "f32", 0.0),
         ("verify_32k_n4", 32768, 4, args.slots, 0, "f32", 0.0),
-        ("decode_256k", 262144, 1, 2, 1024, "f32", 0.01),
+        ("decode_256k_1024splits", 262144, 1, 2, 1024, "f32", 0.01),
+        ("decode_256k", 262144, 1, 2, 0, "f32", 0.01),
         ("prefill_2k_on_2k", 2048, 2048, 8, 0, "bf16", 0.0),
     ]
     results = {}
@@ -291,13 +315,15 @@ def main():
             byts = kv_bytes(pos + n)
             r["value"] = byts / (r["us_per_step"] * 1e-6) / 1e9
             r["unit"] = "GB/s"
-            r["attend_frac_hbm"] = byts / (r["us_attend"] * 1e-6) / HBM_PEAK
+            r["frac_hbm_step"] = byts / (r["us_per_step"] * 1e-6) / HBM_PEAK
+            r["frac_hbm_kernel"] = byts / (r["us_main"] * 1e-6) / HBM_PEAK
             r["algorithmic_bytes"] = byts
         else:
             fl = causal_flops(pos, n)
             r["value"] = fl / (r["us_per_step"] * 1e-6) / 1e12
             r["unit"] = "TFLOP/s"
-            r["attend_frac_mfma"] = fl / (r["us_attend"] * 1e-6) / MFMA_F16_PEAK
+            r["frac_mfma_step"] = fl / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
+            r["frac_mfma_kernel"] = fl / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
             r["algorithmic_flops"] = fl
         results[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)
@@ -329,18 +355,18 @@ def main():
         "workloads": results,
     }
     if head:
-        line["roofline"] = {"bound": "hbm", "kernel": "k_attend_split<256,8>",
-                            "achieved": round(head["algorithmic_bytes"] / (head["us_attend"] * 1e-6) / 1e9, 2),
+        line["roofline"] = {"bound": "hbm", "kernel": "k_decode<256,0,1,0> (fused decode, grid 128x2)",
+                            "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                            "frac": round(head["attend_frac_hbm"], 4), "traffic": None,
-                            "kernel_us": head["us_attend"]}
+                            "frac": round(head["frac_hbm_kernel"], 4), "traffic": None,
+                            "kernel_us": head["us_main"]}
     pf = results.get("prefill_2k_on_2k")
     if pf:
-        line["prefill_roofline"] = {"bound": "mfma", "kernel": "k_prefill<256>",
-                                    "achieved": round(pf["algorithmic_flops"] / (pf["us_attend"] * 1e-6) / 1e12, 2),
+        line["prefill_roofline"] = {"bound": "mfma", "kernel": "k_prefill<256,f16,bf16>",
+                                    "achieved": round(pf["algorithmic_flops"] / (pf["us_main"] * 1e-6) / 1e12, 2),
                                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                                    "frac": round(pf["attend_frac_mfma"], 4), "traffic": None,
-                                    "kernel_us": pf["us_attend"]}
+                                    "frac": round(pf["frac_mfma_kernel"], 4), "traffic": None,
+                                    "kernel_us": pf["us_main"]}
     print(json.dumps(line), flush=True)
 
 

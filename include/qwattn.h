@@ -28,13 +28,15 @@
  *                        as the reference uploads them (src/qwen4_vk.cpp:444-448, qk_norm_rope.comp:33).
  *  - rope [n_pos][R/2][2] fp32 (cos, sin) of the fp32 angle (float)p * inv_freq[i],
  *                        inv_freq[i] = (float)(1 / theta^(2i/R)) (src/qwen4_vk.cpp:494-504).
- *  - K cache [cap][NKV][D] fp16 — the reference's kv16 layout (src/qwen4_vk.cpp:565-574).
- *  - V cache [cap/8][NKV][D][8] fp16 — position-interleaved in groups of 8: element (p, h, d) sits
- *                        at ((p/8)*NKV + h)*D*8 + d*8 + p%8. This is the one layout that differs
- *                        from the reference: it makes each 16-byte load hold 8 consecutive keys of
- *                        one dim, which is the operand shape of the gfx950 MFMA for P*V. `cap` is a
- *                        multiple of 8. Prefix copies by whole 8-row groups stay valid, so the
- *                        reference's grow-by-copy (ensure_kv) carries over unchanged.
+ *  - K and V caches [cap/32][NKV][32*D] fp16, cap a multiple of 32: blocks of 32 positions, one
+ *                        32*D part per KV head. The reference keeps [cap][NKV][D] rows
+ *                        (src/qwen4_vk.cpp:565-574); here the elements inside a part are ordered so
+ *                        that every matrix-core operand fragment is one contiguous kilobyte:
+ *                          K (key kb = p % 32, dim d): (((d/32)*2 + (kb/4)%2)*4 + (d/8)%4)*16
+ *                                                      + (kb/8)*4 + kb%4) * 8 + d%8
+ *                          V (key kb, dim d):          (((d/16)*4 + kb/8)*16 + d%16) * 8 + kb%8
+ *                        Blocks stay in position order, so the reference's grow-by-copy (ensure_kv)
+ *                        carries over: the old caches are a byte prefix of the grown ones.
  *  - q    [n][NH][D] fp32 normalized + rotated query (the reference's q_out).
  *  - out  [n][NH][D] fp32 gated attention output (the reference's att_, input of o_proj).
  */
@@ -94,7 +96,7 @@ int qwattn_fill_rope(qwattn_ctx* ctx, void* stream, float* rope, int n_pos);
 /* ---- KV cache owned by the context (reference: alloc_state / ensure_kv, src/qwen4_vk.cpp:565-574,
  * 657-685) ---- */
 /* Allocates n_slots (one per full-attention layer) K and V caches of `cap` tokens (rounded up to a
- * multiple of 8, at most max_ctx), zero-filled. Any previous caches are freed. */
+ * multiple of 32, at most max_ctx rounded up), zero-filled. Any previous caches are freed. */
 int qwattn_kv_alloc(qwattn_ctx* ctx, int n_slots, int cap);
 /* Grows every slot to hold `tokens` positions: new capacity max(2*cap, tokens), at most max_ctx,
  * copying each slot's rows; no-op when tokens <= cap. Synchronizes `stream`. Same contract as
@@ -119,16 +121,29 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* ctx, void* stream, const void* qg, co
 
 /* Split-KV causal GQA attention partials (reference: shaders/attention.comp, pipeline
  * attention_kv16, dispatched at src/qwen4_vk.cpp:985-988 with PcAttn). Token t attends to keys
- * [0, pos+t+1); the keys [0, pos+n) are cut into `n_split` chunks (0 = automatic), and each
- * workgroup serves all NH/NKV query heads of one KV head for one chunk, so every K/V row is read
- * from HBM once. Requires n * NH/NKV <= 32 (decode n=1, MTP verify n<=4 at NH/NKV=8). Partials
- * (running max in log2 units, sum, unnormalized o[D]) go to the context's scratch; returns the
- * split count actually used in *used_splits (may be NULL). */
+ * [0, pos+t+1); the keys [0, pos+n) are cut into `n_split` chunks (0 = automatic: one workgroup per
+ * CU), and each workgroup serves all NH/NKV query heads of all n tokens of one KV head for one chunk,
+ * so every K/V row is read from HBM once. `q` is the normalized, rotated query [n][NH][D] fp32 (the
+ * reference's q_out) and rows [pos, pos+n) must already be in the caches. Requires n * NH/NKV <= 32
+ * (decode n=1, MTP verify n<=4 at NH/NKV=8). Partials (running max in log2 units, sum, unnormalized
+ * o[D]) go to the context's scratch; returns the split count actually used in *used_splits (may be
+ * NULL). */
 int qwattn_attend_partial(qwattn_ctx* ctx, void* stream, const float* q, const void* kcache,
                           const void* vcache, int kv_cap, int pos, int n, int n_split,
                           int* used_splits);
 
-/* Log-sum-exp merge of the partials of the last qwattn_attend_partial plus the sigmoid output gate
+/* The reference's qk_norm_rope + attention dispatches of one decode / verify pass in one launch
+ * (src/qwen4_vk.cpp:968-988): from the projection outputs qg, k, v of the n new tokens it applies the
+ * QK-RMSNorm (1 + w) and partial RoPE, appends the new K/V rows at positions pos.. pos+n-1 of the
+ * caches, and writes the split-KV partials exactly as qwattn_attend_partial would for the normalized
+ * query. Requires n <= 8 and n * NH/NKV <= 32. Follow with qwattn_combine. */
+int qwattn_decode_partial(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
+                          int in_dtype, const float* qn, const float* kn, const float* rope,
+                          void* kcache, void* vcache, int kv_cap, int pos, int n, int n_split,
+                          int* used_splits);
+
+/* Log-sum-exp merge of the partials of the last qwattn_attend_partial / qwattn_decode_partial plus the
+ * sigmoid output gate
  * (reference: shaders/attn_combine.comp, dispatched at src/qwen4_vk.cpp:990-992 with
  * PcAttnCombine): out[t][h][d] = (sum_z o_z e^{m_z-M}) / (sum_z l_z e^{m_z-M}) * sigmoid(gate),
  * gate = qg[t][h][D + d]; splits with l = 0 are skipped. */
@@ -146,9 +161,10 @@ int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dt
 
 /* The whole attention body between the projections, for one full-attention layer `slot` of the
  * context's caches (reference: the dispatches of Qwen4Vulkan::attention, src/qwen4_vk.cpp:968-992;
- * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): norm + rope + append,
- * then split-KV attend + combine for n * NH/NKV <= 32, else the MFMA prefill kernel. `n_split` as in
- * qwattn_attend_partial. The normalized query goes to a context-owned buffer. */
+ * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): for n <= 8 and
+ * n * NH/NKV <= 32 the fused qwattn_decode_partial then qwattn_combine (two launches); otherwise norm +
+ * rope + append, then the MFMA prefill kernel (or split attend + combine for small groups). `n_split`
+ * as in qwattn_attend_partial. */
 int qwattn_layer_attention(qwattn_ctx* ctx, void* stream, int slot, const void* qg, const void* k,
                            const void* v, int in_dtype, const float* qn, const float* kn, float* out,
                            int pos, int n, int n_split);

@@ -60,6 +60,7 @@ def load_library():
         "qwattn_kv_slot": [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_I)],
         "qwattn_qk_norm_rope_append": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I],
         "qwattn_attend_partial": [_P, _P, _P, _P, _P, _I, _I, _I, _I, ctypes.POINTER(_I)],
+        "qwattn_decode_partial": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, ctypes.POINTER(_I)],
         "qwattn_combine": [_P, _P, _P, _I, _P, _I, _I],
         "qwattn_attend_prefill": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
@@ -93,15 +94,36 @@ def _stream(stream):
 _DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
 
-def v_rows(vcache, cap, n_kv, d):
-    """[cap/8][NKV][D][8] interleaved V cache -> [cap][NKV][D] rows (a copy)."""
-    return vcache.view(cap // 8, n_kv, d, 8).permute(0, 3, 1, 2).reshape(cap, n_kv, d)
+BLK = 32  # positions per cache block
 
 
-def v_interleave(rows):
-    """[cap][NKV][D] rows -> the [cap/8][NKV][D][8] interleaved V cache layout (cap % 8 == 0)."""
-    cap, n_kv, d = rows.shape
-    return rows.view(cap // 8, 8, n_kv, d).permute(0, 2, 3, 1).contiguous().view(-1)
+def k_block(rows):
+    """[cap][NKV][D] K rows -> the blocked K cache layout of include/qwattn.h, flat (cap % 32 == 0):
+    block b, head h, key kb, dim d at ((b*NKV + h)*32*D) + ((((d/32)*2 + (kb/4)%2)*4 + (d/8)%4)*16
+    + (kb/8)*4 + kb%4)*8 + d%8."""
+    cap, nkv, d = rows.shape
+    x = rows.reshape(cap // BLK, 4, 2, 4, nkv, d // 32, 4, 8)  # [b][kb/8][kb/4%2][kb%4][h][d/32][d/8%4][d%8]
+    return x.permute(0, 4, 5, 2, 6, 1, 3, 7).contiguous().view(-1)
+
+
+def k_rows(kcache, cap, nkv, d):
+    """Inverse of k_block: the flat blocked K cache -> [cap][NKV][D] rows (a copy)."""
+    x = kcache.view(cap // BLK, nkv, d // 32, 2, 4, 4, 4, 8)   # [b][h][d/32][s][g][kb/8][kb%4][e]
+    return x.permute(0, 5, 3, 6, 1, 2, 4, 7).reshape(cap, nkv, d)
+
+
+def v_block(rows):
+    """[cap][NKV][D] V rows -> the blocked V cache layout, flat: block b, head h, key kb, dim d at
+    ((b*NKV + h)*32*D) + (((d/16)*4 + kb/8)*16 + d%16)*8 + kb%8."""
+    cap, nkv, d = rows.shape
+    x = rows.reshape(cap // BLK, 4, 8, nkv, d // 16, 16)        # [b][kb/8][kb%8][h][d/16][d%16]
+    return x.permute(0, 3, 4, 1, 5, 2).contiguous().view(-1)
+
+
+def v_rows(vcache, cap, nkv, d):
+    """Inverse of v_block."""
+    x = vcache.view(cap // BLK, nkv, d // 16, 4, 16, 8)         # [b][h][d/16][kb/8][d%16][kb%8]
+    return x.permute(0, 3, 5, 1, 2, 4).reshape(cap, nkv, d)
 
 
 class Attention:
@@ -153,11 +175,11 @@ class Attention:
         self._check(self.lib.qwattn_kv_grow(self.h, _stream(stream), tokens))
 
     def kv_slot(self, slot):
-        """(K cache [cap, NKV, D] fp16 view, V cache flat fp16 view in the interleaved layout, cap)."""
+        """(K cache, V cache, cap): flat fp16 views of one slot's blocked caches (see k_rows / v_rows)."""
         k, v, cap = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int()
         self._check(self.lib.qwattn_kv_slot(self.h, slot, ctypes.byref(k), ctypes.byref(v), ctypes.byref(cap)))
         n = cap.value * self.NKV * self.D
-        kc = _wrap_device_halfs(k.value, n, self.device).view(cap.value, self.NKV, self.D)
+        kc = _wrap_device_halfs(k.value, n, self.device)
         vc = _wrap_device_halfs(v.value, n, self.device)
         return kc, vc, cap.value
 
@@ -171,6 +193,14 @@ class Attention:
         used = ctypes.c_int()
         self._check(self.lib.qwattn_attend_partial(self.h, _stream(stream), _ptr(q), _ptr(kcache), _ptr(vcache),
                                                    kv_cap, pos, n, n_split, ctypes.byref(used)))
+        return used.value
+
+    def decode_partial(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, pos, n, n_split=0, stream=None):
+        """Fused norm + rope + append + split-KV partials (n <= 8, n * NH/NKV <= 32); returns splits."""
+        used = ctypes.c_int()
+        self._check(self.lib.qwattn_decode_partial(
+            self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
+            _ptr(kcache), _ptr(vcache), kv_cap, pos, n, n_split, ctypes.byref(used)))
         return used.value
 
     def combine(self, qg, out, n, n_split, stream=None):

@@ -25,6 +25,42 @@ __device__ __forceinline__ float load_in(const void* p, size_t i) {
     }
 }
 
+// N consecutive elements of a projection-output row as fp32 with vector loads: fp32 in 16-byte pieces
+// when N % 4 == 0, bf16 in 16-byte pieces when N % 8 == 0 (the caller guarantees the alignment).
+template <int DT, int N>
+__device__ __forceinline__ void load_vec(const void* p, size_t off, float (&x)[N]) {
+    if constexpr (DT == 0) {
+        const float* f = static_cast<const float*>(p) + off;
+        if constexpr (N % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < N; i += 4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(f + i);
+                x[i] = v[0], x[i + 1] = v[1], x[i + 2] = v[2], x[i + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; i++) x[i] = f[i];
+        }
+    } else {
+        const uint16_t* b = static_cast<const uint16_t*>(p) + off;
+        if constexpr (N % 8 == 0) {
+#pragma unroll
+            for (int i = 0; i < N; i += 8) {
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 v = *reinterpret_cast<const u32x4*>(b + i);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    x[i + 2 * k] = __uint_as_float(v[k] << 16);
+                    x[i + 2 * k + 1] = __uint_as_float(v[k] & 0xffff0000u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; i++) x[i] = __uint_as_float((uint32_t)b[i] << 16);
+        }
+    }
+}
+
 // 16x16x32 fp16 MFMA, fp32 accumulate. Lane l: A row / B column l%16, k = 8*(l/16) + slot;
 // C rows 4*(l/16) + i, column l%16.
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
@@ -51,5 +87,69 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// ---- K/V cache layout ------------------------------------------------------------------------------
+// Both caches are [cap/32][NKV][32*D] fp16: blocks of 32 positions, one 32*D part per KV head. Inside a
+// part the elements are ordered so that every MFMA operand fragment of the decode and prefill kernels
+// is one contiguous kilobyte (64 lanes x 16 bytes):
+//  K: (key kb, dim d) -> (((d/32)*2 + s)*4 + (d/8)%4)*16 + c)*8 + d%8 with c = (kb/8)*4 + kb%4,
+//     s = (kb/4)%2. Fragment (kk, s) of v_mfma_f32_16x16x32_f16's A operand — lane (c, g) holding key
+//     8*(c/4) + 4*s + c%4, dims 32*kk + 8*g .. +7 — is the kilobyte at (kk*2 + s) KB, and the score
+//     tile it produces leaves keys 8*g .. 8*g+7 of every column in lane group g.
+//  V: (key kb, dim d) -> (((d/16)*4 + kb/8)*16 + d%16)*8 + kb%8. Fragment dt of the P.V product's A
+//     operand (V^T: lane (c, g) holding dim 16*dt + c for keys 8*g .. 8*g+7) is the kilobyte at dt KB.
+constexpr int kBlk = 32;  // positions per cache block
+
+__device__ __forceinline__ int k_off(int kb, int d) {
+    const int c = ((kb >> 3) << 2) | (kb & 3), s = (kb >> 2) & 1;
+    return (((((d >> 5) << 1) | s) * 4 + ((d >> 3) & 3)) * 16 + c) * 8 + (d & 7);
+}
+
+__device__ __forceinline__ int v_off(int kb, int d) {
+    return (((d >> 4) * 4 + (kb >> 3)) * 16 + (d & 15)) * 8 + (kb & 7);
+}
+
+// Element offset of (position p, KV head h) part start.
+__device__ __forceinline__ size_t kv_part(int p, int h, int NKV, int D) {
+    return ((size_t)(p >> 5) * NKV + h) * (size_t)(kBlk * D);
+}
+
+// RMSNorm with the (1 + w) multiplier and partial rotate-half RoPE of one head row, one 64-lane wave
+// per row (the reference's qk_norm_rope.comp:26-42 / src/qwen4_cpu.cpp:19-23, 281-289):
+//   y = x * rsqrt(mean(x^2) + eps) * (1 + w);  for d < R/2:  y'[d] = y[d] cos_d - y[d + R/2] sin_d,
+//   for R/2 <= d < R:  y'[d] = y[d] cos_{d-R/2} + y[d - R/2] sin_{d-R/2}
+// Lane l holds dims l*DPL .. l*DPL + DPL - 1 (DPL = D/64); the RoPE partner sits (R/2)/DPL lanes away
+// (the host requires (R/2) % DPL == 0). `rope_row` is the table row (cos, sin)[R/2] of the position.
+template <int D, int IN_DT>
+__device__ __forceinline__ void norm_rope_row(const void* src, size_t off, const float* w,
+                                              const float* rope_row, int R, float eps, int lane,
+                                              float (&y)[D / 64]) {
+    constexpr int DPL = D / 64;
+    const int d0 = lane * DPL;
+    float x[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; j++) x[j] = load_in<IN_DT>(src, off + d0 + j);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; j++) ss += x[j] * x[j];
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < DPL; j++) y[j] = x[j] * r * (1.0f + w[d0 + j]);
+    const int half = R >> 1;
+    const int offl = half / DPL;
+    const bool lo_half = d0 < half;
+    const int src_lane = d0 < R ? (lo_half ? lane + offl : lane - offl) & 63 : lane;
+#pragma unroll
+    for (int j = 0; j < DPL; j++) {
+        const float partner = __shfl(y[j], src_lane, 64);
+        const int d = d0 + j;
+        if (d < R) {
+            const int i = lo_half ? d : d - half;
+            const float c = rope_row[2 * i], s = rope_row[2 * i + 1];
+            y[j] = lo_half ? y[j] * c - partner * s : y[j] * c + partner * s;
+        }
+    }
+}
 
 }  // namespace qw

@@ -1,0 +1,538 @@
+// Split-KV causal GQA attention for decode and MTP verify, plus the log-sum-exp combine, for gfx950.
+//
+// Replaces shaders/attention.comp (attention_kv16) and shaders/attn_combine.comp, and — in the fused
+// form used by the layer entry point — also shaders/qk_norm_rope.comp for the new tokens. Semantics per
+// query row (token t, head h): keys j < len_t = pos + t + 1, score q.k_j / sqrt(D), softmax, times V;
+// the key axis [0, pos + n) is cut into chunks, each chunk leaves an unnormalized partial (m, l, o[D])
+// (attention.comp:26-75), and the combine merges them, skipping l = 0 splits, then applies
+// sigmoid(gate) (attn_combine.comp:13-29).
+//
+// MI355X design (not the reference's):
+//  - One workgroup per (chunk, KV head) serves every query row that shares the KV head — the G = NH/NKV
+//    heads of each of the n tokens, 8 or 16 rows — so each K/V row leaves HBM once (the reference runs
+//    one workgroup per query head and relies on L2 for the G-fold re-read). More than 16 rows (the
+//    4-token verify at G = 8) go to 16-row slices on grid.z: the slices of a chunk run side by side, so
+//    the second read of the chunk is served by the 256 MB Infinity Cache, and each slice keeps the
+//    register budget that lets it double-buffer its tiles.
+//  - The cache's blocked layout (common.hpp) makes every MFMA operand fragment one contiguous kilobyte,
+//    so a wave streams a 32-key tile (K and V, 32 KB at D = 256) with 32 fully coalesced 16-byte-per-lane
+//    loads straight into the operand registers — no LDS staging. Each wave keeps two tiles in flight
+//    (register double buffering): the next-but-one tile's K loads go out as soon as the current tile's
+//    scores are done, its V loads as soon as P.V is done.
+//  - S^T[32 keys x rows] = K . Q^T and O^T[D x rows] += V^T . P^T on v_mfma_f32_16x16x32_f16 with fp32
+//    accumulation. Q and P are carried as an fp16 "hi" part plus an fp16 "lo" remainder (22 mantissa
+//    bits together), so scores and weights keep fp32-level accuracy against the fp16 cache; with at most
+//    8 rows the lo parts ride in the otherwise unused columns 8-15 of the same MFMA.
+//  - Scores are in log2 units (q pre-multiplied by log2(e)/sqrt(D)), so exponentials are v_exp_f32.
+//  - Fused form: every workgroup normalizes and rotates its own query rows (RMSNorm (1+w) + partial
+//    RoPE, while its first tiles are in flight), and the workgroup whose chunk holds the n new positions
+//    normalizes/rotates their K rows, writes K and V to the cache for later steps, and patches them into
+//    its loaded tile registers — so one launch does the work of the reference's qk_norm_rope + attention
+//    dispatches.
+//  - The combine runs one workgroup per (row, 64-dim slice) with every partial load of a batch issued
+//    before any is used.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace qw {
+
+// MODE 0: at most 8 query rows, their fp16 lo parts in columns 8-15 of the same MFMA; MODE 1: a slice of
+// 16 rows, hi and lo parts as two MFMAs into one accumulator.
+template <int D, int MODE>
+struct DecCfg {
+    static constexpr int NKS = D / 32;                     // k-steps of the QK^T product
+    static constexpr int NDT = D / 16;                     // 16-dim tiles of the P.V product
+    static constexpr int RMAX = MODE == 0 ? 8 : 16;        // query rows of the workgroup
+    static constexpr int NQS = MODE == 0 ? 1 : 2;          // Q fragment sets in LDS (hi, lo)
+    static constexpr int QBYTES = NQS * NKS * 1024;
+    static constexpr int OSTRIDE = D + 4;                  // floats per row of the wave-partial buffer
+    static constexpr int MBYTES = 4 * RMAX * OSTRIDE * 4;
+    static constexpr int UBYTES = QBYTES > MBYTES ? QBYTES : MBYTES;
+    static constexpr int BLKE = kBlk * D;                  // elements of one (block, KV head) part
+    static constexpr int NB = 2;                           // blocks the new positions of a pass can span
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f16x8 as_h8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+__device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
+
+template <int D, int MODE, int FUSED, int IN_DT>
+__global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
+    using C = DecCfg<D, MODE>;
+    constexpr int NKS = C::NKS, NDT = C::NDT, RMAX = C::RMAX, BLKE = C::BLKE, NB = C::NB;
+    constexpr int NPT = MODE == 0 ? 1 : 2;  // P operands (hi, lo) per tile
+    constexpr int DPL2 = D / 32;            // dims per lane in the row passes
+    constexpr int QPASS = RMAX / 8;         // query-row passes per wave
+    constexpr float TAU = 8.f;              // a running max moves only when exceeded by this (log2 units)
+
+    __shared__ __attribute__((aligned(16))) unsigned char s_u[C::UBYTES];  // Q fragments, then wave partials
+    // new positions (fused): images of their cache blocks, [K, V][block], in the cache's blocked layout
+    __shared__ __attribute__((aligned(16))) f16 s_img[FUSED ? 2 * NB : 1][FUSED ? BLKE : 8];
+    __shared__ float sM[4][RMAX], sL[4][RMAX], sF[4][RMAX];
+    f16* s_q = reinterpret_cast<f16*>(s_u);
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int z = blockIdx.x, kvh = blockIdx.y;
+    const int G = a.NH / a.NKV;
+    const int r0 = blockIdx.z * RMAX;                  // first query row of this slice
+    const int rows = min(RMAX, a.n * G - r0);          // query rows of this workgroup
+    const int maxlen = a.pos + a.n;
+    const int kb = z * a.chunk;
+    const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, kb + a.chunk);
+    const int ntile_wg = (ke - kb + 31) >> 5;
+    const int ntile = ntile_wg > wave ? (ntile_wg - wave + 3) >> 2 : 0;  // tiles wave, wave + 4, ...
+    const int new_lo = FUSED ? a.pos : maxlen;        // first position not read from the cache
+
+    // Buffer resources over this chunk's blocks of this KV head. Tiles past the blocks that hold cached
+    // positions (the chunk end, or — fused — blocks of new positions only) fall outside the range and
+    // load zeros without touching memory, so every prefetch is issued unconditionally.
+    const int load_end = min(ke, new_lo);
+    const int nload = load_end > kb ? ((load_end - 1) >> 5) - (kb >> 5) + 1 : 0;
+    const int bstride = a.NKV * BLKE * 2;  // bytes between consecutive blocks of one head
+    const size_t part0 = ((size_t)(kb >> 5) * a.NKV + kvh) * BLKE;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.kc) + part0, (short)0, nload * bstride, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.vc) + part0, (short)0, nload * bstride, 0x00020000);
+    auto load_k = [&](f16x8 (&kt)[NKS][2], int t) {  // t: tile index within the chunk
+        const int off = t * bstride + lane * 16;
+#pragma unroll
+        for (int kk = 0; kk < NKS; kk++)
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+                kt[kk][s] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(rk, off + (kk * 2 + s) * 1024, 0, 0));
+    };
+    auto load_v = [&](f16x8 (&vt)[NDT], int t) {
+        const int off = t * bstride + lane * 16;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) vt[dt] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(rv, off + dt * 1024, 0, 0));
+    };
+
+    // ---- row passes: query rows (and, fused, the new K/V rows) normalized and rotated -------------
+    // Two rows per wave per pass, 32 lanes per row, DPL2 dims per lane. Their loads are issued before
+    // the tile loads: load completion is counted in order, so the passes finish while tiles stream in.
+    const int hw = lane >> 5, hl = lane & 31, d0 = hl * DPL2;
+    const int t_lo = FUSED ? max(a.pos, kb) - a.pos : 0;
+    const int t_hi = FUSED ? max(t_lo, min(maxlen, ke) - a.pos) : 0;
+    const int half_r = a.R >> 1;
+    float wq[DPL2], wk[DPL2];
+    float qx[QPASS][DPL2], qcv[QPASS][2 * DPL2];
+    float nx[DPL2], ncv[2 * DPL2], nv[DPL2];
+    bool qvalid[QPASS];
+    const bool rot = FUSED && d0 < a.R;  // lanes whose DPL2 dims are rotated (R/2 is a multiple of DPL2)
+    // one row's DPL2 values and (cos, sin) pairs: raw loads only (an invalid row reads row 0, lanes
+    // outside the rotated dims read the start of the table, padded for this); validity is applied
+    // when the row is finished, so nothing here waits for memory
+    auto issue_row = [&](float (&x)[DPL2], float (&cv)[2 * DPL2], const void* src, size_t off, int p, bool valid) {
+        load_vec<FUSED ? IN_DT : 0, DPL2>(src, (valid ? off : 0) + d0, x);
+        if constexpr (FUSED) {
+            const int i0 = rot ? (d0 < half_r ? d0 : d0 - half_r) : 0;
+            load_vec<0, 2 * DPL2>(a.rope, (size_t)(valid && rot ? p : 0) * a.R + 2 * i0, cv);
+        }
+    };
+    // y = x * rsqrt(mean(x^2) + eps) * (1 + w), then rotate-half on d < R (as norm_rope_row, with the
+    // row spread over 32 lanes; the partner dim d +- R/2 sits (R/2)/DPL2 lanes away in the same half)
+    auto finish_row = [&](const float (&xr)[DPL2], const float (&cv)[2 * DPL2], bool valid, const float (&w)[DPL2],
+                          float (&y)[DPL2]) {
+        float x[DPL2];
+        float ss = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            x[jj] = valid ? xr[jj] : 0.f;
+            ss += x[jj] * x[jj];
+        }
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) y[jj] = x[jj] * r * (1.0f + w[jj]);
+        const int offl = half_r / DPL2;
+        const bool lo_half = d0 < half_r;
+        const int src_lane = rot ? (lo_half ? lane + offl : lane - offl) : lane;
+        float partner[DPL2];
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) partner[jj] = __shfl(y[jj], src_lane, 64);  // all issued, then used
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            const float cs = rot ? cv[2 * jj] : 1.f, sn = rot ? cv[2 * jj + 1] : 0.f;
+            y[jj] = lo_half ? y[jj] * cs - partner[jj] * sn : y[jj] * cs + partner[jj] * sn;
+        }
+    };
+#pragma unroll
+    for (int ps = 0; ps < QPASS; ps++) {
+        const int r = ps * 8 + wave * 2 + hw;  // row within the slice
+        const bool valid = r < rows;
+        const int t = valid ? (r0 + r) / G : 0, h = kvh * G + (valid ? (r0 + r) % G : 0);
+        qvalid[ps] = valid;
+        if constexpr (FUSED) issue_row(qx[ps], qcv[ps], a.q, ((size_t)t * a.NH + h) * 2 * D, a.pos + t, valid);
+        else issue_row(qx[ps], qcv[ps], a.q, ((size_t)t * a.NH + h) * D, 0, valid);
+    }
+    const int tn = t_lo + wave * 2 + hw;  // new row of this half-wave (fused)
+    const bool has_new = FUSED && tn < t_hi;
+    if constexpr (FUSED) {
+        load_vec<0, DPL2>(a.qn, d0, wq);
+        load_vec<0, DPL2>(a.kn, d0, wk);
+        const size_t src = ((size_t)(has_new ? tn : 0) * a.NKV + kvh) * D;
+        issue_row(nx, ncv, a.knew, src, a.pos + (has_new ? tn : 0), has_new);
+        load_vec<IN_DT, DPL2>(a.vnew, src + d0, nv);
+    }
+
+    // ---- first two tiles in flight (kept after the row loads and before their use) ----------------
+    f16x8 kA[NKS][2], kB[NKS][2], vA[NDT], vB[NDT];
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(kA, wave);
+    load_v(vA, wave);
+    load_k(kB, wave + 4);
+    load_v(vB, wave + 4);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- finish the passes: query fp16 hi/lo fragments -> LDS; new rows -> block images and caches --
+#pragma unroll
+    for (int ps = 0; ps < QPASS; ps++) {
+        const int r = ps * 8 + wave * 2 + hw;
+        float y[DPL2];
+        if constexpr (FUSED) {
+            finish_row(qx[ps], qcv[ps], qvalid[ps], wq, y);
+        } else {
+#pragma unroll
+            for (int jj = 0; jj < DPL2; jj++) y[jj] = qvalid[ps] ? qx[ps][jj] : 0.f;
+        }
+        // the lane's DPL2 dims are consecutive inside one 8-dim group, so its hi and lo parts are one
+        // vector store each into the fragment layout
+        typedef f16 f16v __attribute__((ext_vector_type(DPL2)));
+        f16v hv, lv;
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            const float ys = y[jj] * a.q_scale;
+            const f16 hi = (f16)ys;
+            hv[jj] = hi;
+            lv[jj] = (f16)(ys - (float)hi);
+        }
+        const int col = MODE == 0 ? r : (r & 15);
+        const int kk = d0 >> 5, L = ((d0 >> 3) & 3) * 16 + col, e = d0 & 7;
+        *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L) * 8 + e]) = hv;
+        if constexpr (MODE == 0) *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L + 8) * 8 + e]) = lv;
+        else *reinterpret_cast<f16v*>(&s_q[((NKS + kk) * 64 + L) * 8 + e]) = lv;
+    }
+    if constexpr (FUSED) {
+        float y[DPL2];
+        finish_row(nx, ncv, has_new, wk, y);  // computed by every half-wave, stored by the owners
+        if (has_new) {
+            const int p = a.pos + tn;
+            const size_t part = kv_part(p, kvh, a.NKV, D);
+            f16* kw = reinterpret_cast<f16*>(a.kc) + part;
+            f16* vw = reinterpret_cast<f16*>(a.vc) + part;
+            const int pb = p & (kBlk - 1), bi = (p >> 5) - (a.pos >> 5);
+#pragma unroll
+            for (int jj = 0; jj < DPL2; jj++) {
+                const int d = d0 + jj;
+                const f16 kh = (f16)y[jj];
+                const f16 vh = (f16)nv[jj];
+                s_img[bi][k_off(pb, d)] = kh;
+                s_img[NB + bi][v_off(pb, d)] = vh;
+                if (blockIdx.z == 0) {  // every slice needs the rows; slice 0 writes them to the cache
+                    kw[k_off(pb, d)] = kh;
+                    vw[v_off(pb, d)] = vh;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- per column: query row, causal key limit inside this chunk, softmax state ----------------
+    const int rcol = MODE == 0 ? (c & 7) : c;
+    const int lim = rcol < rows ? min(a.pos + (r0 + rcol) / G + 1, ke) : 0;
+    float m_run = kNegInf, l_run = 0.f;
+    f32x4 acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f16x8 qreg[MODE == 0 ? NKS : 1];
+    if constexpr (MODE == 0) {
+#pragma unroll
+        for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
+    }
+    auto qfrag = [&](int set, int kk) -> f16x8 {
+        return *reinterpret_cast<const f16x8*>(s_q + ((set * NKS + kk) * 64 + lane) * 8);
+    };
+
+    // scores of one tile: sc[s][i] is key tb + 8g + 4s + i of column c
+    auto scores = [&](f16x8 (&kt)[NKS][2], int tb, f32x4 (&sc)[2]) {
+        if (FUSED && tb + 32 > new_lo) {  // new positions: take the fresh rows from the block image
+            const int bi = (tb >> 5) - (a.pos >> 5);
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const int key = tb + ((c >> 2) << 3) + 4 * s + (c & 3);
+                const bool fresh = key >= new_lo && key < maxlen;
+#pragma unroll
+                for (int kk = 0; kk < NKS; kk++) {
+                    const f16x8 im = *reinterpret_cast<const f16x8*>(&s_img[bi][((kk * 2 + s) * 64 + lane) * 8]);
+                    kt[kk][s] = fresh ? im : kt[kk][s];
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < NKS; kk++) {
+                if constexpr (MODE == 0) {
+                    x = mfma16(kt[kk][s], qreg[kk], x);
+                } else {
+                    x = mfma16(kt[kk][s], qfrag(0, kk), x);
+                    x = mfma16(kt[kk][s], qfrag(1, kk), x);
+                }
+            }
+            sc[s] = x;
+        }
+    };
+
+    auto softmax_pv = [&](f16x8 (&vt)[NDT], int tb, f32x4 (&sc)[2]) {
+        if (tb + 32 > new_lo) {
+            // positions past the cache end may hold stale or unwritten memory: zeroed; new positions
+            // (fused) take the fresh V rows from the block image. Masks per dword = two keys.
+            uint32_t keep[4], take[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int k0 = tb + 8 * g + 2 * k;
+                keep[k] = (k0 < new_lo ? 0x0000ffffu : 0u) | (k0 + 1 < new_lo ? 0xffff0000u : 0u);
+                take[k] = FUSED ? ((k0 >= new_lo && k0 < maxlen ? 0x0000ffffu : 0u) |
+                                   (k0 + 1 >= new_lo && k0 + 1 < maxlen ? 0xffff0000u : 0u)) : 0u;
+            }
+            const int bi = (tb >> 5) - (a.pos >> 5);
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                u32x4 v = as_u4(vt[dt]);
+                u32x4 im = {0u, 0u, 0u, 0u};
+                if constexpr (FUSED) im = *reinterpret_cast<const u32x4*>(&s_img[NB + bi][(dt * 64 + lane) * 8]);
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[k] = (v[k] & keep[k]) | (im[k] & take[k]);
+                vt[dt] = as_h8(v);
+            }
+        }
+        float sv[8];
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float v = MODE == 0 ? sc[s][i] + xor8(sc[s][i]) : sc[s][i];
+                const int key = tb + 8 * g + 4 * s + i;
+                sv[s * 4 + i] = key < lim ? v : kNegInf;
+            }
+        float mx = sv[0];
+#pragma unroll
+        for (int k = 1; k < 8; k++) mx = fmaxf(mx, sv[k]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // lazy rescale: the reference max moves (and o, l are rescaled) only when a column's max grows
+        // by more than TAU, so the weights below stay <= 2^TAU; a column's first finite max is taken
+        // as is (its o and l are still zero)
+        if (m_run == kNegInf) m_run = mx;
+        const bool grow = mx > m_run + TAU;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = fmaxf(m_run, mx);
+            const float corr = exp2_fast(m_run - m_new);
+            m_run = m_new;
+            l_run *= corr;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) acc[dt] *= corr;
+        }
+        const float m_use = m_run == kNegInf ? 0.f : m_run;
+        float psum = 0.f;
+        f16x8 pop[NPT];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float p = exp2_fast(sv[k] - m_use);
+            psum += p;
+            const f16 ph = (f16)p;
+            const f16 pl = (f16)(p - (float)ph);
+            if constexpr (MODE == 0) {
+                pop[0][k] = c >= 8 ? pl : ph;
+            } else {
+                pop[0][k] = ph;
+                pop[1][k] = pl;
+            }
+        }
+        l_run += psum;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int u = 0; u < NPT; u++) acc[dt] = mfma16(vt[dt], pop[u], acc[dt]);
+    };
+
+    // ---- main loop: two register buffers, tiles wave, wave + 4, ...; loads always issued ----------
+    for (int i = 0; i < ntile; i += 2) {
+        {
+            const int t = wave + 4 * i, tb = kb + 32 * t;
+            f32x4 sc[2];
+            scores(kA, tb, sc);
+            load_k(kA, t + 8);
+            softmax_pv(vA, tb, sc);
+            load_v(vA, t + 8);
+        }
+        {
+            const int t = wave + 4 * (i + 1), tb = kb + 32 * t;
+            f32x4 sc[2];
+            const bool live = i + 1 < ntile;
+            if (live) scores(kB, tb, sc);
+            load_k(kB, t + 8);
+            if (live) softmax_pv(vB, tb, sc);
+            load_v(vB, t + 8);
+        }
+    }
+
+    // ---- wave results -> LDS (the Q fragments are dead once every wave is here) -------------------
+    __syncthreads();
+    float* sO = reinterpret_cast<float*>(s_u);
+    {
+        float l = l_run;
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if constexpr (MODE == 0) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[dt][i] += xor8(acc[dt][i]);
+        }
+        if (MODE != 0 || c < 8) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                *reinterpret_cast<f32x4*>(&sO[(wave * RMAX + c) * C::OSTRIDE + dt * 16 + g * 4]) = acc[dt];
+            if (g == 0) {
+                sM[wave][c] = m_run;
+                sL[wave][c] = l;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- merge the 4 waves: per-row weights first, then every element without branches ----------
+    if (tid < rows) {
+        const int r = tid;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            if (sL[w][r] > 0.f) M = fmaxf(M, sM[w][r]);
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = sL[w][r] > 0.f ? exp2_fast(sM[w][r] - M) : 0.f;
+            sF[w][r] = f;
+            L += sL[w][r] * f;
+        }
+        const int t = (r0 + r) / G, h = kvh * G + (r0 + r) % G;
+        const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
+        a.part_ml[row * 2] = M;
+        a.part_ml[row * 2 + 1] = L;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < rows * (D / 4); idx += 256) {
+        const int r = idx / (D / 4), d = (idx % (D / 4)) * 4;
+        f32x4 o = *reinterpret_cast<const f32x4*>(&sO[r * C::OSTRIDE + d]) * sF[0][r];
+#pragma unroll
+        for (int w = 1; w < 4; w++) o += *reinterpret_cast<const f32x4*>(&sO[(w * RMAX + r) * C::OSTRIDE + d]) * sF[w][r];
+        const int t = (r0 + r) / G, h = kvh * G + (r0 + r) % G;
+        const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
+        *reinterpret_cast<f32x4*>(&a.part_o[row * D + d]) = o;
+    }
+}
+
+template <int D, int FUSED, int IN_DT>
+static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
+    const int rows = a.n * (a.NH / a.NKV);
+    const dim3 block(256);
+    if (rows <= 8) hipLaunchKernelGGL((k_decode<D, 0, FUSED, IN_DT>), dim3(a.n_split, a.NKV, 1), block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<D, 1, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), block, 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_decode_d(const DecodeArgs& a, bool fused, int in_dtype, hipStream_t s) {
+    if (!fused) return launch_mode<D, 0, 0>(a, s);
+    return in_dtype == 0 ? launch_mode<D, 1, 0>(a, s) : launch_mode<D, 1, 1>(a, s);
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s) {
+    if (D == 256) return launch_decode_d<256>(a, fused, in_dtype, s);
+    if (D == 128) return launch_decode_d<128>(a, fused, in_dtype, s);
+    return launch_decode_d<64>(a, fused, in_dtype, s);
+}
+
+// ---- combine ---------------------------------------------------------------------------------------
+// One workgroup per (row, 64-dim slice): 16 split lanes x 16 dim lanes of 4 dims. Each thread merges
+// the splits z = zg, zg + 16, ... with an online (m, l, o) update, loading a batch of 8 splits before
+// using any; the 16 thread-partials of a dim group then merge through LDS. Splits with l = 0 are
+// skipped (attn_combine.comp:17-26).
+template <int IN_DT>
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a, int D) {
+    constexpr int BATCH = 8;
+    __shared__ float sMt[16][16], sLt[16][16];
+    __shared__ f32x4 sOt[16][16];
+    const int tid = threadIdx.x;
+    const int zg = tid >> 4, q = tid & 15;
+    const int row = blockIdx.x;  // t * NH + h
+    const int S = a.n_split;
+    const int d0 = blockIdx.y * 64 + q * 4;
+    const float* ml = a.part_ml + (size_t)row * S * 2;
+    const float* po = a.part_o + (size_t)row * S * D + d0;
+
+    float M = kNegInf, L = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int z0 = zg; z0 < S; z0 += 16 * BATCH) {
+        float m[BATCH], l[BATCH];
+        f32x4 o[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {  // every load of the batch is issued before any is used
+            const int zz = min(z0 + 16 * u, S - 1);
+            m[u] = ml[2 * zz];
+            l[u] = ml[2 * zz + 1];
+            o[u] = *reinterpret_cast<const f32x4*>(po + (size_t)zz * D);
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+            if (z0 + 16 * u < S && l[u] > 0.f) {
+                const float mn = fmaxf(M, m[u]);
+                const float cf = exp2_fast(M - mn), cu = exp2_fast(m[u] - mn);
+                L = L * cf + l[u] * cu;
+                O = O * cf + o[u] * cu;
+                M = mn;
+            }
+        }
+    }
+    sMt[zg][q] = M;
+    sLt[zg][q] = L;
+    sOt[zg][q] = O;
+    __syncthreads();
+    if (zg == 0) {
+        float Mx = kNegInf;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (sLt[k][q] > 0.f) Mx = fmaxf(Mx, sMt[k][q]);
+        float Ls = 0.f;
+        f32x4 Os = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (sLt[k][q] > 0.f) {
+                const float f = exp2_fast(sMt[k][q] - Mx);
+                Ls += sLt[k][q] * f;
+                Os += sOt[k][q] * f;
+            }
+        }
+        const int t = row / a.NH, h = row % a.NH;
+        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + d0;
+        float* out = a.out + (size_t)row * D + d0;
+        const float inv = 1.0f / Ls;
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = Os[i] * inv * sigmoid(load_in<IN_DT>(a.qg, gb + i));
+    }
+}
+
+hipError_t launch_combine(const CombineArgs& a, int D, int in_dtype, hipStream_t s) {
+    const dim3 grid(a.n * a.NH, D / 64), block(256);
+    if (in_dtype == 0) hipLaunchKernelGGL(k_combine<0>, grid, block, 0, s, a, D);
+    else hipLaunchKernelGGL(k_combine<1>, grid, block, 0, s, a, D);
+    return hipGetLastError();
+}
+
+}  // namespace qw

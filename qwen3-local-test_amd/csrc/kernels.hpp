@@ -1,5 +1,5 @@
 // Host-side launchers of the gfx950 kernels (internal to libqwattn; the C ABI in qwattn.cpp checks
-// every shape and pointer before calling these).
+// every shape and pointer before calling these). K/V caches use the blocked layout of common.hpp.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -12,27 +12,35 @@ struct NormRopeArgs {
     const void* qg;      // [n][NH][2D]
     const void* k;       // [n][NKV][D]
     const void* v;       // [n][NKV][D]
-    const float* qn;     // [D], multiplier (1 + w)
+    const float* qn;     // [D], w of the (1 + w) multiplier
     const float* kn;     // [D]
     const float* rope;   // [>= pos+n][R/2][2]
-    uint16_t* kcache;    // [cap][NKV][D] fp16
-    uint16_t* vcache;    // [cap/8][NKV][D][8] fp16
+    uint16_t* kcache;    // blocked fp16
+    uint16_t* vcache;    // blocked fp16
     void* q_out;         // [n][NH][D] fp32, or fp16 pre-scaled by log2(e)/sqrt(D)
     int pos, n, NH, NKV, R;
     float eps, q_scale;
 };
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int D, int in_dtype, int q_dtype, hipStream_t s);
 
-struct SplitArgs {
-    const float* q;       // [n][NH][D] fp32 (normalized, rotated, not scaled)
-    const uint16_t* kc;   // [cap][NKV][D]
-    const uint16_t* vc;   // [cap/8][NKV][D][8]
+// Split-KV decode / verify. With `fused`, q is the projection output qg [n][NH][2D] (in_dtype) and the
+// kernel also does the QK-norm, RoPE and the K/V append of the n new tokens (knew/vnew [n][NKV][D]);
+// otherwise q is the normalized, rotated query [n][NH][D] fp32 and the new rows are already cached.
+struct DecodeArgs {
+    const void* q;
+    const void* knew;
+    const void* vnew;
+    const float* qn;      // fused: norm weights w (multiplier 1 + w)
+    const float* kn;
+    const float* rope;    // fused: rope table
+    uint16_t* kc;         // blocked K cache
+    uint16_t* vc;         // blocked V cache
     float* part_o;        // [n*NH][n_split][D]
     float* part_ml;       // [n*NH][n_split][2]: running max (log2 units), sum
-    int pos, n, NH, NKV, chunk, n_split;
-    float q_scale;        // log2(e) / sqrt(D)
+    int pos, n, NH, NKV, R, chunk, n_split;
+    float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
 };
-hipError_t launch_attend_split(const SplitArgs& a, int D, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 
 struct CombineArgs {
     const float* part_o;

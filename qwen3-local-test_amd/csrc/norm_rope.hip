@@ -5,12 +5,13 @@
 //   d < R/2:      y'[d] = y[d] cos_i - y[d + R/2] sin_i            (qk_norm_rope.comp:36-42,
 //   R/2 <= d < R: y'[d] = y[d] cos_i + y[d - R/2] sin_i             src/qwen4_cpu.cpp:281-289)
 // with (cos_i, sin_i) from row p = pos + t of the rope table. Query heads write q_out; key heads
-// write K cache row p (round-to-nearest-even fp16, as packHalf2x16) and copy V into the V cache.
+// write K cache position p (round-to-nearest-even fp16, as packHalf2x16) and copy V into the V cache.
 //
 // MI355X layout: one 64-lane wavefront per (token, head) — the reference uses a 256-invocation
 // workgroup with an LDS reduction per head — so the mean of squares is a wave reduction with no
-// barrier, and each lane holds D/64 contiguous dims (one 16-byte load at D = 256). The RoPE partner
-// dim d +- R/2 lives R/2/(D/64) lanes away and comes in through a cross-lane shuffle.
+// barrier (norm_rope_row in common.hpp). The caches are written in the blocked layout of common.hpp.
+// The split-KV decode kernel (decode.hip) does the same work inline for its new tokens; this kernel
+// serves prefill chunks and callers of the per-dispatch entry point.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -29,38 +30,10 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
     const int p = a.pos + t;
     const int d0 = lane * DPL;
 
-    float x[DPL];
     const size_t src = is_q ? ((size_t)t * a.NH + h) * 2 * D : ((size_t)t * a.NKV + h) * D;
-    const void* base = is_q ? a.qg : a.k;
-#pragma unroll
-    for (int j = 0; j < DPL; j++) x[j] = load_in<IN_DT>(base, src + d0 + j);
-
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < DPL; j++) ss += x[j] * x[j];
-    ss = wave_sum(ss);
-    const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
-    const float* w = is_q ? a.qn : a.kn;
     float y[DPL];
-#pragma unroll
-    for (int j = 0; j < DPL; j++) y[j] = x[j] * r * (1.0f + w[d0 + j]);
-
-    // partial rotate-half: the partner of dim d is d + half (d < half) or d - half (half <= d < R)
-    const int half = a.R >> 1;
-    const int off = half / DPL;  // lanes between partners (host checks half % DPL == 0)
-    const bool lo_half = d0 < half;
-    const int src_lane = lo_half ? lane + off : lane - off;
-    const float* rp = a.rope + (size_t)p * a.R;
-#pragma unroll
-    for (int j = 0; j < DPL; j++) {
-        const float partner = __shfl(y[j], src_lane & 63, 64);
-        const int d = d0 + j;
-        if (d < a.R) {
-            const int i = lo_half ? d : d - half;
-            const float c = rp[2 * i], s = rp[2 * i + 1];
-            y[j] = lo_half ? y[j] * c - partner * s : y[j] * c + partner * s;
-        }
-    }
+    norm_rope_row<D, IN_DT>(is_q ? a.qg : a.k, src, is_q ? a.qn : a.kn, a.rope + (size_t)p * a.R, a.R, a.eps,
+                            lane, y);
 
     if (is_q) {
         if constexpr (Q_DT == 0) {
@@ -73,14 +46,16 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
             for (int j = 0; j < DPL; j++) qo[j] = (f16)(y[j] * a.q_scale);
         }
     } else {
-        f16* kc = reinterpret_cast<f16*>(a.kcache) + ((size_t)p * a.NKV + h) * D + d0;
-#pragma unroll
-        for (int j = 0; j < DPL; j++) kc[j] = (f16)y[j];
-        // V cache: groups of 8 positions interleaved per dim
-        f16* vc = reinterpret_cast<f16*>(a.vcache) + (((size_t)(p >> 3) * a.NKV + h) * D + d0) * 8 + (p & 7);
+        const size_t part = kv_part(p, h, a.NKV, D);
+        f16* kc = reinterpret_cast<f16*>(a.kcache) + part;
+        f16* vc = reinterpret_cast<f16*>(a.vcache) + part;
+        const int kb = p & (kBlk - 1);
         const size_t vs = ((size_t)t * a.NKV + h) * D + d0;
 #pragma unroll
-        for (int j = 0; j < DPL; j++) vc[j * 8] = (f16)load_in<IN_DT>(a.v, vs + j);
+        for (int j = 0; j < DPL; j++) {
+            kc[k_off(kb, d0 + j)] = (f16)y[j];
+            vc[v_off(kb, d0 + j)] = (f16)load_in<IN_DT>(a.v, vs + j);
+        }
     }
 }
 

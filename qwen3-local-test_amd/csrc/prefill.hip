@@ -10,9 +10,10 @@
 //  - S^T[32 keys x 32 rows] = K Q^T and O^T[D x 32 rows] += V^T P^T on v_mfma_f32_32x32x16_f16 with
 //    fp32 accumulators (O^T lives in 8 x 16 accumulator registers per lane at D = 256). Q is fp16
 //    pre-multiplied by log2(e)/sqrt(D) and stays in registers for the whole key sweep.
-//  - K tiles (64 keys) sit in LDS row-major with the 16-byte chunk index XOR-swizzled by the key so
-//    the 32 lanes that read one dim chunk of 32 different keys hit distinct banks; V tiles keep the
-//    cache's 8-position interleave, which is already the A-operand shape of the P.V product.
+//  - K tiles (64 keys) are gathered from the blocked cache (common.hpp) into LDS row-major with the
+//    16-byte chunk index XOR-swizzled by the key so the 32 lanes that read one dim chunk of 32 different
+//    keys hit distinct banks; V tiles are gathered as 8-position groups per dim, the A-operand shape of
+//    the P.V product.
 //  - Global->LDS staging is double-buffered with one barrier per tile: tile i+1 is in flight in
 //    registers while tile i is consumed, then lands in the other LDS buffer.
 //  - Key tiles strictly below every row's causal limit skip the mask; tiles past it are skipped.
@@ -111,11 +112,11 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
             const int idx = i * 256 + tid;           // chunk index within the tile
             const int key = idx / CH, ch = idx % CH;
             const int gk = min(k0 + key, last_row);
-            stK[i] = *reinterpret_cast<const f16x8*>(kc + ((size_t)gk * a.NKV + kvh) * D + ch * 8);
-            // V: 8 blocks of 8 positions, each D chunks of 16 bytes
+            stK[i] = *reinterpret_cast<const f16x8*>(kc + kv_part(gk, kvh, a.NKV, D) + k_off(gk & (kBlk - 1), ch * 8));
+            // V: 8 groups of 8 positions, each D chunks of 16 bytes (8 consecutive keys of one dim)
             const int vb = idx / D, vd = idx % D;
-            const int gb = min(k0 / 8 + vb, last_row >> 3);
-            stV[i] = *reinterpret_cast<const f16x8*>(vc + (((size_t)gb * a.NKV + kvh) * D + vd) * 8);
+            const int gp = min(k0 / 8 + vb, last_row >> 3) * 8;
+            stV[i] = *reinterpret_cast<const f16x8*>(vc + kv_part(gp, kvh, a.NKV, D) + v_off(gp & (kBlk - 1), vd));
         }
     };
     auto store_tile = [&](int buf, int kt) {

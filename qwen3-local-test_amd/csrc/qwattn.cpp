@@ -28,7 +28,7 @@ struct qwattn_ctx {
     float* q32 = nullptr;        // [max_tokens][NH][D] layer-path query (fp32)
     void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
-    int last_splits = 0;         // split count of the last qwattn_attend_partial
+    int last_splits = 0;         // split count of the last qwattn_attend_partial / qwattn_decode_partial
     int last_n = 0;
     std::vector<uint16_t*> kc, vc;
     int kv_cap = 0;
@@ -75,9 +75,10 @@ int check_shape(qwattn_ctx* c, const qwattn_config& g) {
         return fail(c, QWATTN_EINVAL, "unsupported attention head counts (%d, %d)", g.n_heads, g.n_kv_heads);
     if (g.head_dim != 64 && g.head_dim != 128 && g.head_dim != 256)
         return fail(c, QWATTN_EINVAL, "head_dim %d not supported (64, 128, 256)", g.head_dim);
-    const int dpl = g.head_dim / 64;
+    // RoPE pairs (d, d + R/2) are exchanged between lanes that hold D/32 consecutive dims each
+    const int dpl = g.head_dim / 32;
     if (g.rope_dim < 0 || g.rope_dim > g.head_dim || g.rope_dim % 2 || (g.rope_dim / 2) % dpl)
-        return fail(c, QWATTN_EINVAL, "unsupported rope dimension %d", g.rope_dim);
+        return fail(c, QWATTN_EINVAL, "unsupported rope dimension %d (R/2 must be a multiple of %d)", g.rope_dim, dpl);
     const int G = g.n_heads / g.n_kv_heads;
     if (G > 32 || 128 % G)
         return fail(c, QWATTN_EINVAL, "GQA group %d not supported (a power of two <= 32)", G);
@@ -93,24 +94,40 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
     if (n > c->cfg.max_tokens) return fail(c, QWATTN_EINVAL, "n = %d exceeds max_tokens %d", n, c->cfg.max_tokens);
     if ((long long)pos + n > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow (%d + %d > %d)", pos, n, c->cfg.max_ctx);
     if ((long long)pos + n > kv_cap) return fail(c, QWATTN_ERANGE, "context overflow: %d + %d rows exceed the K/V cache capacity %d", pos, n, kv_cap);
-    if (kv_cap % 8) return fail(c, QWATTN_EINVAL, "K/V cache capacity %d is not a multiple of 8", kv_cap);
+    if (kv_cap % 32) return fail(c, QWATTN_EINVAL, "K/V cache capacity %d is not a multiple of 32", kv_cap);
     return QWATTN_OK;
 }
 
-// The split chunk: ceil(maxlen / n_split) rounded up to the 32-key tile; n_split 0 = automatic (about
-// two workgroups per CU, at least one 32-key tile per wave).
-void pick_split(const qwattn_ctx* c, int maxlen, int n_split, int* chunk, int* used) {
-    if (n_split <= 0) {
-        const int target = std::max(1, 2 * c->n_cu / c->cfg.n_kv_heads);
-        int ch = (maxlen + target - 1) / target;
-        ch = std::max(128, (ch + 127) / 128 * 128);
-        n_split = (maxlen + ch - 1) / ch;
+// Split of the key axis [0, maxlen) for the decode kernel: `chunk` keys per workgroup (a multiple of
+// the 32-key tile), `used` chunks, the last one ending at maxlen. A requested count n_split > 0 follows
+// the reference (chunk = ceil(maxlen / n_split), src/qwen4_vk.cpp:974-978, rounded up to the tile).
+// n_split = 0 picks one workgroup per CU: chunk = maxlen / (CUs per KV head and row slice) rounded down
+// to the tile,
+// and a remainder of at most a quarter chunk — typically the one new position of a decode step — is
+// absorbed by the last chunk instead of costing a second round of workgroups.
+void pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int* chunk, int* used) {
+    const int maxs = c->cfg.max_splits;
+    const int rows = n * (c->cfg.n_heads / c->cfg.n_kv_heads);
+    const int slices = rows <= 8 ? 1 : (rows + 15) / 16;  // the decode kernel's 16-row slices (grid.z)
+    int ch, S;
+    if (n_split > 0) {
+        S = std::min(n_split, maxs);
+        ch = (maxlen + S - 1) / S;
+        ch = (ch + 31) / 32 * 32;
+        S = (maxlen + ch - 1) / ch;
+    } else {
+        const int target = std::max(1, c->n_cu / (c->cfg.n_kv_heads * slices));
+        ch = std::max(32, maxlen / target / 32 * 32);
+        S = std::max(1, maxlen / ch);
+        if (maxlen - S * ch > ch / 4) S++;
+        if (S > maxs) {
+            ch = (maxlen + maxs - 1) / maxs;
+            ch = (ch + 31) / 32 * 32;
+            S = (maxlen + ch - 1) / ch;
+        }
     }
-    n_split = std::min(n_split, c->cfg.max_splits);
-    int ch = (maxlen + n_split - 1) / n_split;
-    ch = (ch + 31) / 32 * 32;
     *chunk = ch;
-    *used = (maxlen + ch - 1) / ch;
+    *used = S;
 }
 
 }  // namespace
@@ -143,7 +160,8 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     c->n_cu = prop.multiProcessorCount;
     const int NH = cfg->n_heads, NKV = cfg->n_kv_heads, D = cfg->head_dim, R = cfg->rope_dim;
     c->split_rows = 32 * NKV;
-    const size_t rope_n = (size_t)cfg->max_ctx * std::max(1, R / 2) * 2;
+    // + 64 floats: the decode kernel's lanes outside the rotated dims read (and discard) the table start
+    const size_t rope_n = (size_t)cfg->max_ctx * std::max(1, R / 2) * 2 + 64;
     const size_t part = (size_t)c->split_rows * cfg->max_splits;
     const size_t qn = (size_t)cfg->max_tokens * NH * D;
     bool ok = hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
@@ -206,7 +224,7 @@ int qwattn_fill_rope(qwattn_ctx* c, void* stream, float* rope, int n_pos) {
 int qwattn_kv_alloc(qwattn_ctx* c, int n_slots, int cap) {
     if (!c) return QWATTN_EINVAL;
     if (n_slots <= 0 || cap <= 0) return fail(c, QWATTN_EINVAL, "qwattn_kv_alloc: %d slots of %d tokens", n_slots, cap);
-    cap = std::min((cap + 7) / 8 * 8, (c->cfg.max_ctx + 7) / 8 * 8);
+    cap = std::min((cap + 31) / 32 * 32, (c->cfg.max_ctx + 31) / 32 * 32);
     DeviceGuard dg(c->device);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
@@ -231,8 +249,8 @@ int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
     if (tokens <= c->kv_cap) return QWATTN_OK;
     if (tokens > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow growing the K/V caches to %d", tokens);
     long long cap = std::max<long long>(2ll * c->kv_cap, tokens);
-    cap = std::min<long long>(cap, (c->cfg.max_ctx + 7) / 8 * 8);
-    cap = (cap + 7) / 8 * 8;
+    cap = std::min<long long>(cap, (c->cfg.max_ctx + 31) / 32 * 32);
+    cap = (cap + 31) / 32 * 32;
     DeviceGuard dg(c->device);
     hipStream_t s = (hipStream_t)stream;
     const size_t per = (size_t)c->cfg.n_kv_heads * c->cfg.head_dim * 2;
@@ -244,7 +262,7 @@ int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
             if (nk) (void)hipFree(nk);
             return fail(c, QWATTN_ENOMEM, "out of VRAM growing the K/V caches");
         }
-        // both layouts keep rows [0, cap) as a prefix (the V interleave groups 8 whole positions)
+        // the blocked layout keeps whole 32-position blocks in order, so the old caches are a prefix
         HIP_TRY(c, hipMemsetAsync(nk, 0, bytes, s));
         HIP_TRY(c, hipMemsetAsync(nv, 0, bytes, s));
         HIP_TRY(c, hipMemcpyAsync(nk, c->kc[i], old_bytes, hipMemcpyDeviceToDevice, s));
@@ -299,11 +317,39 @@ int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const voi
     if (n * G > 32)
         return fail(c, QWATTN_EINVAL, "qwattn_attend_partial: n * NH/NKV = %d > 32 rows (use the prefill kernel)", n * G);
     int chunk = 0, used = 0;
-    pick_split(c, pos + n, n_split, &chunk, &used);
+    pick_split(c, pos + n, n, n_split, &chunk, &used);
     DeviceGuard dg(c->device);
-    qw::SplitArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, c->part_o, c->part_ml, pos, n,
-                    g.n_heads, g.n_kv_heads, chunk, used, qw::kLog2eHost / std::sqrt((float)g.head_dim)};
-    HIP_TRY(c, qw::launch_attend_split(a, g.head_dim, (hipStream_t)stream));
+    qw::DecodeArgs a{q, nullptr, nullptr, nullptr, nullptr, nullptr, (uint16_t*)kcache, (uint16_t*)vcache,
+                     c->part_o, c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+    HIP_TRY(c, qw::launch_decode(a, g.head_dim, false, QWATTN_F32, (hipStream_t)stream));
+    c->last_splits = used;
+    c->last_n = n;
+    if (used_splits) *used_splits = used;
+    return QWATTN_OK;
+}
+
+int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
+                          const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
+                          int pos, int n, int n_split, int* used_splits) {
+    if (!c) return QWATTN_EINVAL;
+    if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || (!rope && c->cfg.rope_dim))
+        return fail(c, QWATTN_EINVAL, "qwattn_decode_partial: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    int rc = check_call(c, pos, n, kv_cap);
+    if (rc) return rc;
+    const qwattn_config& g = c->cfg;
+    const int G = g.n_heads / g.n_kv_heads;
+    if (n * G > 32 || n > 8)
+        return fail(c, QWATTN_EINVAL, "qwattn_decode_partial: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
+                    "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
+    int chunk = 0, used = 0;
+    pick_split(c, pos + n, n, n_split, &chunk, &used);
+    DeviceGuard dg(c->device);
+    qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
+                     c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+    HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
     if (used_splits) *used_splits = used;
@@ -314,7 +360,8 @@ int qwattn_combine(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, fl
     if (!c) return QWATTN_EINVAL;
     if (!qg || !out) return fail(c, QWATTN_EINVAL, "qwattn_combine: null pointer");
     if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
-    if (c->last_splits == 0) return fail(c, QWATTN_ESTATE, "qwattn_combine: no partials (call qwattn_attend_partial first)");
+    if (c->last_splits == 0)
+        return fail(c, QWATTN_ESTATE, "qwattn_combine: no partials (call qwattn_attend_partial or qwattn_decode_partial first)");
     if (n != c->last_n || n_split != c->last_splits)
         return fail(c, QWATTN_EINVAL, "qwattn_combine: n=%d splits=%d do not match the last partials (n=%d splits=%d)", n,
                     n_split, c->last_n, c->last_splits);
@@ -346,12 +393,19 @@ int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg
     if (slot < 0 || slot >= (int)c->kc.size())
         return fail(c, QWATTN_ESTATE, "qwattn_layer_attention: slot %d of %d allocated K/V caches", slot, (int)c->kc.size());
     const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
+    int rc, used = 0;
+    if (n * G <= 32 && n <= 8) {
+        // decode / verify: one fused launch (norm + rope + append + split attend), then the combine
+        rc = qwattn_decode_partial(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap,
+                                   pos, n, n_split, &used);
+        if (rc) return rc;
+        return qwattn_combine(c, stream, qg, in_dtype, out, n, used);
+    }
     const bool split = n * G <= 32;
-    int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
-                                        c->kv_cap, split ? (void*)c->q32 : c->q16, split ? QWATTN_F32 : QWATTN_F16, pos, n);
+    rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
+                                    c->kv_cap, split ? (void*)c->q32 : c->q16, split ? QWATTN_F32 : QWATTN_F16, pos, n);
     if (rc) return rc;
     if (split) {
-        int used = 0;
         rc = qwattn_attend_partial(c, stream, c->q32, c->kc[slot], c->vc[slot], c->kv_cap, pos, n, n_split, &used);
         if (rc) return rc;
         return qwattn_combine(c, stream, qg, in_dtype, out, n, used);

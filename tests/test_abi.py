@@ -47,6 +47,6 @@ def test_bad_shapes_rejected_before_any_device_call():
     """Shape checks come first: they fail identically with or without a GPU."""
     qw = common.load_package()
     for args, pat in [((16, 3, 256, 64), "head counts"), ((16, 2, 96, 64), "head_dim"),
-                      ((16, 2, 256, 63), "rope dimension"), ((64, 1, 256, 64), "GQA group")]:
+                      ((16, 2, 256, 63), "rope dimension"), ((16, 2, 256, 12), "rope dimension"), ((64, 1, 256, 64), "GQA group")]:
         with pytest.raises(qw.QwattnError, match=pat):
             qw.Attention(*args)

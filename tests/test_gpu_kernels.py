@@ -27,14 +27,23 @@ def make_ctx(qw, s, max_ctx=8192, max_tokens=2048, max_splits=1024):
                         max_splits=max_splits)
 
 
+def capacity(rows):
+    return (rows + 31) // 32 * 32
+
+
 def gpu_caches(qw, k16, v16, cap):
-    """Caller-owned device caches of capacity cap holding rows [0, len(k16))."""
+    """Caller-owned device caches (blocked layout) of capacity cap holding rows [0, len(k16))."""
     rows, nkv, d = k16.shape
-    kc = torch.zeros((cap, nkv, d), dtype=torch.float16, device=DEV)
-    kc[:rows] = dev(k16)
+    krows = torch.zeros((cap, nkv, d), dtype=torch.float16, device=DEV)
+    krows[:rows] = dev(k16)
     vrows = torch.zeros((cap, nkv, d), dtype=torch.float16, device=DEV)
     vrows[:rows] = dev(v16)
-    return kc, qw.v_interleave(vrows)
+    return qw.k_block(krows), qw.v_block(vrows)
+
+
+def empty_caches(s, cap):
+    n = cap * s.NKV * s.D
+    return (torch.zeros(n, dtype=torch.float16, device=DEV), torch.zeros(n, dtype=torch.float16, device=DEV))
 
 
 # ---- rope table --------------------------------------------------------------------------------------
@@ -69,9 +78,8 @@ def test_qk_norm_rope_append(qw, oracle, s, n, pos, dtype):
     # the oracle sees exactly the values the GPU reads
     qg_h, k_h, v_h = host(qg_d), host(k_d), host(v_d)
     ctx = make_ctx(qw, s, max_ctx=262144)
-    cap = (pos + n + 7) // 8 * 8
-    kc = torch.zeros((cap, s.NKV, s.D), dtype=torch.float16, device=DEV)
-    vc = torch.zeros(cap * s.NKV * s.D, dtype=torch.float16, device=DEV)
+    cap = capacity(pos + n)
+    kc, vc = empty_caches(s, cap)
     q_out = torch.zeros((n, s.NH, s.D), device=DEV)
     ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, q_out, pos, n)
     q16 = torch.zeros((n, s.NH, s.D), dtype=torch.float16, device=DEV)
@@ -80,13 +88,15 @@ def test_qk_norm_rope_append(qw, oracle, s, n, pos, dtype):
     rq, rk, rv = oracle.qk_norm_rope(qg_h, k_h, v_h, 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
     assert np.abs(host(q_out) - rq).max() <= 2e-5 * max(1.0, np.abs(rq).max())
     # fp16 K rows: within one fp16 rounding step of the oracle's fp32 row
-    gk = host(kc[pos:pos + n])
+    krows = qw.k_rows(kc, cap, s.NKV, s.D)
+    gk = host(krows[pos:pos + n])
     assert np.all(np.abs(gk - rk[pos:pos + n]) <= np.abs(rk[pos:pos + n]) * 2.0 ** -10 + 1e-6)
     # V is copied: bit-exact fp16 of the input
     gv = host(qw.v_rows(vc, cap, s.NKV, s.D)[pos:pos + n])
     assert np.array_equal(gv, v_h.astype(np.float16).astype(np.float32))
     # rows outside [pos, pos+n) untouched
-    assert float(kc[:pos].abs().max() if pos else 0) == 0.0
+    assert float(krows[:pos].abs().max() if pos else 0) == 0.0
+    assert float(krows[pos + n:].abs().max() if pos + n < cap else 0) == 0.0
     # fp16 prefill operand = fp16(q * log2(e)/sqrt(D))
     ref16 = rq * (qw.LOG2E / np.sqrt(s.D))
     assert np.all(np.abs(host(q16) - ref16) <= np.abs(ref16) * 2.0 ** -10 + 1e-6)
@@ -121,7 +131,7 @@ CASES_DEC = [
 def test_split_decode_parity(qw, oracle, s, pos, n, n_split):
     print(f"decode {s} pos={pos} n={n} split={n_split}", flush=True)
     rows = pos + n
-    cap = (rows + 7) // 8 * 8
+    cap = capacity(rows)
     k16, v16 = cache_rows(100 + pos, rows, s)
     r = np.random.default_rng(pos + 7)
     q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
@@ -147,7 +157,7 @@ def test_split_peaked_keys(qw, oracle):
     q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
     qg = r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32)
     ctx = make_ctx(qw, s, max_ctx=rows + 7)
-    cap = (rows + 7) // 8 * 8
+    cap = capacity(rows)
     kc, vc = gpu_caches(qw, k16, v16, cap)
     out, _ = run_split(qw, ctx, dev(q), kc, vc, cap, dev(qg), pos, n, 256)
     ref = oracle.attention(q, k16.astype(np.float32), v16.astype(np.float32), pos, qg)
@@ -164,7 +174,7 @@ def test_split_invariance(qw, n):
     s = QWEN3_NEXT
     pos = 5000
     rows = pos + n
-    cap = (rows + 7) // 8 * 8
+    cap = capacity(rows)
     k16, v16 = cache_rows(3, rows, s)
     r = np.random.default_rng(4)
     q = dev(r.standard_normal((n, s.NH, s.D)).astype(np.float32))
@@ -183,7 +193,7 @@ def test_verify_equals_sequential_decodes(qw):
     s = QWEN3_NEXT
     pos, n = 3000, 4
     rows = pos + n
-    cap = (rows + 7) // 8 * 8
+    cap = capacity(rows)
     k16, v16 = cache_rows(21, rows, s)
     r = np.random.default_rng(22)
     q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
@@ -195,6 +205,94 @@ def test_verify_equals_sequential_decodes(qw):
         one, _ = run_split(qw, ctx, dev(q[t:t + 1]), kc, vc, cap, dev(qg[t:t + 1]), pos + t, 1)
         # the single-token pass carries P's fp16 remainder, the 4-token pass rounds P to fp16 once
         assert np.abs(one[0] - together[t]).max() <= 2e-5, t
+
+
+# ---- fused decode: norm + rope + append + split attend in one launch ----------------------------------
+
+CASES_FUSED = [
+    (TINY, 128, 1, 0, "f32"),           # BASELINE config 1 through the fused path
+    (TINY, 0, 1, 0, "f32"),             # first token: the only key is the new one
+    (TINY, 45, 4, 0, "bf16"),
+    (TINY_GGUF, 300, 1, 3, "f32"),      # the reference's tiny shape, 3 splits
+    (TINY_GGUF, 30, 4, 2, "bf16"),      # new keys straddle a block and a split boundary
+    (QWEN3_NEXT, 16384, 1, 0, "f32"),
+    (QWEN3_NEXT, 16384, 1, 64, "bf16"),  # BASELINE config 2 with the reference's 64 splits
+    (QWEN3_NEXT, 32768, 4, 0, "f32"),
+    (QWEN3_NEXT, 32766, 4, 0, "f32"),   # the 4 new keys straddle a 32-key block
+    (QWEN3_NEXT, 1000, 3, 7, "bf16"),
+    (QWEN3_NEXT, 32768, 1, 0, "f32"),   # the headline shape
+]
+
+
+def _fused_setup(qw, s, pos, n, dtype, seed):
+    rows = pos + n
+    cap = capacity(rows)
+    k16, v16 = cache_rows(seed, pos, s) if pos else (np.zeros((0, s.NKV, s.D), np.float16),) * 2
+    qg, k, v, qn, kn = projections(seed + 1, n, s)
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    qg_d, k_d, v_d = dev(qg).to(tdt), dev(k).to(tdt), dev(v).to(tdt)
+    # stale rows at the new positions and NaN past the cache end must not reach the result
+    krows = torch.full((cap, s.NKV, s.D), float("nan"), dtype=torch.float16, device=DEV)
+    vrows = torch.full((cap, s.NKV, s.D), float("nan"), dtype=torch.float16, device=DEV)
+    krows[pos:rows] = 100.0
+    vrows[pos:rows] = -100.0
+    if pos:
+        krows[:pos] = dev(k16)
+        vrows[:pos] = dev(v16)
+    return cap, k16, v16, qg_d, k_d, v_d, dev(qn), dev(kn), qw.k_block(krows), qw.v_block(vrows)
+
+
+@pytest.mark.parametrize("s,pos,n,n_split,dtype", CASES_FUSED, ids=lambda v: repr(v))
+def test_fused_decode_parity(qw, oracle, s, pos, n, n_split, dtype):
+    """qwattn_decode_partial + qwattn_combine against the oracle's norm/rope/append and attention on the
+    same inputs; the appended rows land in the cache (K within one fp16 step, V bit-exact), earlier rows
+    are untouched, stale rows at the new positions and NaN past the end do not leak in."""
+    print(f"fused decode {s} pos={pos} n={n} split={n_split} {dtype}", flush=True)
+    rows = pos + n
+    cap, k16, v16, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, dtype, 400 + pos + n)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    out = torch.zeros((n, s.NH, s.D), device=DEV)
+    used = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, n_split)
+    ctx.combine(qg_d, out, n, used)
+    torch.cuda.synchronize()
+    qg_h, k_h, v_h = host(qg_d), host(k_d), host(v_d)
+    rq, rk, _ = oracle.qk_norm_rope(qg_h, k_h, v_h, 1 + host(qn_d), 1 + host(kn_d), pos, s.R, s.theta, s.eps)
+    krows, vrows = qw.k_rows(kc, cap, s.NKV, s.D), qw.v_rows(vc, cap, s.NKV, s.D)
+    gk = host(krows[pos:rows])
+    assert np.all(np.abs(gk - rk[pos:rows]) <= np.abs(rk[pos:rows]) * 2.0 ** -10 + 1e-6)
+    assert np.array_equal(host(vrows[pos:rows]), v_h.astype(np.float16).astype(np.float32))
+    if pos:
+        assert np.array_equal(host(krows[:pos]), k16.astype(np.float32))
+        assert np.array_equal(host(vrows[:pos]), v16.astype(np.float32))
+    ref = oracle.attention(rq, host(krows[:rows]), host(vrows[:rows]), pos, qg_h)
+    assert_parity(host(out), ref, f"{s} pos={pos} n={n} splits={used}")
+
+
+@pytest.mark.parametrize("s,pos,n", [(QWEN3_NEXT, 5000, 1), (QWEN3_NEXT, 4093, 4), (TINY, 77, 2)], ids=repr)
+def test_fused_equals_unfused(qw, s, pos, n):
+    """The fused launch computes what the per-dispatch entry points compute in sequence
+    (qk_norm_rope_append -> attend_partial -> combine). The fused kernel sums the RMSNorm over 32 lanes
+    per row, the standalone kernel over 64, so K rows may differ by one fp16 rounding step and the
+    outputs by fp32 rounding; V rows and the split are identical."""
+    cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 500 + pos)
+    kc2, vc2 = kc.clone(), vc.clone()
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    out = torch.zeros((n, s.NH, s.D), device=DEV)
+    used = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, 0)
+    ctx.combine(qg_d, out, n, used)
+    q = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.qk_norm_rope_append(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc2, vc2, cap, q, pos, n)
+    out2 = torch.zeros((n, s.NH, s.D), device=DEV)
+    used2 = ctx.attend_partial(q, kc2, vc2, cap, pos, n, 0)
+    ctx.combine(qg_d, out2, n, used2)
+    torch.cuda.synchronize()
+    assert used == used2
+    k1 = host(qw.k_rows(kc, cap, s.NKV, s.D)[:pos + n])
+    k2 = host(qw.k_rows(kc2, cap, s.NKV, s.D)[:pos + n])
+    assert np.array_equal(k1[:pos], k2[:pos])
+    assert np.all(np.abs(k1[pos:] - k2[pos:]) <= np.abs(k2[pos:]) * 2.0 ** -10)
+    assert torch.equal(qw.v_rows(vc, cap, s.NKV, s.D)[:pos + n], qw.v_rows(vc2, cap, s.NKV, s.D)[:pos + n])
+    assert np.abs(host(out) - host(out2)).max() <= 2e-6
 
 
 # ---- prefill -------------------------------------------------------------------------------------------
@@ -216,14 +314,12 @@ def test_prefill_parity(qw, oracle, s, pos, n):
     oracle's norm/rope/append and attention on the same values."""
     print(f"prefill {s} pos={pos} n={n}", flush=True)
     rows = pos + n
-    cap = (rows + 7) // 8 * 8
+    cap = capacity(rows)
     k16, v16 = cache_rows(40 + pos, pos, s) if pos else (np.zeros((0, s.NKV, s.D), np.float16),) * 2
     qg, k, v, qn, kn = projections(41 + n, n, s)
     qg_d, k_d, v_d = dev(qg).to(torch.bfloat16), dev(k).to(torch.bfloat16), dev(v).to(torch.bfloat16)
     ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=max(n, 1))
-    kc, vc = gpu_caches(qw, k16, v16, cap) if pos else (
-        torch.zeros((cap, s.NKV, s.D), dtype=torch.float16, device=DEV),
-        torch.zeros(cap * s.NKV * s.D, dtype=torch.float16, device=DEV))
+    kc, vc = gpu_caches(qw, k16, v16, cap) if pos else empty_caches(s, cap)
     q16 = torch.zeros((n, s.NH, s.D), dtype=torch.float16, device=DEV)
     ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, q16, pos, n)
     out = torch.zeros((n, s.NH, s.D), device=DEV)
@@ -232,7 +328,7 @@ def test_prefill_parity(qw, oracle, s, pos, n):
     out = host(out)
     # oracle on the same inputs; K/V cache rows as the GPU holds them (fp16)
     rq, _, _ = oracle.qk_norm_rope(host(qg_d), host(k_d), host(v_d), 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
-    kcache = host(kc[:rows])
+    kcache = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
     vcache = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
     qg_h = host(qg_d)
     # all tokens when small, else a spread of tokens including the first and the last
@@ -248,7 +344,7 @@ def test_prefill_equals_decodes(qw):
     s = QWEN3_NEXT
     pos, n = 200, 70
     rows = pos + n
-    cap = (rows + 7) // 8 * 8
+    cap = capacity(rows)
     k16, v16 = cache_rows(51, rows, s)
     r = np.random.default_rng(52)
     q = r.standard_normal((n, s.NH, s.D)).astype(np.float32)
@@ -330,8 +426,7 @@ def test_rollback_is_position_reset(qw, oracle):
 def test_errors_are_status_codes(qw):
     s = QWEN3_NEXT
     ctx = make_ctx(qw, s, max_ctx=1024, max_tokens=64)
-    kc = torch.zeros((1024, s.NKV, s.D), dtype=torch.float16, device=DEV)
-    vc = torch.zeros(1024 * s.NKV * s.D, dtype=torch.float16, device=DEV)
+    kc, vc = empty_caches(s, 1024)
     q = torch.zeros((8, s.NH, s.D), device=DEV)
     with pytest.raises(qw.QwattnError, match="context overflow") as e:
         ctx.attend_partial(q, kc, vc, 1024, 1024, 1)
@@ -340,7 +435,9 @@ def test_errors_are_status_codes(qw):
         ctx.attend_partial(q, kc, vc, 1024, 10, 8)
     with pytest.raises(qw.QwattnError, match="slot"):
         ctx.layer_attention(0, q, q, q, q, q, q, 0, 1)
-    with pytest.raises(qw.QwattnError, match="not a multiple of 8"):
-        ctx.attend_partial(q, kc, vc, 1020, 0, 1)
+    with pytest.raises(qw.QwattnError, match="not a multiple of 32"):
+        ctx.attend_partial(q, kc, vc, 1000, 0, 1)
+    with pytest.raises(qw.QwattnError, match="fused decode"):
+        ctx.decode_partial(q, q, q, q, q, ctx.rope_table(), kc, vc, 1024, 10, 9)
     with pytest.raises(qw.QwattnError):
         qw.Attention(16, 3, 256, 64)
