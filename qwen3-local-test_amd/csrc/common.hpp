@@ -3,9 +3,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -86,7 +90,22 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// 1 / (1 + e^-x) with the hardware exponential and reciprocal (about 1 ulp each); saturates to 0 for
+// x below about -88 (e^-x overflows, its reciprocal is 0) and to 1 above
+__device__ __forceinline__ float sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1, each body a separate
+// instantiation, so indices into register arrays stay static whatever the body size (flat expansion).
+template <int B, typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, B + I>{}), ...);
+}
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq<B>(f, std::make_integer_sequence<int, E - B>{});
+}
 
 // ---- K/V cache layout ------------------------------------------------------------------------------
 // Both caches are [cap/32][NKV][32*D] fp16: blocks of 32 positions, one 32*D part per KV head. Inside a
