@@ -179,13 +179,16 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         load_vec<IN_DT, DPL2>(a.vnew, src + d0, nv);
     }
 
-    // ---- first two tiles in flight (kept after the row loads and before their use) ----------------
+    // ---- first tile in flight (kept after the row loads and before their use); the second follows the
+    // passes. Load completion is counted in order with a 6-bit counter: the passes wait for their own
+    // loads by allowing the younger tile loads to stay outstanding, which works while those number at
+    // most 63. And with HBM saturated, issuing a load stalls the wave until earlier requests drain, so
+    // nothing the passes could do should wait behind a long burst of tile loads.
     f16x8 kA[NKS][2], kB[NKS][2], vA[NDT], vB[NDT];
+    static_assert(2 * NKS + NDT <= 63, "row-pass wait must fit the load counter");
     __builtin_amdgcn_sched_barrier(0);
     load_k(kA, wave);
     load_v(vA, wave);
-    load_k(kB, wave + 4);
-    load_v(vB, wave + 4);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- finish the passes: query fp16 hi/lo fragments -> LDS; new rows -> block images and caches --
@@ -239,6 +242,10 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             }
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(kB, wave + 4);
+    load_v(vB, wave + 4);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
     // ---- per column: query row, causal key limit inside this chunk, softmax state ----------------
@@ -361,24 +368,29 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             for (int u = 0; u < NPT; u++) acc[dt] = mfma16(vt[dt], pop[u], acc[dt]);
     };
 
-    // ---- main loop: two register buffers, tiles wave, wave + 4, ...; loads always issued ----------
+    // ---- main loop: two register buffers, tiles wave, wave + 4, ...; a buffer's next loads go out
+    // once its whole tile is computed, so a wave stalled on issuing them never holds data it could use
+    // (past the last cached block the loads read zeros without traffic) --------------------------------
     for (int i = 0; i < ntile; i += 2) {
         {
             const int t = wave + 4 * i, tb = kb + 32 * t;
             f32x4 sc[2];
             scores(kA, tb, sc);
-            load_k(kA, t + 8);
             softmax_pv(vA, tb, sc);
-            load_v(vA, t + 8);
+            if (i + 2 < ntile) {
+                load_k(kA, t + 8);
+                load_v(vA, t + 8);
+            }
         }
-        {
+        if (i + 1 < ntile) {
             const int t = wave + 4 * (i + 1), tb = kb + 32 * t;
             f32x4 sc[2];
-            const bool live = i + 1 < ntile;
-            if (live) scores(kB, tb, sc);
-            load_k(kB, t + 8);
-            if (live) softmax_pv(vB, tb, sc);
-            load_v(vB, t + 8);
+            scores(kB, tb, sc);
+            softmax_pv(vB, tb, sc);
+            if (i + 3 < ntile) {
+                load_k(kB, t + 8);
+                load_v(vB, t + 8);
+            }
         }
     }
 
