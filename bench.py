@@ -14,9 +14,10 @@ already resident in HBM when the timed region starts.
 
 The same JSON line carries the other BASELINE configurations (16K decode with the reference's 64
 splits, the 4-token MTP verify at 32K, 256K decode with 1% of keys x8, and the 2,048-token causal
-prefill on 2,048 cached tokens in TFLOP/s), the roofline of the dominant kernel (per-launch HIP-event
-durations on the stream the kernels run on), and the CPU baseline: the reference's CPU attention
-timed on this host's cores over a bounded sample.
+prefill on 2,048 cached tokens in TFLOP/s), the roofline of the dominant kernel (its mean launch
+duration from HIP events around batches of 16 back-to-back launches on the stream the kernels run on;
+HBM traffic per launch from the committed rocprofv3 PMC summary in profiles/), and the CPU baseline:
+the reference's CPU attention timed on this host's cores over a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -116,6 +117,17 @@ class Workload:
             a.attend_prefill(self.q, kc, vc, cap, self.qg, self.out, self.pos, self.n)
         ev[2].record()
 
+    def main_only(self, slot):
+        """The dominant kernel alone (it is idempotent: the fused decode rewrites the same new rows, the
+        prefill reads the queries the last norm dispatch left)."""
+        a = self.att
+        kc, vc, cap = self.slot_views[slot]
+        if self.split:
+            a.decode_partial(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.pos, self.n,
+                             self.n_split)
+        else:
+            a.attend_prefill(self.q, kc, vc, cap, self.qg, self.out, self.pos, self.n)
+
     def close(self):
         self.slot_views = []
         self.att.close()
@@ -200,15 +212,43 @@ def run_workload(wl, steps, warmup, graph):
     k_all = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
     if not bool(torch.isfinite(wl.out).all()):
         raise RuntimeError(f"{wl.name}: non-finite attention output")
-    r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all)}
+    # the dominant kernel's launch duration: batches of 16 back-to-back launches between two events on
+    # the library's stream, queued behind a GPU sleep (an event between every two launches would add its
+    # own cost to each figure); the mean per launch includes the in-stream gap between launches
+    per_launch = []
+    for b in range(max(2, steps // 16)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gpu_sleep(2.0)
+        e0.record()
+        for i in range(16):
+            wl.main_only((b * 16 + i) % wl.slots)
+        e1.record()
+        torch.cuda.synchronize()
+        per_launch.append(e0.elapsed_time(e1) * 1e3 / 16)
+    r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all),
+         "us_main": statistics.mean(per_launch), "us_main_batches": len(per_launch)}
     if wl.split:
-        r.update({"kernel": "k_decode (fused norm+rope+append+split attend)", "us_main": statistics.mean(k_first),
-                  "us_main_median": statistics.median(k_first), "us_combine": statistics.mean(k_second),
-                  "splits": wl.used})
+        r.update({"kernel": "k_decode (fused norm+rope+append+split attend)", "us_main_each_event": statistics.mean(k_first),
+                  "us_combine": statistics.mean(k_second), "splits": wl.used})
     else:
-        r.update({"kernel": "k_prefill", "us_norm_rope": statistics.mean(k_first), "us_main": statistics.mean(k_second),
-                  "us_main_median": statistics.median(k_second)})
+        r.update({"kernel": "k_prefill", "us_norm_rope": statistics.mean(k_first),
+                  "us_main_each_event": statistics.mean(k_second)})
     return r
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_decode_decode_32k_k_prefill_prefill_2k_hbm_traffic.md")
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE, scaled by a plain copy of known size), or None when the summary does not hold it."""
+    import re
+    try:
+        txt = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(rf"^traffic_bytes_per_launch {re.escape(kernel)} {re.escape(workload)}: (\d+)$", txt, re.M)
+    return int(m.group(1)) if m else None
 
 
 def cpu_info():
@@ -275,6 +315,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", default="", help="comma-separated subset of workloads (for profiling)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 16 plain device copies of MIB MiB (the reference kernel for scaling PMC "
+                         "FETCH_SIZE / WRITE_SIZE readings to bytes), then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -285,6 +328,15 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(16):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 16}))
+        return
     qw = load_package()
     qw.load_library()
     graph = not args.no_graph
@@ -358,14 +410,18 @@ def main():
         line["roofline"] = {"bound": "hbm", "kernel": "k_decode<256,0,1,0> (fused decode, grid 128x2)",
                             "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                            "frac": round(head["frac_hbm_kernel"], 4), "traffic": None,
+                            "frac": round(head["frac_hbm_kernel"], 4),
+                            "traffic": measured_traffic("k_decode", "decode_32k"),
+                            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
                             "kernel_us": head["us_main"]}
     pf = results.get("prefill_2k_on_2k")
     if pf:
         line["prefill_roofline"] = {"bound": "mfma", "kernel": "k_prefill<256,f16,bf16>",
                                     "achieved": round(pf["algorithmic_flops"] / (pf["us_main"] * 1e-6) / 1e12, 2),
                                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                                    "frac": round(pf["frac_mfma_kernel"], 4), "traffic": None,
+                                    "frac": round(pf["frac_mfma_kernel"], 4),
+                                    "traffic": measured_traffic("k_prefill", "prefill_2k_on_2k"),
+                                    "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
                                     "kernel_us": pf["us_main"]}
     print(json.dumps(line), flush=True)
 
