@@ -15,10 +15,16 @@
 //    the second read of the chunk is served by the 256 MB Infinity Cache, and each slice keeps the
 //    register budget that lets it double-buffer its tiles.
 //  - The cache's blocked layout (common.hpp) makes every MFMA operand fragment one contiguous kilobyte,
-//    so a wave streams a 32-key tile (K and V, 32 KB at D = 256) with 32 fully coalesced 16-byte-per-lane
-//    loads straight into the operand registers — no LDS staging. Each wave keeps two tiles in flight
-//    (register double buffering): the next-but-one tile's K loads go out as soon as the current tile's
-//    scores are done, its V loads as soon as P.V is done.
+//    so a 32-key tile (K and V, 32 KB at D = 256) moves with 32 fully coalesced 16-byte-per-lane loads.
+//  - Up to 8 rows (k_decode_ld: single-token decode, n * G <= 8): two loader waves copy tiles straight
+//    into LDS (buffer_load ... lds) through a two-slot ring per compute wave and publish each landed tile
+//    through an LDS counter; two compute waves take a tile into registers, free its slot at once and
+//    compute on it, so each compute wave sees up to two tiles in flight with no register cost. The
+//    copies start at launch, right after the compute waves have issued their row loads, so the prologue
+//    (norm, RoPE, cache append) runs under the first tiles' latency.
+//  - More rows (k_decode, 16-row slices): each wave streams its tiles straight into the operand
+//    registers, two tiles in flight (register double buffering): the next-but-one tile's K loads go out
+//    as soon as the current tile's scores are done, its V loads as soon as P.V is done.
 //  - S^T[32 keys x rows] = K . Q^T and O^T[D x rows] += V^T . P^T on v_mfma_f32_16x16x32_f16 with fp32
 //    accumulation. Q and P are carried as an fp16 "hi" part plus an fp16 "lo" remainder (22 mantissa
 //    bits together), so scores and weights keep fp32-level accuracy against the fp16 cache; with at most
@@ -27,10 +33,12 @@
 //  - Fused form: every workgroup normalizes and rotates its own query rows (RMSNorm (1+w) + partial
 //    RoPE, while its first tiles are in flight), and the workgroup whose chunk holds the n new positions
 //    normalizes/rotates their K rows, writes K and V to the cache for later steps, and patches them into
-//    its loaded tile registers — so one launch does the work of the reference's qk_norm_rope + attention
+//    its loaded tiles — so one launch does the work of the reference's qk_norm_rope + attention
 //    dispatches.
 //  - The combine runs one workgroup per (row, 64-dim slice) with every partial load of a batch issued
 //    before any is used.
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -450,11 +458,437 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     }
 }
 
+// s_waitcnt immediate for "at most n vector-memory loads outstanding" (gfx9 encoding: vmcnt split over
+// bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// ---- decode with producer waves (at most 8 query rows) -------------------------------------------
+// With HBM saturated, issuing a load stalls the issuing wave until earlier requests drain, so a wave that
+// both streams and computes spends most of the stream blocked with data it could be using. Here the
+// workgroup's waves 0-1 only compute and waves 2-3 only stream: loader wave 2 + p copies compute wave
+// p's tiles (tiles p, p + 2, ...) with direct-to-LDS loads into two 32-key slots, patches the new
+// positions (fresh K/V rows, zero V past the last position) into the slot that holds them, and publishes
+// each tile through an LDS counter; the compute wave copies the slot into registers, frees it at once and
+// computes, so two tiles per pair are in flight while one is being computed. Spin waits are bounded, so
+// every wave exits even if a counter were never reached.
+template <int D, int FUSED, int IN_DT>
+__global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
+    constexpr int NKS = D / 32, NDT = D / 16, RMAX = 8, BLKE = kBlk * D;
+    constexpr int DPL2 = D / 32;            // dims per lane in the row passes
+    constexpr int NCW = 2;                  // compute waves (the other two load)
+    constexpr int QPASS = RMAX / (2 * NCW);  // query-row passes per compute wave, two rows per pass
+    constexpr int NPASS = RMAX / (2 * NCW);  // new-row passes (at most 8 new rows per workgroup)
+    constexpr float TAU = 8.f;
+    constexpr int TILE_E = 2 * BLKE;        // a slot: the K part then the V part of one block
+    constexpr int PIECES = BLKE * 2 / 1024;  // 1 KB direct loads per part
+    constexpr int OSTRIDE = D + 4;
+    constexpr int SPIN_MAX = 1 << 22;
+    static_assert(2 * PIECES <= 63, "one tile's loads must fit the load counter");
+
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    f16* ring = reinterpret_cast<f16*>(smem);                 // [NCW][2][TILE_E]
+    f16* s_q = ring + NCW * 2 * TILE_E;                        // Q fragments (hi rows 0-7, lo rows 8-15)
+    f16* s_new = s_q + NKS * 64 * 8;                           // new rows: [K, V][8][D]
+    // tile counters in a separate LDS object: an access the compiler cannot tell apart from the
+    // direct-to-LDS copies' destination makes it wait for every outstanding copy first
+    __shared__ int s_cnt[2 * NCW];
+    int* ready = s_cnt;        // [NCW] tiles published per pair
+    int* freed = s_cnt + NCW;  // [NCW] tiles released per pair
+    __shared__ float sM[NCW][RMAX], sL[NCW][RMAX], sF[NCW][RMAX];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int z = blockIdx.x, kvh = blockIdx.y;
+    const int G = a.NH / a.NKV;
+    const int rows = min(RMAX, a.n * G);
+    const int maxlen = a.pos + a.n;
+    const int kb = z * a.chunk;
+    const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, kb + a.chunk);
+    const int ntile_wg = (ke - kb + 31) >> 5;
+    const bool loader = wave >= NCW;
+    const int pr = loader ? wave - NCW : wave;                        // pair
+    const int ntp = ntile_wg > pr ? (ntile_wg - pr + NCW - 1) / NCW : 0;  // tiles pr, pr + NCW, ...
+    const int new_lo = FUSED ? a.pos : maxlen;                        // first position not read from the cache
+    if (tid < 2 * NCW) ready[tid] = 0;  // ready[] and freed[] (published by the barrier below)
+
+    // ---- loaders: the first two tiles of the pair go out at once ---------------------------------
+    const int load_end = min(ke, new_lo);
+    const int nload = load_end > kb ? ((load_end - 1) >> 5) - (kb >> 5) + 1 : 0;
+    const int bstride = a.NKV * BLKE * 2;  // bytes between consecutive blocks of one head
+    const size_t part0 = ((size_t)(kb >> 5) * a.NKV + kvh) * BLKE;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.kc) + part0, (short)0, nload * bstride, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.vc) + part0, (short)0, nload * bstride, 0x00020000);
+    auto slot = [&](int i) { return ring + (pr * 2 + (i & 1)) * TILE_E; };
+    auto dma = [&](int i) {  // tile pr + NCW*i into slot i & 1 (range-checked: past nload, zeros)
+        f16* dst = slot(i);
+        const int off = (pr + NCW * i) * bstride + lane * 16;
+#pragma unroll
+        for (int j = 0; j < PIECES; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(dst + j * 512), 16,
+                                                     off + j * 1024, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < PIECES; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(dst + BLKE + j * 512),
+                                                     16, off + j * 1024, 0, 0, 0);
+    };
+    // ---- compute waves: query rows (and, fused, the new K/V rows) normalized and rotated ------------
+    // Two rows per compute wave per pass, 32 lanes per row, DPL2 dims per lane.
+    const int hw = lane >> 5, hl = lane & 31, d0 = hl * DPL2;
+    const int t_lo = FUSED ? max(a.pos, kb) - a.pos : 0;
+    const int t_hi = FUSED ? max(t_lo, min(maxlen, ke) - a.pos) : 0;
+    const int half_r = a.R >> 1;
+    const bool rot = FUSED && d0 < a.R;  // lanes whose DPL2 dims are rotated (R/2 is a multiple of DPL2)
+    auto issue_row = [&](float (&x)[DPL2], float (&cv)[2 * DPL2], const void* src, size_t off, int p, bool valid) {
+        load_vec<FUSED ? IN_DT : 0, DPL2>(src, (valid ? off : 0) + d0, x);
+        if constexpr (FUSED) {
+            const int i0 = rot ? (d0 < half_r ? d0 : d0 - half_r) : 0;
+            load_vec<0, 2 * DPL2>(a.rope, (size_t)(valid && rot ? p : 0) * a.R + 2 * i0, cv);
+        }
+    };
+    // y = x * rsqrt(mean(x^2) + eps) * (1 + w), then rotate-half on d < R (the partner dim d +- R/2 sits
+    // (R/2)/DPL2 lanes away in the same half-wave)
+    auto finish_row = [&](const float (&xr)[DPL2], const float (&cv)[2 * DPL2], bool valid, const float (&w)[DPL2],
+                          float (&y)[DPL2]) {
+        float x[DPL2];
+        float ss = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            x[jj] = valid ? xr[jj] : 0.f;
+            ss += x[jj] * x[jj];
+        }
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) y[jj] = x[jj] * r * (1.0f + w[jj]);
+        const int offl = half_r / DPL2;
+        const bool lo_half = d0 < half_r;
+        const int src_lane = rot ? (lo_half ? lane + offl : lane - offl) : lane;
+        float partner[DPL2];
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) partner[jj] = __shfl(y[jj], src_lane, 64);
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            const float cs = rot ? cv[2 * jj] : 1.f, sn = rot ? cv[2 * jj + 1] : 0.f;
+            y[jj] = lo_half ? y[jj] * cs - partner[jj] * sn : y[jj] * cs + partner[jj] * sn;
+        }
+    };
+    if (!loader) {
+        float wq[DPL2], wk[DPL2];
+        float qx[QPASS][DPL2], qcv[QPASS][2 * DPL2];
+        float nx[NPASS][DPL2], ncv[NPASS][2 * DPL2], nv[NPASS][DPL2];
+        if constexpr (FUSED) {
+            load_vec<0, DPL2>(a.qn, d0, wq);
+            load_vec<0, DPL2>(a.kn, d0, wk);
+        }
+#pragma unroll
+        for (int ps = 0; ps < QPASS; ps++) {
+            const int r = ps * 2 * NCW + wave * 2 + hw;
+            const bool valid = r < rows;
+            const int t = valid ? r / G : 0, h = kvh * G + (valid ? r % G : 0);
+            if constexpr (FUSED) issue_row(qx[ps], qcv[ps], a.q, ((size_t)t * a.NH + h) * 2 * D, a.pos + t, valid);
+            else issue_row(qx[ps], qcv[ps], a.q, ((size_t)t * a.NH + h) * D, 0, valid);
+        }
+        if constexpr (FUSED) {
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ps++) {
+                const int tn = t_lo + ps * 2 * NCW + wave * 2 + hw;
+                const bool has = tn < t_hi;
+                const size_t src = ((size_t)(has ? tn : 0) * a.NKV + kvh) * D;
+                issue_row(nx[ps], ncv[ps], a.knew, src, a.pos + (has ? tn : 0), has);
+                load_vec<IN_DT, DPL2>(a.vnew, src + d0, nv[ps]);
+            }
+        }
+        // the rows' loads are out: let the loaders start (a bare barrier, no wait on these loads)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int ps = 0; ps < QPASS; ps++) {
+            const int r = ps * 2 * NCW + wave * 2 + hw;
+            float y[DPL2];
+            if constexpr (FUSED) {
+                finish_row(qx[ps], qcv[ps], r < rows, wq, y);
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < DPL2; jj++) y[jj] = r < rows ? qx[ps][jj] : 0.f;
+            }
+            // fp16 hi part in column r, lo remainder in column r + 8 of the Q^T fragments
+            typedef f16 f16v __attribute__((ext_vector_type(DPL2)));
+            f16v hv, lv;
+#pragma unroll
+            for (int jj = 0; jj < DPL2; jj++) {
+                const float ys = y[jj] * a.q_scale;
+                const f16 hi = (f16)ys;
+                hv[jj] = hi;
+                lv[jj] = (f16)(ys - (float)hi);
+            }
+            const int kk = d0 >> 5, L = ((d0 >> 3) & 3) * 16 + r, e = d0 & 7;
+            *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L) * 8 + e]) = hv;
+            *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L + 8) * 8 + e]) = lv;
+        }
+        if constexpr (FUSED) {
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ps++) {
+                const int tn = t_lo + ps * 2 * NCW + wave * 2 + hw;
+                float y[DPL2];
+                finish_row(nx[ps], ncv[ps], tn < t_hi, wk, y);
+                if (tn < t_hi) {
+                    const int p = a.pos + tn;
+                    const size_t part = kv_part(p, kvh, a.NKV, D);
+                    f16* kw = reinterpret_cast<f16*>(a.kc) + part;
+                    f16* vw = reinterpret_cast<f16*>(a.vc) + part;
+                    const int pb = p & (kBlk - 1), nr = p - new_lo;  // new_lo = pos: row index of the new rows
+#pragma unroll
+                    for (int jj = 0; jj < DPL2; jj++) {
+                        const int d = d0 + jj;
+                        const f16 kh = (f16)y[jj];
+                        const f16 vh = (f16)nv[ps][jj];
+                        s_new[nr * D + d] = kh;
+                        s_new[(8 + nr) * D + d] = vh;
+                        kw[k_off(pb, d)] = kh;
+                        vw[v_off(pb, d)] = vh;
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): s_q, s_new and the counters are in LDS
+    } else {
+        // wait until the compute waves' row loads are issued, then put the first two tiles in flight
+        // behind them: issued any earlier, the copies would queue the row loads behind the whole stream
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        if (ntp > 0) dma(0);
+        if (ntp > 1) dma(1);
+    }
+    // a bare barrier: the LDS writes above are complete (the compute waves waited for them), and a
+    // fenced one would also wait for the copies in flight and the cache-row stores
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x4 acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (loader) {
+        // ---- stream the pair's tiles; publish each once landed (and patched) -----------------------
+        for (int i = 0; i < ntp; i++) {
+            if (i + 1 < ntp) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PIECES));  // tile i landed, i+1 may not
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            const int tb = kb + 32 * (pr + NCW * i);
+            if (tb + 32 > new_lo) {
+                // keys from new_lo on: the new rows (fused) where they exist, else V = 0 over whatever the
+                // copy brought (stale or unwritten cache memory never reaches the sums; K needs no
+                // clearing there, those scores are masked).
+                f16* sl = slot(i);
+                const int k_from = max(new_lo - tb, 0);               // first patched key of the block
+                const int k_new_end = FUSED ? min(maxlen - tb, 32) : k_from;  // new keys: [k_from, k_new_end)
+                const int n_new = k_new_end - k_from;
+                // K of the new keys: (key, 8-dim group) pieces of 16 bytes, row layout -> block layout
+                for (int idx = lane; idx < n_new * (D / 8); idx += 64) {
+                    const int key = k_from + idx / (D / 8), d8 = (idx % (D / 8)) * 8;
+                    *reinterpret_cast<f16x8*>(&sl[k_off(key, d8)]) =
+                        *reinterpret_cast<const f16x8*>(&s_new[(tb + key - new_lo) * D + d8]);
+                }
+                // V: zeros over keys [k_from, 32) (whole 8-key groups as 16-byte stores, the partial group
+                // key by key), then the new keys' values; one wave's LDS stores land in issue order. Plain
+                // loops on purpose: this runs once per launch, and unrolled select code would be fetched
+                // cold into the instruction cache at several microseconds.
+                const int g_from = k_from >> 3;
+#pragma nounroll
+                for (int d = lane; d < D; d += 64) {
+#pragma nounroll
+                    for (int key = k_from; key < (g_from + 1) * 8 && key < 32; key++) sl[BLKE + v_off(key, d)] = (f16)0.f;
+#pragma nounroll
+                    for (int gg = g_from + 1; gg < 4; gg++) *reinterpret_cast<f16x8*>(&sl[BLKE + v_off(gg * 8, d)]) = f16x8{};
+#pragma nounroll
+                    for (int key = k_from; key < k_new_end; key++)
+                        sl[BLKE + v_off(key, d)] = s_new[(8 + tb + key - new_lo) * D + d];
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the patch is in LDS
+            }
+            // publish: the waits above already order the tile before the counter, and a release store
+            // would also wait for the next tile's loads (the whole load counter), halving the pipeline
+            {
+                // an LDS store the compiler can see would wait for the next tile's loads too (it cannot
+                // tell the counter from the copies' destination); the waits above already order it
+                const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&ready[pr]));
+                asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(i + 1) : "memory");
+            }
+            if (i + 2 < ntp) {
+                // wait for the compute wave to free the slot; read through inline assembly as well, since
+                // an LDS read the compiler can see would first wait for all of this wave's copies
+                const uint32_t faddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&freed[pr]));
+                for (int spin = 0; spin < SPIN_MAX; spin++) {
+                    int f;
+                    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(f) : "v"(faddr) : "memory");
+                    if (__builtin_amdgcn_readfirstlane(f) >= i + 1) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                dma(i + 2);
+            }
+        }
+    } else {
+        // ---- compute the pair's tiles from the slots ----------------------------------------------
+        const int rcol = c & 7;
+        const int lim = rcol < rows ? min(a.pos + rcol / G + 1, ke) : 0;
+        f16x8 qreg[NKS];
+#pragma unroll
+        for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
+        for (int i = 0; i < ntp; i++) {
+            for (int spin = 0; __hip_atomic_load(&ready[pr], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1 &&
+                               spin < SPIN_MAX;
+                 spin++)
+                __builtin_amdgcn_s_sleep(1);
+            const f16* sl = slot(i);
+            f16x8 kt[NKS][2], vt[NDT];
+#pragma unroll
+            for (int kk = 0; kk < NKS; kk++)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) kt[kk][s2] = *reinterpret_cast<const f16x8*>(sl + ((kk * 2 + s2) * 64 + lane) * 8);
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) vt[dt] = *reinterpret_cast<const f16x8*>(sl + BLKE + (dt * 64 + lane) * 8);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile is in registers, the slot is free
+            asm volatile("" ::: "memory");
+            __hip_atomic_store(&freed[pr], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+
+            const int tb = kb + 32 * (pr + NCW * i);
+            // scores: sc[s][i] is key tb + 8g + 4s + i of column c (fp16 hi in columns 0-7, lo in 8-15)
+            f32x4 sc[2];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < NKS; kk++) x = mfma16(kt[kk][s2], qreg[kk], x);
+                sc[s2] = x;
+            }
+            float sv[8];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float v = sc[s2][e] + xor8(sc[s2][e]);
+                    sv[s2 * 4 + e] = tb + 8 * g + 4 * s2 + e < lim ? v : kNegInf;
+                }
+            float mx = sv[0];
+#pragma unroll
+            for (int k = 1; k < 8; k++) mx = fmaxf(mx, sv[k]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            // lazy rescale (see k_decode)
+            if (m_run == kNegInf) m_run = mx;
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + TAU) != 0) {
+                const float m_new = fmaxf(m_run, mx);
+                const float corr = exp2_fast(m_run - m_new);
+                m_run = m_new;
+                l_run *= corr;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) acc[dt] *= corr;
+            }
+            const float m_use = m_run == kNegInf ? 0.f : m_run;
+            float psum = 0.f;
+            f16x8 pop;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float pk = exp2_fast(sv[k] - m_use);
+                psum += pk;
+                const f16 ph = (f16)pk;
+                pop[k] = c >= 8 ? (f16)(pk - (float)ph) : ph;
+            }
+            l_run += psum;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) acc[dt] = mfma16(vt[dt], pop, acc[dt]);
+        }
+    }
+
+    // ---- merge the compute waves (the ring is dead once every wave is here) ---------------------
+    __syncthreads();
+    float* sO = reinterpret_cast<float*>(ring);
+    if (!loader) {
+        float l = l_run;
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[dt][e] += xor8(acc[dt][e]);
+        if (c < 8) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                *reinterpret_cast<f32x4*>(&sO[(wave * RMAX + c) * OSTRIDE + dt * 16 + g * 4]) = acc[dt];
+            if (g == 0) {
+                sM[wave][c] = m_run;
+                sL[wave][c] = l;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < rows) {
+        const int r = tid;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < NCW; w++)
+            if (sL[w][r] > 0.f) M = fmaxf(M, sM[w][r]);
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NCW; w++) {
+            const float f = sL[w][r] > 0.f ? exp2_fast(sM[w][r] - M) : 0.f;
+            sF[w][r] = f;
+            L += sL[w][r] * f;
+        }
+        const int t = r / G, h = kvh * G + r % G;
+        const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
+        a.part_ml[row * 2] = M;
+        a.part_ml[row * 2 + 1] = L;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < rows * (D / 4); idx += 256) {
+        const int r = idx / (D / 4), d = (idx % (D / 4)) * 4;
+        f32x4 o = *reinterpret_cast<const f32x4*>(&sO[r * OSTRIDE + d]) * sF[0][r];
+#pragma unroll
+        for (int w = 1; w < NCW; w++) o += *reinterpret_cast<const f32x4*>(&sO[(w * RMAX + r) * OSTRIDE + d]) * sF[w][r];
+        const int t = r / G, h = kvh * G + r % G;
+        const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
+        *reinterpret_cast<f32x4*>(&a.part_o[row * D + d]) = o;
+    }
+}
+
+template <int D>
+constexpr size_t decode_ld_lds() {
+    return (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2 + (size_t)2 * 8 * D * 2;
+}
+
 template <int D, int FUSED, int IN_DT>
 static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
     const dim3 block(256);
-    if (rows <= 8) hipLaunchKernelGGL((k_decode<D, 0, FUSED, IN_DT>), dim3(a.n_split, a.NKV, 1), block, 0, s, a);
+    if (rows <= 8) {
+        auto kern = k_decode_ld<D, FUSED, IN_DT>;
+        const size_t shm = decode_ld_lds<D>();
+        // the dynamic-LDS limit is a per-device attribute of the function: raise it once per device
+        static std::atomic<uint64_t> raised{0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        const uint64_t bit = 1ull << (dev & 63);
+        if (!(raised.load(std::memory_order_acquire) & bit)) {
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+            if (e != hipSuccess) return e;
+            raised.fetch_or(bit, std::memory_order_acq_rel);
+        }
+        hipLaunchKernelGGL(kern, dim3(a.n_split, a.NKV, 1), block, shm, s, a);
+    }
     else hipLaunchKernelGGL((k_decode<D, 1, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), block, 0, s, a);
     return hipGetLastError();
 }
