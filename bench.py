@@ -90,6 +90,7 @@ class Workload:
         self.qn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.kn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.split = n * (NH // NKV) <= 32 and n <= 8
+        self.one_launch = n * (NH // NKV) <= 8  # decode: the combine runs inside the attend launch
         self.q = None if self.split else torch.zeros((n, NH, D), device="cuda", dtype=torch.float16)
         self.out = torch.zeros((n, NH, D), device="cuda")
         self.rope = self.att.rope_table()
@@ -105,7 +106,11 @@ class Workload:
         a = self.att
         kc, vc, cap = self.slot_views[slot]
         ev[0].record()
-        if self.split:
+        if self.one_launch:
+            self.used = a.decode(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.out, self.pos,
+                                 self.n, self.n_split)
+            ev[1].record()
+        elif self.split:
             self.used = a.decode_partial(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.pos,
                                          self.n, self.n_split)
             ev[1].record()
@@ -122,7 +127,10 @@ class Workload:
         prefill reads the queries the last norm dispatch left)."""
         a = self.att
         kc, vc, cap = self.slot_views[slot]
-        if self.split:
+        if self.one_launch:
+            a.decode(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.out, self.pos, self.n,
+                     self.n_split)
+        elif self.split:
             a.decode_partial(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.pos, self.n,
                              self.n_split)
         else:
@@ -228,8 +236,13 @@ def run_workload(wl, steps, warmup, graph):
     r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all),
          "us_main": statistics.mean(per_launch), "us_main_batches": len(per_launch)}
     if wl.split:
-        r.update({"kernel": "k_decode (fused norm+rope+append+split attend)", "us_main_each_event": statistics.mean(k_first),
-                  "us_combine": statistics.mean(k_second), "splits": wl.used})
+        if wl.one_launch:
+            r.update({"kernel": "k_decode_ld (fused norm+rope+append+split attend+combine, one launch)",
+                      "us_main_each_event": statistics.mean(k_first), "splits": wl.used})
+        else:
+            r.update({"kernel": "k_decode (fused norm+rope+append+split attend)",
+                      "us_main_each_event": statistics.mean(k_first), "us_combine": statistics.mean(k_second),
+                      "splits": wl.used})
     else:
         r.update({"kernel": "k_prefill", "us_norm_rope": statistics.mean(k_first),
                   "us_main_each_event": statistics.mean(k_second)})
@@ -407,7 +420,7 @@ def main():
         "workloads": results,
     }
     if head:
-        line["roofline"] = {"bound": "hbm", "kernel": "k_decode<256,0,1,0> (fused decode, grid 128x2)",
+        line["roofline"] = {"bound": "hbm", "kernel": "k_decode_ld<256,1,0> (one-launch decode, grid 128x2)",
                             "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                             "frac": round(head["frac_hbm_kernel"], 4),

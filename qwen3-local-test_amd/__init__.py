@@ -61,6 +61,7 @@ def load_library():
         "qwattn_qk_norm_rope_append": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I],
         "qwattn_attend_partial": [_P, _P, _P, _P, _P, _I, _I, _I, _I, ctypes.POINTER(_I)],
         "qwattn_decode_partial": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, ctypes.POINTER(_I)],
+        "qwattn_decode": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, ctypes.POINTER(_I)],
         "qwattn_combine": [_P, _P, _P, _I, _P, _I, _I],
         "qwattn_attend_prefill": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
@@ -201,6 +202,15 @@ class Attention:
         self._check(self.lib.qwattn_decode_partial(
             self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
             _ptr(kcache), _ptr(vcache), kv_cap, pos, n, n_split, ctypes.byref(used)))
+        return used.value
+
+    def decode(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, n_split=0, stream=None):
+        """Norm + rope + append + split-KV attend + combine and gate in one launch (n * NH/NKV <= 8);
+        returns the split count."""
+        used = ctypes.c_int()
+        self._check(self.lib.qwattn_decode(
+            self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
+            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n, n_split, ctypes.byref(used)))
         return used.value
 
     def combine(self, qg, out, n, n_split, stream=None):

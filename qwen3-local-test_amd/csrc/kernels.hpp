@@ -39,6 +39,9 @@ struct DecodeArgs {
     float* part_ml;       // [n*NH][n_split][2]: running max (log2 units), sum
     int pos, n, NH, NKV, R, chunk, n_split;
     float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
+    float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
+                          // the same launch (nullptr: partials only, for a separate combine)
+    int* arrive;          // with out: [NKV] arrival counters, zero before the launch and again after it
 };
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 

@@ -25,6 +25,7 @@ struct qwattn_ctx {
     float* rope = nullptr;       // [max_ctx][R/2][2]
     float* part_o = nullptr;     // [split_rows][max_splits][D]
     float* part_ml = nullptr;    // [split_rows][max_splits][2]
+    int* arrive = nullptr;       // [NKV] arrival counters of qwattn_decode (zero between launches)
     float* q32 = nullptr;        // [max_tokens][NH][D] layer-path query (fp32)
     void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
@@ -163,11 +164,16 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     // + 64 floats: the decode kernel's lanes outside the rotated dims read (and discard) the table start
     const size_t rope_n = (size_t)cfg->max_ctx * std::max(1, R / 2) * 2 + 64;
     const size_t part = (size_t)c->split_rows * cfg->max_splits;
+    if (part * D * sizeof(float) >= ((size_t)1 << 31)) {  // the kernels address the partials with 32-bit offsets
+        delete c;
+        return fail(nullptr, QWATTN_EINVAL, "max_splits %d: the split partials would exceed 2 GiB", cfg->max_splits);
+    }
     const size_t qn = (size_t)cfg->max_tokens * NH * D;
     bool ok = hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
               hipMalloc(&c->rope, sizeof(float) * rope_n) == hipSuccess &&
               hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
               hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
+              hipMalloc(&c->arrive, sizeof(int) * NKV) == hipSuccess &&
               hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess;
     if (!ok) {
         qwattn_destroy(c);
@@ -178,7 +184,8 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     for (int i = 0; i < R / 2; i++) inv[i] = (float)(1.0 / std::pow((double)cfg->rope_theta, (2.0 * i) / R));
     if (hipMemcpy(c->inv_freq, inv.data(), sizeof(float) * inv.size(), hipMemcpyHostToDevice) != hipSuccess ||
         (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
-        hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
+        hipMemset(c->arrive, 0, sizeof(int) * NKV) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
     }
@@ -190,7 +197,8 @@ int qwattn_destroy(qwattn_ctx* c) {
     if (!c) return QWATTN_OK;
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
-    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->q32, c->q16})
+    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->arrive,
+                    (void*)c->q32, c->q16})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
@@ -321,7 +329,7 @@ int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const voi
     DeviceGuard dg(c->device);
     qw::DecodeArgs a{q, nullptr, nullptr, nullptr, nullptr, nullptr, (uint16_t*)kcache, (uint16_t*)vcache,
                      c->part_o, c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, false, QWATTN_F32, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -348,10 +356,37 @@ int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const voi
     DeviceGuard dg(c->device);
     qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
                      c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
+    if (used_splits) *used_splits = used;
+    return QWATTN_OK;
+}
+
+int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
+                  const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
+                  float* out, int pos, int n, int n_split, int* used_splits) {
+    if (!c) return QWATTN_EINVAL;
+    if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || !out || (!rope && c->cfg.rope_dim))
+        return fail(c, QWATTN_EINVAL, "qwattn_decode: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    int rc = check_call(c, pos, n, kv_cap);
+    if (rc) return rc;
+    const qwattn_config& g = c->cfg;
+    const int G = g.n_heads / g.n_kv_heads;
+    if (n * G > 8)
+        return fail(c, QWATTN_EINVAL, "qwattn_decode: n * NH/NKV = %d > 8 rows (use qwattn_decode_partial + "
+                    "qwattn_combine)", n * G);
+    int chunk = 0, used = 0;
+    pick_split(c, pos + n, n, n_split, &chunk, &used);
+    DeviceGuard dg(c->device);
+    qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
+                     c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), out, c->arrive};
+    HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
+    // the partials are consumed in the launch: a following qwattn_combine has nothing to merge
+    c->last_splits = 0;
     if (used_splits) *used_splits = used;
     return QWATTN_OK;
 }
@@ -394,6 +429,9 @@ int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg
         return fail(c, QWATTN_ESTATE, "qwattn_layer_attention: slot %d of %d allocated K/V caches", slot, (int)c->kc.size());
     const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
     int rc, used = 0;
+    if (n * G <= 8)  // single-token decode: one launch, combine included
+        return qwattn_decode(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
+                             pos, n, n_split, &used);
     if (n * G <= 32 && n <= 8) {
         // decode / verify: one fused launch (norm + rope + append + split attend), then the combine
         rc = qwattn_decode_partial(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap,

@@ -295,6 +295,79 @@ def test_fused_equals_unfused(qw, s, pos, n):
     assert np.abs(host(out) - host(out2)).max() <= 2e-6
 
 
+ONE_LAUNCH = [c for c in CASES_FUSED if c[2] * (c[0].NH // c[0].NKV) <= 8]
+
+
+@pytest.mark.parametrize("s,pos,n,n_split,dtype", ONE_LAUNCH, ids=lambda v: repr(v))
+def test_decode_one_launch_parity(qw, oracle, s, pos, n, n_split, dtype):
+    """qwattn_decode (norm, rope, append, split attend and the combine with its gate in one launch)
+    against the oracle, with the cache checks of the two-launch test."""
+    print(f"one-launch decode {s} pos={pos} n={n} split={n_split} {dtype}", flush=True)
+    rows = pos + n
+    cap, k16, v16, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, dtype, 400 + pos + n)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
+    torch.cuda.synchronize()
+    qg_h, k_h, v_h = host(qg_d), host(k_d), host(v_d)
+    rq, rk, _ = oracle.qk_norm_rope(qg_h, k_h, v_h, 1 + host(qn_d), 1 + host(kn_d), pos, s.R, s.theta, s.eps)
+    krows, vrows = qw.k_rows(kc, cap, s.NKV, s.D), qw.v_rows(vc, cap, s.NKV, s.D)
+    assert np.all(np.abs(host(krows[pos:rows]) - rk[pos:rows]) <= np.abs(rk[pos:rows]) * 2.0 ** -10 + 1e-6)
+    assert np.array_equal(host(vrows[pos:rows]), v_h.astype(np.float16).astype(np.float32))
+    ref = oracle.attention(rq, host(krows[:rows]), host(vrows[:rows]), pos, qg_h)
+    assert_parity(host(out), ref, f"{s} pos={pos} n={n} splits={used}")
+
+
+def test_decode_one_launch_equals_two_launches(qw):
+    """The in-launch combine merges what qwattn_combine merges: over a run of calls on one context with
+    changing split counts (fewer splits than query rows, one split, many), each output matches
+    decode_partial + combine to fp32 rounding (the two merges visit the splits in different orders).
+    A wrong re-arm of the arrival counters would leave a later call with no combiner or too early a
+    one."""
+    s, pos, n = QWEN3_NEXT, 3000, 1
+    cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 77)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    for n_split in [3, 0, 1, 7, 93, 0, 2]:
+        print(f"one-launch vs two-launch splits={n_split}", flush=True)
+        out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+        used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
+        out2 = torch.zeros((n, s.NH, s.D), device=DEV)
+        used2 = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, n_split)
+        ctx.combine(qg_d, out2, n, used2)
+        torch.cuda.synchronize()
+        assert used == used2
+        assert np.abs(host(out) - host(out2)).max() <= 2e-6, f"splits={used}"
+
+
+def test_decode_one_launch_graph_replays(qw):
+    """Captured into a HIP graph, the one-launch decode gives the eager result on every replay, with
+    eager work and synchronizations in between (the counters re-arm inside the kernel; nothing is
+    cleared by a memset node)."""
+    s, pos, n = QWEN3_NEXT, 8190, 1
+    cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 91)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    rope = ctx.rope_table()
+    eager = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, rope, kc, vc, cap, eager, pos, n, 0)
+    torch.cuda.synchronize()
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, rope, kc, vc, cap, out, pos, n, 0, stream=stream)
+    for rep in range(4):
+        print(f"graph replay {rep}", flush=True)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+        ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, rope, kc, vc, cap, eager, pos, n, 0)  # eager work in between
+        torch.cuda.synchronize()
+
+
 # ---- prefill -------------------------------------------------------------------------------------------
 
 CASES_PF = [
