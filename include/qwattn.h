@@ -142,13 +142,14 @@ int qwattn_decode_partial(qwattn_ctx* ctx, void* stream, const void* qg, const v
                           void* kcache, void* vcache, int kv_cap, int pos, int n, int n_split,
                           int* used_splits);
 
-/* All three of the reference's decode dispatches in one launch (src/qwen4_vk.cpp:968-992: qk_norm_rope,
+/* All three of the reference's decode dispatches (src/qwen4_vk.cpp:968-992: qk_norm_rope,
  * attention, attn_combine): qwattn_decode_partial followed, inside the same kernel, by the log-sum-exp
  * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. The last workgroups of each KV
  * head to finish merge the split partials; arrival counters in the context re-arm themselves at the end
  * of every launch, so the call allocates and clears nothing and can be captured into a graph. Calls on
- * one context must not overlap (one stream, or ordered streams). Requires n * NH/NKV <= 8
- * (single-token decode); returns QWATTN_EINVAL otherwise (use qwattn_decode_partial + qwattn_combine). */
+ * one context must not overlap (one stream, or ordered streams). Same limits as qwattn_decode_partial
+ * (n <= 8, n * NH/NKV <= 32: decode and MTP verify); one launch for n * NH/NKV <= 8, above that (verify)
+ * the attend launch is followed by the combine launch. */
 int qwattn_decode(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
                   int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
                   void* vcache, int kv_cap, float* out, int pos, int n, int n_split, int* used_splits);
@@ -173,8 +174,7 @@ int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dt
 /* The whole attention body between the projections, for one full-attention layer `slot` of the
  * context's caches (reference: the dispatches of Qwen4Vulkan::attention, src/qwen4_vk.cpp:968-992;
  * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): for n <= 8 and
- * n * NH/NKV <= 8 the single launch of qwattn_decode; for n <= 8 and n * NH/NKV <= 32 the fused
- * qwattn_decode_partial then qwattn_combine (two launches); otherwise norm +
+ * n <= 8 and n * NH/NKV <= 32 qwattn_decode; otherwise norm +
  * rope + append, then the MFMA prefill kernel (or split attend + combine for small groups). `n_split`
  * as in qwattn_attend_partial. */
 int qwattn_layer_attention(qwattn_ctx* ctx, void* stream, int slot, const void* qg, const void* k,

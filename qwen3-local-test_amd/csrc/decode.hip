@@ -65,6 +65,118 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f16x8 as_h8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 __device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
+// s_waitcnt immediate for "at most n vector-memory loads outstanding" (gfx9 encoding: vmcnt split over
+// bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+constexpr int kScDevice = 0x10;  // buffer load/store cache policy: device scope (sc1), coherent across XCDs
+
+// In-launch log-sum-exp combine (attn_combine.comp:13-29), run at the end of a decode workgroup whose
+// partials are written. The work is cut into units of one query row x 64 dims. Each workgroup counts its
+// arrival on its KV head's counter; the last NC = min(units, n_split) to arrive become the combiners:
+// combiner c waits (bounded) until every workgroup of the head has arrived, then merges units c, c + NC,
+// ... over all splits and writes them gated. Only those NC workgroups per head ever wait, and they wait
+// for workgroups that are already past their own arrival or still to be dispatched onto the slots every
+// other workgroup frees, so the wait always ends. The last combiner to finish puts the counter back to
+// zero for the next launch, so no clearing pass is needed (and none is recorded into a captured graph).
+// Launches that share a counter array must not overlap.
+template <int D, int IN_DT>
+__device__ __forceinline__ void combine_last(const DecodeArgs& a, int r0, int rows, int G, int kvh, int ctr) {
+    constexpr int UD = 64;                 // dims of a unit
+    constexpr int NUD = D / UD;            // units per row
+    constexpr int NSG = 256 / (UD / 4);    // split groups (16): thread tid takes splits tid % NSG + NSG * j
+    static_assert(D % UD == 0, "head_dim must be a multiple of 64");
+    constexpr int BATCH = 8;
+    constexpr int SPIN_MAX = 1 << 22;
+    __shared__ int s_arrival;
+    const int tid = threadIdx.x;
+    const int S = a.n_split;
+    // the partials went out as device-coherent stores: once acknowledged they are visible to every
+    // workgroup's device-coherent loads, so completing them is the whole release (no cache write-back)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    if (tid == 0) s_arrival = __hip_atomic_fetch_add(&a.arrive[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int units = rows * NUD;
+    const int NC = min(units, S);
+    const int ci = s_arrival - (S - NC);
+    if (ci < 0) return;
+    // 16 consecutive lanes hold the 16 split groups of one float4 column: the final merge is a butterfly
+    // inside those lanes (no LDS, no barrier)
+    const int sg = tid % NSG, col = tid / NSG;
+    auto gate_of = [&](int u, float (&gt)[4]) {  // the gate does not depend on the other workgroups
+        const int r = r0 + u / NUD, t = r / G, h = kvh * G + r % G;
+        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + (u % NUD) * UD + col * 4;
+#pragma unroll
+        for (int i = 0; i < 4; i++) gt[i] = load_in<IN_DT>(a.q, gb + i);
+    };
+    float gate[4];
+    gate_of(ci, gate);
+    if (tid == 0) {
+        for (int spin = 0; __hip_atomic_load(&a.arrive[ctr], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S &&
+                           spin < SPIN_MAX;
+             spin++)
+            __builtin_amdgcn_s_sleep(2);
+    }
+    __syncthreads();
+    for (int u = ci; u < units; u += NC) {
+        if (u != ci) gate_of(u, gate);
+        const int r = r0 + u / NUD, t = r / G, h = kvh * G + r % G;
+        const int d0 = (u % NUD) * UD + col * 4;
+        const size_t row = ((size_t)t * a.NH + h) * S;
+        // device-coherent loads: the other workgroups' stores, never a stale line of this XCD's L2
+        const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + row * 2, (short)0, S * 8, 0x00020000);
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + row * D, (short)0, S * D * 4, 0x00020000);
+        float M = kNegInf, L = 0.f;
+        f32x4 O = {0.f, 0.f, 0.f, 0.f};
+        for (int z0 = sg; z0 < S; z0 += NSG * BATCH) {
+            float m[BATCH], l[BATCH];
+            f32x4 o[BATCH];
+#pragma unroll
+            for (int k = 0; k < BATCH; k++) {  // every load of the batch is issued before any is used
+                const int zz = min(z0 + NSG * k, S - 1);
+                const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, zz * 8, 0, kScDevice));
+                m[k] = ml[0];
+                l[k] = ml[1];
+                o[k] = __builtin_amdgcn_raw_buffer_load_b128(ro, (zz * D + d0) * 4, 0, kScDevice);
+            }
+#pragma unroll
+            for (int k = 0; k < BATCH; k++) {
+                if (z0 + NSG * k < S && l[k] > 0.f) {
+                    const float mn = fmaxf(M, m[k]);
+                    const float cf = exp2_fast(M - mn), cu = exp2_fast(m[k] - mn);
+                    L = L * cf + l[k] * cu;
+                    O = O * cf + o[k] * cu;
+                    M = mn;
+                }
+            }
+        }
+#pragma unroll
+        for (int x = 1; x < NSG; x <<= 1) {  // merge with the lane x away (L = 0: nothing to merge)
+            const float Mo = __shfl_xor(M, x, 64), Lo = __shfl_xor(L, x, 64);
+            f32x4 Oo;
+#pragma unroll
+            for (int i = 0; i < 4; i++) Oo[i] = __shfl_xor(O[i], x, 64);
+            const float mn = fmaxf(M, Mo);
+            const float cf = L > 0.f ? exp2_fast(M - mn) : 0.f, co = Lo > 0.f ? exp2_fast(Mo - mn) : 0.f;
+            L = L * cf + Lo * co;
+            O = O * cf + Oo * co;
+            M = mn;
+        }
+        if (sg == 0) {
+            const float inv = 1.0f / L;
+            f32x4 res;
+#pragma unroll
+            for (int i = 0; i < 4; i++) res[i] = O[i] * inv * sigmoid(gate[i]);
+            *reinterpret_cast<f32x4*>(&a.out[((size_t)t * a.NH + h) * D + d0]) = res;
+        }
+    }
+    // the last combiner to finish re-arms the counter (every combiner is past its wait by then)
+    __syncthreads();
+    if (tid == 0 && __hip_atomic_fetch_add(&a.arrive[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S + NC - 1)
+        __hip_atomic_store(&a.arrive[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int D, int MODE, int FUSED, int IN_DT>
 __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     using C = DecCfg<D, MODE>;
@@ -458,9 +570,6 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     }
 }
 
-// s_waitcnt immediate for "at most n vector-memory loads outstanding" (gfx9 encoding: vmcnt split over
-// bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // ---- decode with producer waves (at most 8 query rows) -------------------------------------------
 // With HBM saturated, issuing a load stalls the issuing wave until earlier requests drain, so a wave that
@@ -471,114 +580,6 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) |
 // each tile through an LDS counter; the compute wave copies the slot into registers, frees it at once and
 // computes, so two tiles per pair are in flight while one is being computed. Spin waits are bounded, so
 // every wave exits even if a counter were never reached.
-constexpr int kScDevice = 0x10;  // buffer load/store cache policy: device scope (sc1), coherent across XCDs
-
-// In-launch log-sum-exp combine (attn_combine.comp:13-29), run at the end of a decode workgroup whose
-// partials are written. The work is cut into units of one query row x 64 dims. Each workgroup counts its
-// arrival on its KV head's counter; the last NC = min(units, n_split) to arrive become the combiners:
-// combiner c waits (bounded) until every workgroup of the head has arrived, then merges units c, c + NC,
-// ... over all splits and writes them gated. Only those NC workgroups per head ever wait, and they wait
-// for workgroups that are already past their own arrival or still to be dispatched onto the slots every
-// other workgroup frees, so the wait always ends. The last combiner to finish puts the counter back to
-// zero for the next launch, so no clearing pass is needed (and none is recorded into a captured graph).
-// Launches that share a counter array must not overlap.
-template <int D, int IN_DT>
-__device__ __forceinline__ void combine_last(const DecodeArgs& a, int rows, int G, int kvh) {
-    constexpr int UD = 64;                 // dims of a unit
-    constexpr int NUD = D / UD;            // units per row
-    constexpr int NSG = 256 / (UD / 4);    // split groups (16): thread tid takes splits tid % NSG + NSG * j
-    static_assert(D % UD == 0, "head_dim must be a multiple of 64");
-    constexpr int BATCH = 8;
-    constexpr int SPIN_MAX = 1 << 22;
-    __shared__ int s_arrival;
-    const int tid = threadIdx.x;
-    const int S = a.n_split;
-    // the partials went out as device-coherent stores: once acknowledged they are visible to every
-    // workgroup's device-coherent loads, so completing them is the whole release (no cache write-back)
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    __syncthreads();
-    if (tid == 0) s_arrival = __hip_atomic_fetch_add(&a.arrive[kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const int units = rows * NUD;
-    const int NC = min(units, S);
-    const int ci = s_arrival - (S - NC);
-    if (ci < 0) return;
-    // 16 consecutive lanes hold the 16 split groups of one float4 column: the final merge is a butterfly
-    // inside those lanes (no LDS, no barrier)
-    const int sg = tid % NSG, col = tid / NSG;
-    auto gate_of = [&](int u, float (&gt)[4]) {  // the gate does not depend on the other workgroups
-        const int r = u / NUD, t = r / G, h = kvh * G + r % G;
-        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + (u % NUD) * UD + col * 4;
-#pragma unroll
-        for (int i = 0; i < 4; i++) gt[i] = load_in<IN_DT>(a.q, gb + i);
-    };
-    float gate[4];
-    gate_of(ci, gate);
-    if (tid == 0) {
-        for (int spin = 0; __hip_atomic_load(&a.arrive[kvh], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S &&
-                           spin < SPIN_MAX;
-             spin++)
-            __builtin_amdgcn_s_sleep(2);
-    }
-    __syncthreads();
-    for (int u = ci; u < units; u += NC) {
-        if (u != ci) gate_of(u, gate);
-        const int r = u / NUD, t = r / G, h = kvh * G + r % G;
-        const int d0 = (u % NUD) * UD + col * 4;
-        const size_t row = ((size_t)t * a.NH + h) * S;
-        // device-coherent loads: the other workgroups' stores, never a stale line of this XCD's L2
-        const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + row * 2, (short)0, S * 8, 0x00020000);
-        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + row * D, (short)0, S * D * 4, 0x00020000);
-        float M = kNegInf, L = 0.f;
-        f32x4 O = {0.f, 0.f, 0.f, 0.f};
-        for (int z0 = sg; z0 < S; z0 += NSG * BATCH) {
-            float m[BATCH], l[BATCH];
-            f32x4 o[BATCH];
-#pragma unroll
-            for (int k = 0; k < BATCH; k++) {  // every load of the batch is issued before any is used
-                const int zz = min(z0 + NSG * k, S - 1);
-                const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, zz * 8, 0, kScDevice));
-                m[k] = ml[0];
-                l[k] = ml[1];
-                o[k] = __builtin_amdgcn_raw_buffer_load_b128(ro, (zz * D + d0) * 4, 0, kScDevice);
-            }
-#pragma unroll
-            for (int k = 0; k < BATCH; k++) {
-                if (z0 + NSG * k < S && l[k] > 0.f) {
-                    const float mn = fmaxf(M, m[k]);
-                    const float cf = exp2_fast(M - mn), cu = exp2_fast(m[k] - mn);
-                    L = L * cf + l[k] * cu;
-                    O = O * cf + o[k] * cu;
-                    M = mn;
-                }
-            }
-        }
-#pragma unroll
-        for (int x = 1; x < NSG; x <<= 1) {  // merge with the lane x away (L = 0: nothing to merge)
-            const float Mo = __shfl_xor(M, x, 64), Lo = __shfl_xor(L, x, 64);
-            f32x4 Oo;
-#pragma unroll
-            for (int i = 0; i < 4; i++) Oo[i] = __shfl_xor(O[i], x, 64);
-            const float mn = fmaxf(M, Mo);
-            const float cf = L > 0.f ? exp2_fast(M - mn) : 0.f, co = Lo > 0.f ? exp2_fast(Mo - mn) : 0.f;
-            L = L * cf + Lo * co;
-            O = O * cf + Oo * co;
-            M = mn;
-        }
-        if (sg == 0) {
-            const float inv = 1.0f / L;
-            f32x4 res;
-#pragma unroll
-            for (int i = 0; i < 4; i++) res[i] = O[i] * inv * sigmoid(gate[i]);
-            *reinterpret_cast<f32x4*>(&a.out[((size_t)t * a.NH + h) * D + d0]) = res;
-        }
-    }
-    // the last combiner to finish re-arms the counter (every combiner is past its wait by then)
-    __syncthreads();
-    if (tid == 0 && __hip_atomic_fetch_add(&a.arrive[kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S + NC - 1)
-        __hip_atomic_store(&a.arrive[kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int D, int FUSED, int IN_DT>
 __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     constexpr int NKS = D / 32, NDT = D / 16, RMAX = 8, BLKE = kBlk * D;
@@ -974,7 +975,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         __builtin_amdgcn_raw_buffer_store_b128(o, rpo, (row * D + d) * 4, 0, kScDevice);
     }
     if constexpr (FUSED) {
-        if (a.out != nullptr) combine_last<D, IN_DT>(a, rows, G, kvh);
+        if (a.out != nullptr) combine_last<D, IN_DT>(a, 0, rows, G, kvh, kvh);
     }
 }
 
@@ -987,7 +988,9 @@ template <int D, int FUSED, int IN_DT>
 static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
     const dim3 block(256);
-    if (a.out != nullptr && (rows > 8 || !FUSED)) return hipErrorInvalidValue;  // the in-launch combine: fused, <= 8 rows
+    // the in-launch combine: fused (it needs the gate) and at most 8 rows (the 16-row kernel has no
+    // registers left for it)
+    if (a.out != nullptr && (!FUSED || rows > 8)) return hipErrorInvalidValue;
     if (rows <= 8) {
         auto kern = k_decode_ld<D, FUSED, IN_DT>;
         const size_t shm = decode_ld_lds<D>();

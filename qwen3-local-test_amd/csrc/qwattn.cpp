@@ -375,16 +375,23 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     if (rc) return rc;
     const qwattn_config& g = c->cfg;
     const int G = g.n_heads / g.n_kv_heads;
-    if (n * G > 8)
-        return fail(c, QWATTN_EINVAL, "qwattn_decode: n * NH/NKV = %d > 8 rows (use qwattn_decode_partial + "
-                    "qwattn_combine)", n * G);
+    if (n * G > 32 || n > 8)
+        return fail(c, QWATTN_EINVAL, "qwattn_decode: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
+                    "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
     int chunk = 0, used = 0;
     pick_split(c, pos + n, n, n_split, &chunk, &used);
     DeviceGuard dg(c->device);
+    // up to 8 query rows the combine runs inside the attend launch; the 16-row-slice kernel (verify) is
+    // followed by the combine kernel
+    const bool one = n * G <= 8;
     qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
                      c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), out, c->arrive};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), one ? out : nullptr, one ? c->arrive : nullptr};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
+    if (!one) {
+        qw::CombineArgs ca{c->part_o, c->part_ml, qg, out, n, g.n_heads, used};
+        HIP_TRY(c, qw::launch_combine(ca, g.head_dim, in_dtype, (hipStream_t)stream));
+    }
     // the partials are consumed in the launch: a following qwattn_combine has nothing to merge
     c->last_splits = 0;
     if (used_splits) *used_splits = used;
@@ -429,16 +436,9 @@ int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg
         return fail(c, QWATTN_ESTATE, "qwattn_layer_attention: slot %d of %d allocated K/V caches", slot, (int)c->kc.size());
     const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
     int rc, used = 0;
-    if (n * G <= 8)  // single-token decode: one launch, combine included
+    if (n * G <= 32 && n <= 8)  // decode / verify: one launch (norm + rope + append + split attend + combine)
         return qwattn_decode(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
                              pos, n, n_split, &used);
-    if (n * G <= 32 && n <= 8) {
-        // decode / verify: one fused launch (norm + rope + append + split attend), then the combine
-        rc = qwattn_decode_partial(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap,
-                                   pos, n, n_split, &used);
-        if (rc) return rc;
-        return qwattn_combine(c, stream, qg, in_dtype, out, n, used);
-    }
     const bool split = n * G <= 32;
     rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
                                     c->kv_cap, split ? (void*)c->q32 : c->q16, split ? QWATTN_F32 : QWATTN_F16, pos, n);

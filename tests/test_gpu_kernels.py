@@ -295,7 +295,7 @@ def test_fused_equals_unfused(qw, s, pos, n):
     assert np.abs(host(out) - host(out2)).max() <= 2e-6
 
 
-ONE_LAUNCH = [c for c in CASES_FUSED if c[2] * (c[0].NH // c[0].NKV) <= 8]
+ONE_LAUNCH = CASES_FUSED
 
 
 @pytest.mark.parametrize("s,pos,n,n_split,dtype", ONE_LAUNCH, ids=lambda v: repr(v))
@@ -320,15 +320,16 @@ def test_decode_one_launch_parity(qw, oracle, s, pos, n, n_split, dtype):
 
 def test_decode_one_launch_equals_two_launches(qw):
     """The in-launch combine merges what qwattn_combine merges: over a run of calls on one context with
-    changing split counts (fewer splits than query rows, one split, many), each output matches
+    changing token counts (decode n=1 on the loader-wave kernel, verify n=4 on two 16-row slices) and
+    split counts (fewer splits than combine units, one split, many), each output matches
     decode_partial + combine to fp32 rounding (the two merges visit the splits in different orders).
     A wrong re-arm of the arrival counters would leave a later call with no combiner or too early a
     one."""
-    s, pos, n = QWEN3_NEXT, 3000, 1
-    cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 77)
+    s, pos = QWEN3_NEXT, 3000
+    cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, 4, "f32", 77)
     ctx = make_ctx(qw, s, max_ctx=cap)
-    for n_split in [3, 0, 1, 7, 93, 0, 2]:
-        print(f"one-launch vs two-launch splits={n_split}", flush=True)
+    for n, n_split in [(1, 3), (4, 0), (1, 0), (4, 1), (1, 1), (4, 7), (1, 93), (4, 93), (1, 0), (2, 2)]:
+        print(f"one-launch vs two-launch n={n} splits={n_split}", flush=True)
         out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
         used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
         out2 = torch.zeros((n, s.NH, s.D), device=DEV)
