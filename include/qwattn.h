@@ -171,11 +171,18 @@ int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dt
                           const void* kcache, const void* vcache, int kv_cap, const void* qg,
                           int in_dtype, float* out, int pos, int n);
 
+/* The reference's prefill dispatches of one chunk (src/qwen4_vk.cpp:968-992) in two launches:
+ * qwattn_qk_norm_rope_append into the context's fp16 query buffer (pre-scaled), then
+ * qwattn_attend_prefill on it. n <= max_tokens. */
+int qwattn_prefill(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
+                   int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
+                   void* vcache, int kv_cap, float* out, int pos, int n);
+
 /* The whole attention body between the projections, for one full-attention layer `slot` of the
  * context's caches (reference: the dispatches of Qwen4Vulkan::attention, src/qwen4_vk.cpp:968-992;
  * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): for n <= 8 and
- * n <= 8 and n * NH/NKV <= 32 qwattn_decode; otherwise norm +
- * rope + append, then the MFMA prefill kernel (or split attend + combine for small groups). `n_split`
+ * n <= 8 and n * NH/NKV <= 32 qwattn_decode; otherwise qwattn_prefill (or norm + rope + append,
+ * split attend and combine when n * NH/NKV <= 32). `n_split`
  * as in qwattn_attend_partial. */
 int qwattn_layer_attention(qwattn_ctx* ctx, void* stream, int slot, const void* qg, const void* k,
                            const void* v, int in_dtype, const float* qn, const float* kn, float* out,

@@ -64,6 +64,7 @@ def load_library():
         "qwattn_decode": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, ctypes.POINTER(_I)],
         "qwattn_combine": [_P, _P, _P, _I, _P, _I, _I],
         "qwattn_attend_prefill": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I],
+        "qwattn_prefill": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
     }
     for name, args in sig.items():
@@ -219,6 +220,12 @@ class Attention:
     def attend_prefill(self, q, kcache, vcache, kv_cap, qg, out, pos, n, stream=None):
         self._check(self.lib.qwattn_attend_prefill(self.h, _stream(stream), _ptr(q), _DT[q.dtype], _ptr(kcache),
                                                    _ptr(vcache), kv_cap, _ptr(qg), _DT[qg.dtype], _ptr(out), pos, n))
+
+    def prefill(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
+        """K/V norm + rope + append, then the MFMA prefill normalizing its own query rows (two launches)."""
+        self._check(self.lib.qwattn_prefill(
+            self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
+            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n))
 
     def attend(self, q, kcache, vcache, kv_cap, qg, out, pos, n, n_split=0, stream=None):
         """Split-KV + combine when n * NH/NKV <= 32, else the prefill kernel (q fp32 unscaled)."""

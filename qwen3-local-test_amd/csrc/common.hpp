@@ -12,6 +12,11 @@ typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// buffer load/store cache policy: device scope (sc1). Such stores reach the point every XCD reads from
+// once acknowledged, and such loads never return a stale line of the local L2: partial results written by
+// one workgroup can be read by another in the same launch without a cache-wide write-back or invalidate.
+constexpr int kScDevice = 0x10;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace qw {
@@ -85,12 +90,6 @@ __device__ __forceinline__ float xor8(float x) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-    return x;
-}
-
 // 1 / (1 + e^-x) with the hardware exponential and reciprocal (about 1 ulp each); saturates to 0 for
 // x below about -88 (e^-x overflows, its reciprocal is 0) and to 1 above
 __device__ __forceinline__ float sigmoid(float x) {
@@ -132,44 +131,6 @@ __device__ __forceinline__ int v_off(int kb, int d) {
 // Element offset of (position p, KV head h) part start.
 __device__ __forceinline__ size_t kv_part(int p, int h, int NKV, int D) {
     return ((size_t)(p >> 5) * NKV + h) * (size_t)(kBlk * D);
-}
-
-// RMSNorm with the (1 + w) multiplier and partial rotate-half RoPE of one head row, one 64-lane wave
-// per row (the reference's qk_norm_rope.comp:26-42 / src/qwen4_cpu.cpp:19-23, 281-289):
-//   y = x * rsqrt(mean(x^2) + eps) * (1 + w);  for d < R/2:  y'[d] = y[d] cos_d - y[d + R/2] sin_d,
-//   for R/2 <= d < R:  y'[d] = y[d] cos_{d-R/2} + y[d - R/2] sin_{d-R/2}
-// Lane l holds dims l*DPL .. l*DPL + DPL - 1 (DPL = D/64); the RoPE partner sits (R/2)/DPL lanes away
-// (the host requires (R/2) % DPL == 0). `rope_row` is the table row (cos, sin)[R/2] of the position.
-template <int D, int IN_DT>
-__device__ __forceinline__ void norm_rope_row(const void* src, size_t off, const float* w,
-                                              const float* rope_row, int R, float eps, int lane,
-                                              float (&y)[D / 64]) {
-    constexpr int DPL = D / 64;
-    const int d0 = lane * DPL;
-    float x[DPL];
-#pragma unroll
-    for (int j = 0; j < DPL; j++) x[j] = load_in<IN_DT>(src, off + d0 + j);
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < DPL; j++) ss += x[j] * x[j];
-    ss = wave_sum(ss);
-    const float r = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-    for (int j = 0; j < DPL; j++) y[j] = x[j] * r * (1.0f + w[d0 + j]);
-    const int half = R >> 1;
-    const int offl = half / DPL;
-    const bool lo_half = d0 < half;
-    const int src_lane = d0 < R ? (lo_half ? lane + offl : lane - offl) & 63 : lane;
-#pragma unroll
-    for (int j = 0; j < DPL; j++) {
-        const float partner = __shfl(y[j], src_lane, 64);
-        const int d = d0 + j;
-        if (d < R) {
-            const int i = lo_half ? d : d - half;
-            const float c = rope_row[2 * i], s = rope_row[2 * i + 1];
-            y[j] = lo_half ? y[j] * c - partner * s : y[j] * c + partner * s;
-        }
-    }
 }
 
 }  // namespace qw

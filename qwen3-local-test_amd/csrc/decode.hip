@@ -69,7 +69,6 @@ __device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x
 // bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-constexpr int kScDevice = 0x10;  // buffer load/store cache policy: device scope (sc1), coherent across XCDs
 
 // In-launch log-sum-exp combine (attn_combine.comp:13-29), run at the end of a decode workgroup whose
 // partials are written. The work is cut into units of one query row x 64 dims. Each workgroup counts its
@@ -252,8 +251,8 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             load_vec<0, 2 * DPL2>(a.rope, (size_t)(valid && rot ? p : 0) * a.R + 2 * i0, cv);
         }
     };
-    // y = x * rsqrt(mean(x^2) + eps) * (1 + w), then rotate-half on d < R (as norm_rope_row, with the
-    // row spread over 32 lanes; the partner dim d +- R/2 sits (R/2)/DPL2 lanes away in the same half)
+    // y = x * rsqrt(mean(x^2) + eps) * (1 + w), then rotate-half on d < R (as k_qk_norm_rope: the row
+    // spread over 32 lanes, the partner dim d +- R/2 (R/2)/DPL2 lanes away in the same half)
     auto finish_row = [&](const float (&xr)[DPL2], const float (&cv)[2 * DPL2], bool valid, const float (&w)[DPL2],
                           float (&y)[DPL2]) {
         float x[DPL2];

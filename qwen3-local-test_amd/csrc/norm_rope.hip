@@ -7,9 +7,12 @@
 // with (cos_i, sin_i) from row p = pos + t of the rope table. Query heads write q_out; key heads
 // write K cache position p (round-to-nearest-even fp16, as packHalf2x16) and copy V into the V cache.
 //
-// MI355X layout: one 64-lane wavefront per (token, head) — the reference uses a 256-invocation
-// workgroup with an LDS reduction per head — so the mean of squares is a wave reduction with no
-// barrier (norm_rope_row in common.hpp). The caches are written in the blocked layout of common.hpp.
+// MI355X layout: a 32-lane half-wavefront per four (token, head) rows, D/32 consecutive dims per lane
+// (the reference uses a 256-invocation workgroup with an LDS reduction per head), so the mean of
+// squares is a five-step shuffle reduction with no barrier, the rows move in 16-byte loads and stores,
+// every load of the four rows is in flight at once, and the RoPE partner d +- R/2 is (R/2)/(D/32)
+// lanes away. The caches are written in the blocked layout of
+// common.hpp (a key row's 8 consecutive dims are one 16-byte piece).
 // The split-KV decode kernel (decode.hip) does the same work inline for its new tokens; this kernel
 // serves prefill chunks and callers of the per-dispatch entry point.
 #include "common.hpp"
@@ -17,44 +20,95 @@
 
 namespace qw {
 
+constexpr int kNormRows = 4;  // rows per half-wave: every load of the four is issued before any is used
+
 template <int D, int IN_DT, int Q_DT>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
-    constexpr int DPL = D / 64;  // dims per lane
-    const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // kNormRows rows per half-wave (32 lanes x DPL consecutive dims each): 16-byte loads of the rows and
+    // 16-byte stores of the query rows and of the key rows' blocked-layout pieces
+    constexpr int DPL = D / 32;
+    constexpr int NR = kNormRows;
+    const int hl = threadIdx.x & 31;
+    const int item0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * NR;
     const int heads = a.NH + a.NKV;
-    if (item >= a.n * heads) return;  // whole wave exits
-    const int t = item / heads, hh = item % heads;
-    const bool is_q = hh < a.NH;
-    const int h = is_q ? hh : hh - a.NH;
-    const int p = a.pos + t;
-    const int d0 = lane * DPL;
+    const int n_items = a.n * heads;
+    if (item0 >= n_items) return;  // whole half-wave exits
+    const int d0 = hl * DPL;
+    const int half_r = a.R >> 1;
+    const bool rot = d0 < a.R;  // DPL divides R/2: a lane's dims are all rotated or all not
+    const bool lo = d0 < half_r;
 
-    const size_t src = is_q ? ((size_t)t * a.NH + h) * 2 * D : ((size_t)t * a.NKV + h) * D;
-    float y[DPL];
-    norm_rope_row<D, IN_DT>(is_q ? a.qg : a.k, src, is_q ? a.qn : a.kn, a.rope + (size_t)p * a.R, a.R, a.eps,
-                            lane, y);
+    float x[NR][DPL], vv[NR][DPL], cs[NR][2 * DPL];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int item = min(item0 + r, n_items - 1);  // past the end: the last row again, not stored
+        const int t = item / heads, hh = item % heads;
+        const bool is_q = hh < a.NH;
+        const int h = is_q ? hh : hh - a.NH;
+        const size_t src = is_q ? ((size_t)t * a.NH + h) * 2 * D : ((size_t)t * a.NKV + h) * D;
+        load_vec<IN_DT, DPL>(is_q ? a.qg : a.k, src + d0, x[r]);
+        if (!is_q) load_vec<IN_DT, DPL>(a.v, ((size_t)t * a.NKV + h) * D + d0, vv[r]);
+        if (rot) load_vec<0, 2 * DPL>(a.rope, (size_t)(a.pos + t) * a.R + 2 * (lo ? d0 : d0 - half_r), cs[r]);
+    }
+    float wq[DPL], wk[DPL];
+    load_vec<0, DPL>(a.qn, d0, wq);
+    load_vec<0, DPL>(a.kn, d0, wk);
+    const int offl = half_r / DPL;
+    // rotate-half: the partner dim d +- R/2 sits (R/2)/DPL lanes away in the same half-wave
+    const int src_lane = (threadIdx.x & 63 & ~31) + (rot ? (lo ? hl + offl : hl - offl) : hl);
 
-    if (is_q) {
-        if constexpr (Q_DT == 0) {
-            float* qo = static_cast<float*>(a.q_out) + ((size_t)t * a.NH + h) * D + d0;
 #pragma unroll
-            for (int j = 0; j < DPL; j++) qo[j] = y[j];
-        } else {
-            f16* qo = static_cast<f16*>(a.q_out) + ((size_t)t * a.NH + h) * D + d0;
+    for (int r = 0; r < NR; r++) {
+        const int item = item0 + r;
+        if (item >= n_items) break;  // uniform over the half-wave
+        const int t = item / heads, hh = item % heads;
+        const bool is_q = hh < a.NH;
+        const int h = is_q ? hh : hh - a.NH;
+        const int p = a.pos + t;
+        float ss = 0.f;
 #pragma unroll
-            for (int j = 0; j < DPL; j++) qo[j] = (f16)(y[j] * a.q_scale);
-        }
-    } else {
-        const size_t part = kv_part(p, h, a.NKV, D);
-        f16* kc = reinterpret_cast<f16*>(a.kcache) + part;
-        f16* vc = reinterpret_cast<f16*>(a.vcache) + part;
-        const int kb = p & (kBlk - 1);
-        const size_t vs = ((size_t)t * a.NKV + h) * D + d0;
+        for (int j = 0; j < DPL; j++) ss += x[r][j] * x[r][j];
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 32);
+        const float rn = 1.0f / sqrtf(ss / (float)D + a.eps);
+        float y[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; j++) y[j] = x[r][j] * rn * (1.0f + (is_q ? wq[j] : wk[j]));
 #pragma unroll
         for (int j = 0; j < DPL; j++) {
-            kc[k_off(kb, d0 + j)] = (f16)y[j];
-            vc[v_off(kb, d0 + j)] = (f16)load_in<IN_DT>(a.v, vs + j);
+            const float partner = __shfl(y[j], src_lane, 64);
+            if (rot) y[j] = lo ? y[j] * cs[r][2 * j] - partner * cs[r][2 * j + 1] : y[j] * cs[r][2 * j] + partner * cs[r][2 * j + 1];
+        }
+        typedef f16 f16v __attribute__((ext_vector_type(DPL)));
+        if (is_q) {
+            if constexpr (Q_DT == 0) {
+                float* qo = static_cast<float*>(a.q_out) + ((size_t)t * a.NH + h) * D + d0;
+                if constexpr (DPL % 4 == 0) {
+#pragma unroll
+                    for (int j = 0; j < DPL; j += 4) *reinterpret_cast<f32x4*>(qo + j) = f32x4{y[j], y[j + 1], y[j + 2], y[j + 3]};
+                } else {
+#pragma unroll
+                    for (int j = 0; j < DPL; j++) qo[j] = y[j];
+                }
+            } else {
+                f16v o;
+#pragma unroll
+                for (int j = 0; j < DPL; j++) o[j] = (f16)(y[j] * a.q_scale);
+                *reinterpret_cast<f16v*>(static_cast<f16*>(a.q_out) + ((size_t)t * a.NH + h) * D + d0) = o;
+            }
+        } else {
+            const size_t part = kv_part(p, h, a.NKV, D);
+            f16* kc = reinterpret_cast<f16*>(a.kcache) + part;
+            f16* vc = reinterpret_cast<f16*>(a.vcache) + part;
+            const int kb = p & (kBlk - 1);
+            // K: the lane's DPL dims are consecutive in the blocked layout (d % 8 runs fastest)
+            f16v ko;
+#pragma unroll
+            for (int j = 0; j < DPL; j++) ko[j] = (f16)y[j];
+            *reinterpret_cast<f16v*>(kc + k_off(kb, d0)) = ko;
+            // V: consecutive dims are 8 elements apart (8 keys of one dim are contiguous)
+#pragma unroll
+            for (int j = 0; j < DPL; j++) vc[v_off(kb, d0 + j)] = (f16)vv[r][j];
         }
     }
 }
@@ -62,7 +116,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
 template <int D>
 static hipError_t launch_d(const NormRopeArgs& a, int in_dtype, int q_dtype, hipStream_t s) {
     const int items = a.n * (a.NH + a.NKV);
-    const dim3 grid((items + 3) / 4), block(256);
+    const dim3 grid((items + 8 * kNormRows - 1) / (8 * kNormRows)), block(256);
     if (in_dtype == 0 && q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 0>), grid, block, 0, s, a);
     else if (in_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 1>), grid, block, 0, s, a);
     else if (q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 0>), grid, block, 0, s, a);

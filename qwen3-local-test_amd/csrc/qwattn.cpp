@@ -429,6 +429,18 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     return QWATTN_OK;
 }
 
+int qwattn_prefill(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
+                   const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
+                   float* out, int pos, int n) {
+    if (!c) return QWATTN_EINVAL;
+    if (!out) return fail(c, QWATTN_EINVAL, "qwattn_prefill: null pointer");
+    // norm + rope + append into the context's fp16 query buffer, then the MFMA prefill on it
+    int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, c->q16,
+                                        QWATTN_F16, pos, n);
+    if (rc) return rc;
+    return qwattn_attend_prefill(c, stream, c->q16, QWATTN_F16, kcache, vcache, kv_cap, qg, in_dtype, out, pos, n);
+}
+
 int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg, const void* k, const void* v,
                            int in_dtype, const float* qn, const float* kn, float* out, int pos, int n, int n_split) {
     if (!c) return QWATTN_EINVAL;
@@ -439,17 +451,16 @@ int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg
     if (n * G <= 32 && n <= 8)  // decode / verify: one launch (norm + rope + append + split attend + combine)
         return qwattn_decode(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
                              pos, n, n_split, &used);
-    const bool split = n * G <= 32;
-    rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
-                                    c->kv_cap, split ? (void*)c->q32 : c->q16, split ? QWATTN_F32 : QWATTN_F16, pos, n);
-    if (rc) return rc;
-    if (split) {
+    if (n * G <= 32) {  // more than 8 tokens in small groups: norm + rope + append, split attend, combine
+        rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
+                                        c->kv_cap, c->q32, QWATTN_F32, pos, n);
+        if (rc) return rc;
         rc = qwattn_attend_partial(c, stream, c->q32, c->kc[slot], c->vc[slot], c->kv_cap, pos, n, n_split, &used);
         if (rc) return rc;
         return qwattn_combine(c, stream, qg, in_dtype, out, n, used);
     }
-    return qwattn_attend_prefill(c, stream, c->q16, QWATTN_F16, c->kc[slot], c->vc[slot], c->kv_cap, qg, in_dtype, out,
-                                 pos, n);
+    return qwattn_prefill(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
+                          pos, n);
 }
 
 }  // extern "C"

@@ -412,6 +412,40 @@ def test_prefill_parity(qw, oracle, s, pos, n):
         assert_parity(out[t:t + 1], ref, f"{s} pos={pos} n={n} token {t}")
 
 
+@pytest.mark.parametrize("s,pos,n", CASES_PF, ids=lambda v: repr(v))
+def test_prefill_entry_parity(qw, oracle, s, pos, n):
+    """qwattn_prefill (norm/rope/append into the context's query buffer, then the MFMA prefill) against
+    the oracle, and identical to the two entry points called in sequence."""
+    print(f"fused prefill {s} pos={pos} n={n}", flush=True)
+    rows = pos + n
+    cap = capacity(rows)
+    k16, v16 = cache_rows(40 + pos, pos, s) if pos else (np.zeros((0, s.NKV, s.D), np.float16),) * 2
+    qg, k, v, qn, kn = projections(41 + n, n, s)
+    qg_d, k_d, v_d = dev(qg).to(torch.bfloat16), dev(k).to(torch.bfloat16), dev(v).to(torch.bfloat16)
+    ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=max(n, 1))
+    kc, vc = gpu_caches(qw, k16, v16, cap) if pos else empty_caches(s, cap)
+    kc2, vc2 = kc.clone(), vc.clone()
+    out = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.prefill(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, out, pos, n)
+    q16 = torch.zeros((n, s.NH, s.D), dtype=torch.float16, device=DEV)
+    ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc2, vc2, cap, q16, pos, n)
+    out2 = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.attend_prefill(q16, kc2, vc2, cap, qg_d, out2, pos, n)
+    torch.cuda.synchronize()
+    # the same K/V rows appended by both paths
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    out, out2 = host(out), host(out2)
+    assert np.array_equal(out, out2)
+    rq, _, _ = oracle.qk_norm_rope(host(qg_d), host(k_d), host(v_d), 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
+    kcache = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
+    vcache = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
+    qg_h = host(qg_d)
+    toks = np.arange(n) if n <= 300 else np.unique(np.r_[0, 1, np.linspace(0, n - 1, 48).astype(int), n - 1])
+    for t in toks:
+        ref = oracle.attention(rq[t:t + 1], kcache, vcache, pos + t, qg_h[t:t + 1])
+        assert_parity(out[t:t + 1], ref, f"{s} pos={pos} n={n} token {t}")
+
+
 def test_prefill_equals_decodes(qw):
     """A prefill chunk gives the same rows as decoding its tokens one at a time (block-causal vs
     token-causal masks agree)."""
