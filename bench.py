@@ -249,7 +249,7 @@ def run_workload(wl, steps, warmup, graph):
     return r
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_decode_decode_32k_k_prefill_prefill_2k_hbm_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_decode_ld_decode_32k_k_prefill_prefill_2k_hbm_traffic.md")
 
 
 def measured_traffic(kernel, workload):
@@ -424,7 +424,7 @@ def main():
                             "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                             "frac": round(head["frac_hbm_kernel"], 4),
-                            "traffic": measured_traffic("k_decode", "decode_32k"),
+                            "traffic": measured_traffic("k_decode_ld", "decode_32k"),
                             "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
                             "kernel_us": head["us_main"]}
     pf = results.get("prefill_2k_on_2k")

@@ -44,14 +44,13 @@
 
 namespace qw {
 
-// MODE 0: at most 8 query rows, their fp16 lo parts in columns 8-15 of the same MFMA; MODE 1: a slice of
-// 16 rows, hi and lo parts as two MFMAs into one accumulator.
-template <int D, int MODE>
+// k_decode: a slice of 16 query rows, hi and lo parts of Q and P as two MFMAs into one accumulator.
+template <int D>
 struct DecCfg {
     static constexpr int NKS = D / 32;                     // k-steps of the QK^T product
     static constexpr int NDT = D / 16;                     // 16-dim tiles of the P.V product
-    static constexpr int RMAX = MODE == 0 ? 8 : 16;        // query rows of the workgroup
-    static constexpr int NQS = MODE == 0 ? 1 : 2;          // Q fragment sets in LDS (hi, lo)
+    static constexpr int RMAX = 16;                        // query rows of the workgroup
+    static constexpr int NQS = 2;                          // Q fragment sets in LDS (hi, lo)
     static constexpr int QBYTES = NQS * NKS * 1024;
     static constexpr int OSTRIDE = D + 4;                  // floats per row of the wave-partial buffer
     static constexpr int MBYTES = 4 * RMAX * OSTRIDE * 4;
@@ -176,11 +175,11 @@ __device__ __forceinline__ void combine_last(const DecodeArgs& a, int r0, int ro
         __hip_atomic_store(&a.arrive[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int MODE, int FUSED, int IN_DT>
+template <int D, int FUSED, int IN_DT>
 __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
-    using C = DecCfg<D, MODE>;
+    using C = DecCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, RMAX = C::RMAX, BLKE = C::BLKE, NB = C::NB;
-    constexpr int NPT = MODE == 0 ? 1 : 2;  // P operands (hi, lo) per tile
+    constexpr int NPT = 2;                  // P operands (hi, lo) per tile
     constexpr int DPL2 = D / 32;            // dims per lane in the row passes
     constexpr int QPASS = RMAX / 8;         // query-row passes per wave
     constexpr float TAU = 8.f;              // a running max moves only when exceeded by this (log2 units)
@@ -332,11 +331,10 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             hv[jj] = hi;
             lv[jj] = (f16)(ys - (float)hi);
         }
-        const int col = MODE == 0 ? r : (r & 15);
+        const int col = r & 15;
         const int kk = d0 >> 5, L = ((d0 >> 3) & 3) * 16 + col, e = d0 & 7;
         *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L) * 8 + e]) = hv;
-        if constexpr (MODE == 0) *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L + 8) * 8 + e]) = lv;
-        else *reinterpret_cast<f16v*>(&s_q[((NKS + kk) * 64 + L) * 8 + e]) = lv;
+        *reinterpret_cast<f16v*>(&s_q[((NKS + kk) * 64 + L) * 8 + e]) = lv;
     }
     if constexpr (FUSED) {
         float y[DPL2];
@@ -368,17 +366,12 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     __syncthreads();
 
     // ---- per column: query row, causal key limit inside this chunk, softmax state ----------------
-    const int rcol = MODE == 0 ? (c & 7) : c;
+    const int rcol = c;
     const int lim = rcol < rows ? min(a.pos + (r0 + rcol) / G + 1, ke) : 0;
     float m_run = kNegInf, l_run = 0.f;
     f32x4 acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    f16x8 qreg[MODE == 0 ? NKS : 1];
-    if constexpr (MODE == 0) {
-#pragma unroll
-        for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
-    }
     auto qfrag = [&](int set, int kk) -> f16x8 {
         return *reinterpret_cast<const f16x8*>(s_q + ((set * NKS + kk) * 64 + lane) * 8);
     };
@@ -403,12 +396,8 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             f32x4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < NKS; kk++) {
-                if constexpr (MODE == 0) {
-                    x = mfma16(kt[kk][s], qreg[kk], x);
-                } else {
-                    x = mfma16(kt[kk][s], qfrag(0, kk), x);
-                    x = mfma16(kt[kk][s], qfrag(1, kk), x);
-                }
+                x = mfma16(kt[kk][s], qfrag(0, kk), x);
+                x = mfma16(kt[kk][s], qfrag(1, kk), x);
             }
             sc[s] = x;
         }
@@ -442,7 +431,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         for (int s = 0; s < 2; s++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float v = MODE == 0 ? sc[s][i] + xor8(sc[s][i]) : sc[s][i];
+                const float v = sc[s][i];
                 const int key = tb + 8 * g + 4 * s + i;
                 sv[s * 4 + i] = key < lim ? v : kNegInf;
             }
@@ -473,12 +462,8 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             psum += p;
             const f16 ph = (f16)p;
             const f16 pl = (f16)(p - (float)ph);
-            if constexpr (MODE == 0) {
-                pop[0][k] = c >= 8 ? pl : ph;
-            } else {
-                pop[0][k] = ph;
-                pop[1][k] = pl;
-            }
+            pop[0][k] = ph;
+            pop[1][k] = pl;
         }
         l_run += psum;
 #pragma unroll
@@ -520,13 +505,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         float l = l_run;
         l += __shfl_xor(l, 16, 64);
         l += __shfl_xor(l, 32, 64);
-        if constexpr (MODE == 0) {
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[dt][i] += xor8(acc[dt][i]);
-        }
-        if (MODE != 0 || c < 8) {
+        {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
                 *reinterpret_cast<f32x4*>(&sO[(wave * RMAX + c) * C::OSTRIDE + dt * 16 + g * 4]) = acc[dt];
@@ -1006,7 +985,7 @@ static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
         }
         hipLaunchKernelGGL(kern, dim3(a.n_split, a.NKV, 1), block, shm, s, a);
     }
-    else hipLaunchKernelGGL((k_decode<D, 1, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), block, 0, s, a);
     return hipGetLastError();
 }
 
