@@ -28,15 +28,17 @@
  *                        as the reference uploads them (src/qwen4_vk.cpp:444-448, qk_norm_rope.comp:33).
  *  - rope [n_pos][R/2][2] fp32 (cos, sin) of the fp32 angle (float)p * inv_freq[i],
  *                        inv_freq[i] = (float)(1 / theta^(2i/R)) (src/qwen4_vk.cpp:494-504).
- *  - K and V caches [cap/32][NKV][32*D] fp16, cap a multiple of 32: blocks of 32 positions, one
- *                        32*D part per KV head. The reference keeps [cap][NKV][D] rows
+ *  - K and V caches [NKV][cap/32][32*D] fp16, cap a multiple of 32: per KV head, blocks of 32
+ *                        positions, one 32*D part per block (a head's key range is one contiguous
+ *                        byte range). The reference keeps [cap][NKV][D] rows
  *                        (src/qwen4_vk.cpp:565-574); here the elements inside a part are ordered so
  *                        that every matrix-core operand fragment is one contiguous kilobyte:
  *                          K (key kb = p % 32, dim d): (((d/32)*2 + (kb/4)%2)*4 + (d/8)%4)*16
  *                                                      + (kb/8)*4 + kb%4) * 8 + d%8
  *                          V (key kb, dim d):          (((d/16)*4 + kb/8)*16 + d%16) * 8 + kb%8
- *                        Blocks stay in position order, so the reference's grow-by-copy (ensure_kv)
- *                        carries over: the old caches are a byte prefix of the grown ones.
+ *                        Blocks stay in position order within a head, so the reference's
+ *                        grow-by-copy (ensure_kv) carries over head by head: each head's old region is
+ *                        a byte prefix of its new one.
  *  - q    [n][NH][D] fp32 normalized + rotated query (the reference's q_out).
  *  - out  [n][NH][D] fp32 gated attention output (the reference's att_, input of o_proj).
  */

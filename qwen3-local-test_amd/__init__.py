@@ -101,31 +101,31 @@ BLK = 32  # positions per cache block
 
 def k_block(rows):
     """[cap][NKV][D] K rows -> the blocked K cache layout of include/qwattn.h, flat (cap % 32 == 0):
-    block b, head h, key kb, dim d at ((b*NKV + h)*32*D) + ((((d/32)*2 + (kb/4)%2)*4 + (d/8)%4)*16
+    head h, block b, key kb, dim d at ((h*(cap/32) + b)*32*D) + ((((d/32)*2 + (kb/4)%2)*4 + (d/8)%4)*16
     + (kb/8)*4 + kb%4)*8 + d%8."""
     cap, nkv, d = rows.shape
     x = rows.reshape(cap // BLK, 4, 2, 4, nkv, d // 32, 4, 8)  # [b][kb/8][kb/4%2][kb%4][h][d/32][d/8%4][d%8]
-    return x.permute(0, 4, 5, 2, 6, 1, 3, 7).contiguous().view(-1)
+    return x.permute(4, 0, 5, 2, 6, 1, 3, 7).contiguous().view(-1)
 
 
 def k_rows(kcache, cap, nkv, d):
     """Inverse of k_block: the flat blocked K cache -> [cap][NKV][D] rows (a copy)."""
-    x = kcache.view(cap // BLK, nkv, d // 32, 2, 4, 4, 4, 8)   # [b][h][d/32][s][g][kb/8][kb%4][e]
-    return x.permute(0, 5, 3, 6, 1, 2, 4, 7).reshape(cap, nkv, d)
+    x = kcache.view(nkv, cap // BLK, d // 32, 2, 4, 4, 4, 8)   # [h][b][d/32][s][g][kb/8][kb%4][e]
+    return x.permute(1, 5, 3, 6, 0, 2, 4, 7).reshape(cap, nkv, d)
 
 
 def v_block(rows):
-    """[cap][NKV][D] V rows -> the blocked V cache layout, flat: block b, head h, key kb, dim d at
-    ((b*NKV + h)*32*D) + (((d/16)*4 + kb/8)*16 + d%16)*8 + kb%8."""
+    """[cap][NKV][D] V rows -> the blocked V cache layout, flat: head h, block b, key kb, dim d at
+    ((h*(cap/32) + b)*32*D) + (((d/16)*4 + kb/8)*16 + d%16)*8 + kb%8."""
     cap, nkv, d = rows.shape
     x = rows.reshape(cap // BLK, 4, 8, nkv, d // 16, 16)        # [b][kb/8][kb%8][h][d/16][d%16]
-    return x.permute(0, 3, 4, 1, 5, 2).contiguous().view(-1)
+    return x.permute(3, 0, 4, 1, 5, 2).contiguous().view(-1)
 
 
 def v_rows(vcache, cap, nkv, d):
     """Inverse of v_block."""
-    x = vcache.view(cap // BLK, nkv, d // 16, 4, 16, 8)         # [b][h][d/16][kb/8][d%16][kb%8]
-    return x.permute(0, 3, 5, 1, 2, 4).reshape(cap, nkv, d)
+    x = vcache.view(nkv, cap // BLK, d // 16, 4, 16, 8)         # [h][b][d/16][kb/8][d%16][kb%8]
+    return x.permute(1, 3, 5, 0, 2, 4).reshape(cap, nkv, d)
 
 
 class Attention:

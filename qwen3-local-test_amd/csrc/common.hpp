@@ -108,9 +108,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // ---- K/V cache layout ------------------------------------------------------------------------------
-// Both caches are [cap/32][NKV][32*D] fp16: blocks of 32 positions, one 32*D part per KV head. Inside a
-// part the elements are ordered so that every MFMA operand fragment of the decode and prefill kernels
-// is one contiguous kilobyte (64 lanes x 16 bytes):
+// Both caches are [NKV][cap/32][32*D] fp16: per KV head, blocks of 32 positions, one 32*D part per block
+// (a head's blocks are contiguous, so a workgroup streaming one head's key range reads one contiguous
+// range). Inside a part the elements are ordered so that every MFMA operand fragment of the decode and
+// prefill kernels is one contiguous kilobyte (64 lanes x 16 bytes):
 //  K: (key kb, dim d) -> (((d/32)*2 + s)*4 + (d/8)%4)*16 + c)*8 + d%8 with c = (kb/8)*4 + kb%4,
 //     s = (kb/4)%2. Fragment (kk, s) of v_mfma_f32_16x16x32_f16's A operand — lane (c, g) holding key
 //     8*(c/4) + 4*s + c%4, dims 32*kk + 8*g .. +7 — is the kilobyte at (kk*2 + s) KB, and the score
@@ -128,9 +129,9 @@ __device__ __forceinline__ int v_off(int kb, int d) {
     return (((d >> 4) * 4 + (kb >> 3)) * 16 + (d & 15)) * 8 + (kb & 7);
 }
 
-// Element offset of (position p, KV head h) part start.
-__device__ __forceinline__ size_t kv_part(int p, int h, int NKV, int D) {
-    return ((size_t)(p >> 5) * NKV + h) * (size_t)(kBlk * D);
+// Element offset of the part holding (position p, KV head h) in a cache of capacity cap (a multiple of 32).
+__device__ __forceinline__ size_t kv_part(int p, int h, int cap, int D) {
+    return ((size_t)h * (cap >> 5) + (p >> 5)) * (size_t)(kBlk * D);
 }
 
 }  // namespace qw

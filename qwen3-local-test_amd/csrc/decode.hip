@@ -208,8 +208,8 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     // load zeros without touching memory, so every prefetch is issued unconditionally.
     const int load_end = min(ke, new_lo);
     const int nload = load_end > kb ? ((load_end - 1) >> 5) - (kb >> 5) + 1 : 0;
-    const int bstride = a.NKV * BLKE * 2;  // bytes between consecutive blocks of one head
-    const size_t part0 = ((size_t)(kb >> 5) * a.NKV + kvh) * BLKE;
+    const int bstride = BLKE * 2;  // bytes between consecutive blocks of one head
+    const size_t part0 = kv_part(kb, kvh, a.cap, D);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.kc) + part0, (short)0, nload * bstride, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         finish_row(nx, ncv, has_new, wk, y);  // computed by every half-wave, stored by the owners
         if (has_new) {
             const int p = a.pos + tn;
-            const size_t part = kv_part(p, kvh, a.NKV, D);
+            const size_t part = kv_part(p, kvh, a.cap, D);
             f16* kw = reinterpret_cast<f16*>(a.kc) + part;
             f16* vw = reinterpret_cast<f16*>(a.vc) + part;
             const int pb = p & (kBlk - 1), bi = (p >> 5) - (a.pos >> 5);
@@ -601,8 +601,8 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     // ---- loaders: the first two tiles of the pair go out at once ---------------------------------
     const int load_end = min(ke, new_lo);
     const int nload = load_end > kb ? ((load_end - 1) >> 5) - (kb >> 5) + 1 : 0;
-    const int bstride = a.NKV * BLKE * 2;  // bytes between consecutive blocks of one head
-    const size_t part0 = ((size_t)(kb >> 5) * a.NKV + kvh) * BLKE;
+    const int bstride = BLKE * 2;  // bytes between consecutive blocks of one head
+    const size_t part0 = kv_part(kb, kvh, a.cap, D);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.kc) + part0, (short)0, nload * bstride, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -726,7 +726,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                 finish_row(nx[ps], ncv[ps], tn < t_hi, wk, y);
                 if (tn < t_hi) {
                     const int p = a.pos + tn;
-                    const size_t part = kv_part(p, kvh, a.NKV, D);
+                    const size_t part = kv_part(p, kvh, a.cap, D);
                     f16* kw = reinterpret_cast<f16*>(a.kc) + part;
                     f16* vw = reinterpret_cast<f16*>(a.vc) + part;
                     const int pb = p & (kBlk - 1), nr = p - new_lo;  // new_lo = pos: row index of the new rows

@@ -20,6 +20,7 @@ struct NormRopeArgs {
     void* q_out;         // [n][NH][D] fp32, or fp16 pre-scaled by log2(e)/sqrt(D)
     int pos, n, NH, NKV, R;
     float eps, q_scale;
+    int cap;             // capacity (positions) of the caches
 };
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int D, int in_dtype, int q_dtype, hipStream_t s);
 
@@ -42,6 +43,7 @@ struct DecodeArgs {
     float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
                           // the same launch (nullptr: partials only, for a separate combine)
     int* arrive;          // with out: [NKV] arrival counters, zero before the launch and again after it
+    int cap;              // capacity (positions) of the caches kc, vc
 };
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 
@@ -62,6 +64,7 @@ struct PrefillArgs {
     float* out;           // [n][NH][D]
     int pos, n, NH, NKV;
     float q_scale;
+    int cap;              // capacity (positions) of the caches kc, vc
 };
 hipError_t launch_prefill(const PrefillArgs& a, int D, int q_dtype, int in_dtype, hipStream_t s);
 

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
                 *reinterpret_cast<f16v*>(static_cast<f16*>(a.q_out) + ((size_t)t * a.NH + h) * D + d0) = o;
             }
         } else {
-            const size_t part = kv_part(p, h, a.NKV, D);
+            const size_t part = kv_part(p, h, a.cap, D);
             f16* kc = reinterpret_cast<f16*>(a.kcache) + part;
             f16* vc = reinterpret_cast<f16*>(a.vcache) + part;
             const int kb = p & (kBlk - 1);

@@ -131,11 +131,11 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
 
     // ---- K/V staging: range-checked buffer loads of whole blocks of this KV head --------------------
     const int nblk = (maxlen + kBlk - 1) / kBlk;  // blocks holding written positions
-    const int bstride = a.NKV * BLKE * 2;         // bytes between consecutive blocks of one head
+    const int bstride = BLKE * 2;                 // bytes between consecutive blocks of one head
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.kc) + (size_t)kvh * BLKE, (short)0, nblk * bstride, 0x00020000);
+        const_cast<uint16_t*>(a.kc) + kv_part(0, kvh, a.cap, D), (short)0, nblk * bstride, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.vc) + (size_t)kvh * BLKE, (short)0, nblk * bstride, 0x00020000);
+        const_cast<uint16_t*>(a.vc) + kv_part(0, kvh, a.cap, D), (short)0, nblk * bstride, 0x00020000);
     // direct-to-LDS copy, piece i of tile kt: 16 bytes per lane, lane-linear, one kilobyte per
     // instruction; each wave copies every fourth kilobyte of the tile
     const int lane16 = lane * 16;

@@ -261,8 +261,9 @@ int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
     cap = (cap + 31) / 32 * 32;
     DeviceGuard dg(c->device);
     hipStream_t s = (hipStream_t)stream;
-    const size_t per = (size_t)c->cfg.n_kv_heads * c->cfg.head_dim * 2;
-    const size_t old_bytes = (size_t)c->kv_cap * per, bytes = (size_t)cap * per;
+    const int nkv = c->cfg.n_kv_heads;
+    const size_t per = (size_t)c->cfg.head_dim * 2;  // bytes per position and KV head
+    const size_t old_head = (size_t)c->kv_cap * per, new_head = (size_t)cap * per, bytes = nkv * new_head;
     for (size_t i = 0; i < c->kc.size(); i++) {
         uint16_t* nk = nullptr;
         uint16_t* nv = nullptr;
@@ -270,11 +271,18 @@ int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
             if (nk) (void)hipFree(nk);
             return fail(c, QWATTN_ENOMEM, "out of VRAM growing the K/V caches");
         }
-        // the blocked layout keeps whole 32-position blocks in order, so the old caches are a prefix
+        // the blocked layout keeps each KV head's 32-position blocks in order, so a head's old region is a
+        // prefix of its new one
         HIP_TRY(c, hipMemsetAsync(nk, 0, bytes, s));
         HIP_TRY(c, hipMemsetAsync(nv, 0, bytes, s));
-        HIP_TRY(c, hipMemcpyAsync(nk, c->kc[i], old_bytes, hipMemcpyDeviceToDevice, s));
-        HIP_TRY(c, hipMemcpyAsync(nv, c->vc[i], old_bytes, hipMemcpyDeviceToDevice, s));
+        for (int h = 0; h < nkv; h++) {
+            HIP_TRY(c, hipMemcpyAsync(reinterpret_cast<char*>(nk) + h * new_head,
+                                      reinterpret_cast<char*>(c->kc[i]) + h * old_head, old_head,
+                                      hipMemcpyDeviceToDevice, s));
+            HIP_TRY(c, hipMemcpyAsync(reinterpret_cast<char*>(nv) + h * new_head,
+                                      reinterpret_cast<char*>(c->vc[i]) + h * old_head, old_head,
+                                      hipMemcpyDeviceToDevice, s));
+        }
         HIP_TRY(c, hipStreamSynchronize(s));
         (void)hipFree(c->kc[i]);
         (void)hipFree(c->vc[i]);
@@ -309,7 +317,7 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* c, void* stream, const void* qg, cons
     const qwattn_config& g = c->cfg;
     qw::NormRopeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, q_out,
                        pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, g.rms_eps,
-                       qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+                       qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap};
     HIP_TRY(c, qw::launch_qk_norm_rope(a, g.head_dim, in_dtype, q_dtype == QWATTN_F16 ? 1 : 0, (hipStream_t)stream));
     return QWATTN_OK;
 }
@@ -329,7 +337,7 @@ int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const voi
     DeviceGuard dg(c->device);
     qw::DecodeArgs a{q, nullptr, nullptr, nullptr, nullptr, nullptr, (uint16_t*)kcache, (uint16_t*)vcache,
                      c->part_o, c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, kv_cap};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, false, QWATTN_F32, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -356,7 +364,7 @@ int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const voi
     DeviceGuard dg(c->device);
     qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
                      c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, kv_cap};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -386,7 +394,8 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     const bool one = n * G <= 8;
     qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
                      c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), one ? out : nullptr, one ? c->arrive : nullptr};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), one ? out : nullptr, one ? c->arrive : nullptr,
+                     kv_cap};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     if (!one) {
         qw::CombineArgs ca{c->part_o, c->part_ml, qg, out, n, g.n_heads, used};
@@ -424,7 +433,7 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     const qwattn_config& g = c->cfg;
     DeviceGuard dg(c->device);
     qw::PrefillArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, qg, out, pos, n, g.n_heads, g.n_kv_heads,
-                      qw::kLog2eHost / std::sqrt((float)g.head_dim)};
+                      qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap};
     HIP_TRY(c, qw::launch_prefill(a, g.head_dim, q_dtype == QWATTN_F16 ? 2 : 0, in_dtype, (hipStream_t)stream));
     return QWATTN_OK;
 }
