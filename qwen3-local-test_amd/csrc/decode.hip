@@ -608,9 +608,12 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.vc) + part0, (short)0, nload * bstride, 0x00020000);
     auto slot = [&](int i) { return ring + (pr * 2 + (i & 1)) * TILE_E; };
-    auto dma = [&](int i) {  // tile pr + NCW*i into slot i & 1 (range-checked: past nload, zeros)
+    // the pair's i-th tile, last block first: the block with the new positions is then the first one
+    // its loader patches, while the other tiles are still on their way, not the last one at the end
+    auto tile_of = [&](int i) { return pr + NCW * (ntp - 1 - i); };
+    auto dma = [&](int i) {  // the pair's i-th tile into slot i & 1 (range-checked: past nload, zeros)
         f16* dst = slot(i);
-        const int off = (pr + NCW * i) * bstride + lane * 16;
+        const int off = tile_of(i) * bstride + lane * 16;
 #pragma unroll
         for (int j = 0; j < PIECES; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(dst + j * 512), 16,
@@ -773,7 +776,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         for (int i = 0; i < ntp; i++) {
             if (i + 1 < ntp) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PIECES));  // tile i landed, i+1 may not
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            const int tb = kb + 32 * (pr + NCW * i);
+            const int tb = kb + 32 * tile_of(i);
             if (tb + 32 > new_lo) {
                 // keys from new_lo on: the new rows (fused) where they exist, else V = 0 over whatever the
                 // copy brought (stale or unwritten cache memory never reaches the sums; K needs no
@@ -850,7 +853,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             asm volatile("" ::: "memory");
             __hip_atomic_store(&freed[pr], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
-            const int tb = kb + 32 * (pr + NCW * i);
+            const int tb = kb + 32 * tile_of(i);
             // scores: sc[s][i] is key tb + 8g + 4s + i of column c (fp16 hi in columns 0-7, lo in 8-15)
             f32x4 sc[2];
 #pragma unroll
