@@ -69,110 +69,187 @@ __device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 
-// In-launch log-sum-exp combine (attn_combine.comp:13-29), run at the end of a decode workgroup whose
-// partials are written. The work is cut into units of one query row x 64 dims. Each workgroup counts its
-// arrival on its KV head's counter; the last NC = min(units, n_split) to arrive become the combiners:
-// combiner c waits (bounded) until every workgroup of the head has arrived, then merges units c, c + NC,
-// ... over all splits and writes them gated. Only those NC workgroups per head ever wait, and they wait
-// for workgroups that are already past their own arrival or still to be dispatched onto the slots every
-// other workgroup frees, so the wait always ends. The last combiner to finish puts the counter back to
-// zero for the next launch, so no clearing pass is needed (and none is recorded into a captured graph).
-// Launches that share a counter array must not overlap.
+// Merges a batch of split partials (m, l, o) into the running (M, L, O) (attn_combine.comp:17-26: the
+// max over the splits with keys, then each partial weighted by exp2(m - max)), in a fixed order and
+// without branches: with a branch per split the compiler sinks that split's loads into it and then waits
+// for them one split at a time, a memory round trip per split instead of one per batch. Bit k of `keys`
+// marks a split of the batch that exists and has keys (l > 0); the others weigh 0 (their o is finite).
+template <int B>
+__device__ __forceinline__ void merge_batch(float& M, float& L, f32x4& O, const float (&m)[B], const float (&l)[B],
+                                            const f32x4 (&o)[B], unsigned keys) {
+    float mx = M;  // -inf (with L = 0) before the first split with keys
+#pragma unroll
+    for (int k = 0; k < B; k++) mx = (keys >> k) & 1 ? fmaxf(mx, m[k]) : mx;
+    const float cf = L > 0.f ? exp2_fast(M - mx) : 0.f;
+    L *= cf;
+    O *= cf;
+#pragma unroll
+    for (int k = 0; k < B; k++) {
+        const float w = (keys >> k) & 1 ? exp2_fast(m[k] - mx) : 0.f;
+        L += l[k] * w;
+        O += o[k] * w;
+    }
+    M = mx;
+}
+
+// In-launch log-sum-exp combine (attn_combine.comp:13-29), run at the end of every workgroup of the
+// one-launch decode once its partials are stored. Each workgroup reads its KV head's epoch word, and once
+// its partial stores are acknowledged it sets its split's flag to epoch + 1 (this launch's epoch). The
+// workgroups of the last NC = min(units, n_split, comb_max) splits of a head are its combiners; the work
+// is cut into units of one query row x 64 dims and combiner c merges units c, c + NC, .... In a combiner,
+// wave 3 polls the head's flags (bounded; every lane a flag per 64 splits, one load per 64 flags) and
+// marks each split it sees set in LDS, while waves 0-2, a third of the splits each, wait on those marks
+// (LDS reads only, so the flag lines see one poller per combiner). Then every wave loads its partials,
+// lane (column c, split lane j) the splits j + 4k of each batch of 32, all loads of a batch issued before
+// any is used, merges them in split order, and the split lanes and then the waves merge in a fixed order,
+// so the result does not depend on arrival order. At most comb_max workgroups of a head wait, the host
+// keeps NKV * comb_max at half the CUs or below, and they wait only for workgroups that never wait, so
+// every wait ends. Each combiner then stores the launch's epoch into the head's epoch word: every
+// workgroup of the head read the word before setting its flag, so this launch's flags can never pass for
+// the next launch's, and no clearing pass is needed (none is recorded into a captured graph). Launches
+// that share the flag array must not overlap.
 template <int D, int IN_DT>
-__device__ __forceinline__ void combine_last(const DecodeArgs& a, int r0, int rows, int G, int kvh, int ctr) {
+__device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int G, int kvh, int z, int e) {
     constexpr int UD = 64;                 // dims of a unit
     constexpr int NUD = D / UD;            // units per row
-    constexpr int NSG = 256 / (UD / 4);    // split groups (16): thread tid takes splits tid % NSG + NSG * j
+    constexpr int NCOL = UD / 4;           // float4 columns of a unit (16)
+    constexpr int NSL = 64 / NCOL;         // split lanes per wave (4)
+    constexpr int BATCH = 32 / NSL;        // splits a lane takes per batch of 32 (8)
     static_assert(D % UD == 0, "head_dim must be a multiple of 64");
-    constexpr int BATCH = 8;
-    constexpr int SPIN_MAX = 1 << 22;
-    __shared__ int s_arrival;
-    const int tid = threadIdx.x;
+    constexpr int SPIN_MAX = 1 << 20;
+    __shared__ float s_wave[4][NCOL][6];            // each wave's (M, L, O) per column
+    __shared__ unsigned char s_seen[kReadyMaxSplits];  // split's flag seen set by the polling wave
+    // wave index through readfirstlane: the compiler then knows it (and the split range and buffer
+    // descriptors derived from it) to be wave-uniform, and keeps the descriptors in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int S = a.n_split;
-    // the partials went out as device-coherent stores: once acknowledged they are visible to every
-    // workgroup's device-coherent loads, so completing them is the whole release (no cache write-back)
+    int* epoch = a.ready + kvh;  // e: this launch's epoch, the word + 1 (read at the kernel start)
+    int* flags = a.ready + ready_flags_at(a.NKV) + (size_t)kvh * ready_stride(S);
+    for (int i = tid; i < S; i += 256) s_seen[i] = 0;
+    // the partials went out as device-coherent stores: once every wave's stores are acknowledged they are
+    // visible to every workgroup's device-coherent loads, so completing them is the whole release (no
+    // cache write-back)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
-    if (tid == 0) s_arrival = __hip_atomic_fetch_add(&a.arrive[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
+    if (tid == 0) __hip_atomic_store(flags + z, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int units = rows * NUD;
-    const int NC = min(units, S);
-    const int ci = s_arrival - (S - NC);
+    const int NC = min(min(units, S), a.comb_max);
+    const int ci = z - (S - NC);
     if (ci < 0) return;
-    // 16 consecutive lanes hold the 16 split groups of one float4 column: the final merge is a butterfly
-    // inside those lanes (no LDS, no barrier)
-    const int sg = tid % NSG, col = tid / NSG;
-    auto gate_of = [&](int u, float (&gt)[4]) {  // the gate does not depend on the other workgroups
-        const int r = r0 + u / NUD, t = r / G, h = kvh * G + r % G;
+    const int col = lane % NCOL, sl = lane / NCOL;
+    auto gate_of = [&](int u, float (&gt)[4]) {  // the output gate of unit u: wave 0 applies it
+        const int r = u / NUD, t = r / G, h = kvh * G + r % G;
         const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + (u % NUD) * UD + col * 4;
 #pragma unroll
         for (int i = 0; i < 4; i++) gt[i] = load_in<IN_DT>(a.q, gb + i);
     };
-    float gate[4];
-    gate_of(ci, gate);
-    if (tid == 0) {
-        for (int spin = 0; __hip_atomic_load(&a.arrive[ctr], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S &&
-                           spin < SPIN_MAX;
-             spin++)
-            __builtin_amdgcn_s_sleep(2);
+    float gate[4] = {0.f, 0.f, 0.f, 0.f};
+    if (wave == 0) gate_of(ci, gate);  // issued now, in by the time the partials are
+    // LDS accesses the compiler cannot see: one it can see makes it wait for every outstanding load first
+    const uint32_t seen_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_seen));
+    // waves 0-2: a third of the splits each (the polling wave takes none)
+    const int Q3 = (S + 2) / 3;
+    const int zb = wave < 3 ? min(S, wave * Q3) : S, ze = wave < 3 ? min(S, zb + Q3) : S;
+    if (wave == 3) {
+        // the polling wave: lane l watches the flags l + 64 j (j < 8 per round of loads)
+        const int J = (S + 63) / 64;
+        for (int j0 = 0; j0 < J; j0 += 8) {
+            unsigned todo = 0;  // bit k: flag lane + 64 (j0 + k) not seen yet
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (j0 + k < J && lane + 64 * (j0 + k) < S) todo |= 1u << k;
+            for (int spin = 0; __ballot(todo != 0) != 0; spin++) {
+                int f[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    f[k] = (todo >> k) & 1 ? __hip_atomic_load(flags + lane + 64 * (j0 + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if (((todo >> k) & 1) && (f[k] == e || spin >= SPIN_MAX)) {
+                        asm volatile("ds_write_b8 %0, %1" ::"v"(seen_at + lane + 64 * (j0 + k)), "v"(1) : "memory");
+                        todo &= ~(1u << k);
+                    }
+                if (todo != 0) __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    } else {
+        // waves 0-2 wait until the polling wave has seen the flags of all their splits: lane l checks the
+        // splits zb + l + 64 j (a short loop of LDS reads only)
+        for (int spin = 0; spin < 4 * SPIN_MAX; spin++) {
+            int missing = 0;
+            for (int zz = zb + lane; zz < ze; zz += 64) {
+                uint32_t sn;
+                asm volatile("ds_read_u8 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(sn) : "v"(seen_at + zz) : "memory");
+                missing |= sn == 0;
+            }
+            if (__ballot(missing) == 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
     }
-    __syncthreads();
+    // every partial of the head is visible from here on: merge the units
     for (int u = ci; u < units; u += NC) {
-        if (u != ci) gate_of(u, gate);
-        const int r = r0 + u / NUD, t = r / G, h = kvh * G + r % G;
+        const int r = u / NUD, t = r / G, h = kvh * G + r % G;
         const int d0 = (u % NUD) * UD + col * 4;
+        if (u != ci && wave == 0) gate_of(u, gate);
         const size_t row = ((size_t)t * a.NH + h) * S;
         // device-coherent loads: the other workgroups' stores, never a stale line of this XCD's L2
         const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + row * 2, (short)0, S * 8, 0x00020000);
         const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + row * D, (short)0, S * D * 4, 0x00020000);
         float M = kNegInf, L = 0.f;
         f32x4 O = {0.f, 0.f, 0.f, 0.f};
-        for (int z0 = sg; z0 < S; z0 += NSG * BATCH) {
+        for (int b0 = zb; b0 < ze; b0 += 32) {  // wave-uniform; every load of a batch is issued before any is used
             float m[BATCH], l[BATCH];
             f32x4 o[BATCH];
 #pragma unroll
-            for (int k = 0; k < BATCH; k++) {  // every load of the batch is issued before any is used
-                const int zz = min(z0 + NSG * k, S - 1);
+            for (int k = 0; k < BATCH; k++) {
+                const int zz = min(b0 + sl + NSL * k, ze - 1);
                 const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, zz * 8, 0, kScDevice));
                 m[k] = ml[0];
                 l[k] = ml[1];
                 o[k] = __builtin_amdgcn_raw_buffer_load_b128(ro, (zz * D + d0) * 4, 0, kScDevice);
             }
+            __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the first wait
+            unsigned keys = 0;
 #pragma unroll
-            for (int k = 0; k < BATCH; k++) {
-                if (z0 + NSG * k < S && l[k] > 0.f) {
-                    const float mn = fmaxf(M, m[k]);
-                    const float cf = exp2_fast(M - mn), cu = exp2_fast(m[k] - mn);
-                    L = L * cf + l[k] * cu;
-                    O = O * cf + o[k] * cu;
-                    M = mn;
-                }
-            }
+            for (int k = 0; k < BATCH; k++) keys |= (b0 + sl + NSL * k < ze && l[k] > 0.f ? 1u : 0u) << k;
+            merge_batch(M, L, O, m, l, o, keys);
         }
-#pragma unroll
-        for (int x = 1; x < NSG; x <<= 1) {  // merge with the lane x away (L = 0: nothing to merge)
-            const float Mo = __shfl_xor(M, x, 64), Lo = __shfl_xor(L, x, 64);
-            f32x4 Oo;
-#pragma unroll
-            for (int i = 0; i < 4; i++) Oo[i] = __shfl_xor(O[i], x, 64);
+        auto merge = [&](float Mo, float Lo, f32x4 Oo) {  // L = 0: nothing to merge
             const float mn = fmaxf(M, Mo);
             const float cf = L > 0.f ? exp2_fast(M - mn) : 0.f, co = Lo > 0.f ? exp2_fast(Mo - mn) : 0.f;
             L = L * cf + Lo * co;
             O = O * cf + Oo * co;
             M = mn;
+        };
+#pragma unroll
+        for (int x = NCOL; x < 64; x <<= 1) {  // the wave's split lanes
+            f32x4 Oo;
+#pragma unroll
+            for (int i = 0; i < 4; i++) Oo[i] = __shfl_xor(O[i], x, 64);
+            merge(__shfl_xor(M, x, 64), __shfl_xor(L, x, 64), Oo);
         }
-        if (sg == 0) {
+        if (sl == 0 && wave > 0 && wave < 3) {
+            s_wave[wave][col][0] = M, s_wave[wave][col][1] = L;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_wave[wave][col][2 + i] = O[i];
+        }
+        __syncthreads();
+        if (wave == 0 && sl == 0) {  // waves 1 and 2, in order
+#pragma unroll
+            for (int w = 1; w < 3; w++)
+                merge(s_wave[w][col][0], s_wave[w][col][1],
+                      f32x4{s_wave[w][col][2], s_wave[w][col][3], s_wave[w][col][4], s_wave[w][col][5]});
             const float inv = 1.0f / L;
             f32x4 res;
 #pragma unroll
             for (int i = 0; i < 4; i++) res[i] = O[i] * inv * sigmoid(gate[i]);
             *reinterpret_cast<f32x4*>(&a.out[((size_t)t * a.NH + h) * D + d0]) = res;
         }
+        __syncthreads();  // s_wave is rewritten by the next unit
     }
-    // the last combiner to finish re-arms the counter (every combiner is past its wait by then)
-    __syncthreads();
-    if (tid == 0 && __hip_atomic_fetch_add(&a.arrive[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S + NC - 1)
-        __hip_atomic_store(&a.arrive[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every flag of the head has been seen by the polling wave: advance the head's epoch (every combiner
+    // stores the same value)
+    if (tid == 0) __hip_atomic_store(epoch, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int FUSED, int IN_DT>
@@ -589,6 +666,15 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     const int G = a.NH / a.NKV;
     const int rows = min(RMAX, a.n * G);
     const int maxlen = a.pos + a.n;
+    // the in-launch combine's epoch word of this KV head, read now (device-coherent, unconditionally: a
+    // zero-sized range without the combine reads 0 and touches no memory) so that its latency hides behind
+    // the prologue; it must be read before this workgroup sets its ready flag
+    int epoch_word = 0;
+    if constexpr (FUSED) {
+        const bool comb = a.out != nullptr;
+        const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(comb ? a.ready + kvh : a.ready, (short)0, comb ? 4 : 0, 0x00020000);
+        epoch_word = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, kScDevice);
+    }
     const int kb = z * a.chunk;
     const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, kb + a.chunk);
     const int ntile_wg = (ke - kb + 31) >> 5;
@@ -956,7 +1042,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         __builtin_amdgcn_raw_buffer_store_b128(o, rpo, (row * D + d) * 4, 0, kScDevice);
     }
     if constexpr (FUSED) {
-        if (a.out != nullptr) combine_last<D, IN_DT>(a, 0, rows, G, kvh, kvh);
+        if (a.out != nullptr) combine_ready<D, IN_DT>(a, rows, G, kvh, z, epoch_word + 1);
     }
 }
 
@@ -969,9 +1055,10 @@ template <int D, int FUSED, int IN_DT>
 static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
     const dim3 block(256);
-    // the in-launch combine: fused (it needs the gate) and at most 8 rows (the 16-row kernel has no
-    // registers left for it)
-    if (a.out != nullptr && (!FUSED || rows > 8)) return hipErrorInvalidValue;
+    // the in-launch combine: fused (it needs the gate), at most 8 rows (the 16-row kernel has no
+    // registers left for it) and at most kReadyMaxSplits splits
+    if (a.out != nullptr && (!FUSED || rows > 8 || a.n_split > kReadyMaxSplits || a.comb_max < 1))
+        return hipErrorInvalidValue;
     if (rows <= 8) {
         auto kern = k_decode_ld<D, FUSED, IN_DT>;
         const size_t shm = decode_ld_lds<D>();
@@ -1006,8 +1093,8 @@ hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, h
 
 // ---- combine ---------------------------------------------------------------------------------------
 // One workgroup per (row, 64-dim slice): 16 split lanes x 16 dim lanes of 4 dims. Each thread merges
-// the splits z = zg, zg + 16, ... with an online (m, l, o) update, loading a batch of 8 splits before
-// using any; the 16 thread-partials of a dim group then merge through LDS. Splits with l = 0 are
+// the splits z = zg, zg + 16, ... in batches of 8 (all loads of a batch issued before any is used,
+// merge_batch); the 16 thread-partials of a dim group then merge through LDS. Splits with l = 0 are
 // skipped (attn_combine.comp:17-26).
 template <int IN_DT>
 __global__ __launch_bounds__(256) void k_combine(CombineArgs a, int D) {
@@ -1021,6 +1108,15 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a, int D) {
     const int d0 = blockIdx.y * 64 + q * 4;
     const float* ml = a.part_ml + (size_t)row * S * 2;
     const float* po = a.part_o + (size_t)row * S * D + d0;
+    // the output gate, loaded up front: loads next to the output stores (which might alias them, as far
+    // as the compiler knows) would each wait for the one before
+    float gate[4];
+    {
+        const int t = row / a.NH, h = row % a.NH;
+        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + d0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) gate[i] = zg == 0 ? load_in<IN_DT>(a.qg, gb + i) : 0.f;
+    }
 
     float M = kNegInf, L = 0.f;
     f32x4 O = {0.f, 0.f, 0.f, 0.f};
@@ -1034,16 +1130,11 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a, int D) {
             l[u] = ml[2 * zz + 1];
             o[u] = *reinterpret_cast<const f32x4*>(po + (size_t)zz * D);
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the first wait
+        unsigned keys = 0;
 #pragma unroll
-        for (int u = 0; u < BATCH; u++) {
-            if (z0 + 16 * u < S && l[u] > 0.f) {
-                const float mn = fmaxf(M, m[u]);
-                const float cf = exp2_fast(M - mn), cu = exp2_fast(m[u] - mn);
-                L = L * cf + l[u] * cu;
-                O = O * cf + o[u] * cu;
-                M = mn;
-            }
-        }
+        for (int u = 0; u < BATCH; u++) keys |= (z0 + 16 * u < S && l[u] > 0.f ? 1u : 0u) << u;
+        merge_batch(M, L, O, m, l, o, keys);
     }
     sMt[zg][q] = M;
     sLt[zg][q] = L;
@@ -1064,12 +1155,11 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a, int D) {
                 Os += sOt[k][q] * f;
             }
         }
-        const int t = row / a.NH, h = row % a.NH;
-        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + d0;
-        float* out = a.out + (size_t)row * D + d0;
         const float inv = 1.0f / Ls;
+        f32x4 res;
 #pragma unroll
-        for (int i = 0; i < 4; i++) out[i] = Os[i] * inv * sigmoid(load_in<IN_DT>(a.qg, gb + i));
+        for (int i = 0; i < 4; i++) res[i] = Os[i] * inv * sigmoid(gate[i]);
+        *reinterpret_cast<f32x4*>(a.out + (size_t)row * D + d0) = res;
     }
 }
 

@@ -42,10 +42,21 @@ struct DecodeArgs {
     float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
     float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
                           // the same launch (nullptr: partials only, for a separate combine)
-    int* arrive;          // with out: [NKV] arrival counters, zero before the launch and again after it
+    int* ready;           // with out: epoch words and ready flags (ready_ints(NKV, n_split) ints, zero at first)
+    int comb_max;         // with out: combining workgroups per KV head at most (NKV * comb_max <= CUs / 2)
     int cap;              // capacity (positions) of the caches kc, vc
 };
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
+
+// Splits at most of the one-launch decode (its combiners track the splits in LDS)
+constexpr int kReadyMaxSplits = 2048;
+// Layout of DecodeArgs::ready (ints): the KV heads' epoch words first, then per KV head one flag per
+// split; the flags start on a 128-byte line and every head's flags take whole lines.
+__host__ __device__ constexpr int ready_flags_at(int NKV) { return (NKV + 31) / 32 * 32; }
+__host__ __device__ constexpr int ready_stride(int n_split) { return (n_split + 31) / 32 * 32; }
+__host__ __device__ constexpr size_t ready_ints(int NKV, int max_splits) {
+    return (size_t)ready_flags_at(NKV) + (size_t)NKV * ready_stride(max_splits);
+}
 
 struct CombineArgs {
     const float* part_o;

@@ -25,7 +25,7 @@ struct qwattn_ctx {
     float* rope = nullptr;       // [max_ctx][R/2][2]
     float* part_o = nullptr;     // [split_rows][max_splits][D]
     float* part_ml = nullptr;    // [split_rows][max_splits][2]
-    int* arrive = nullptr;       // [NKV] arrival counters of qwattn_decode (zero between launches)
+    int* ready = nullptr;        // qwattn_decode: epoch words and per-split ready flags (qw::ready_ints)
     float* q32 = nullptr;        // [max_tokens][NH][D] layer-path query (fp32)
     void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
@@ -173,7 +173,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->rope, sizeof(float) * rope_n) == hipSuccess &&
               hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
               hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
-              hipMalloc(&c->arrive, sizeof(int) * NKV) == hipSuccess &&
+              hipMalloc(&c->ready, sizeof(int) * qw::ready_ints(NKV, cfg->max_splits)) == hipSuccess &&
               hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess;
     if (!ok) {
         qwattn_destroy(c);
@@ -185,7 +185,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     if (hipMemcpy(c->inv_freq, inv.data(), sizeof(float) * inv.size(), hipMemcpyHostToDevice) != hipSuccess ||
         (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
         hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
-        hipMemset(c->arrive, 0, sizeof(int) * NKV) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipMemset(c->ready, 0, sizeof(int) * qw::ready_ints(NKV, cfg->max_splits)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
     }
@@ -197,7 +197,7 @@ int qwattn_destroy(qwattn_ctx* c) {
     if (!c) return QWATTN_OK;
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
-    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->arrive,
+    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ready,
                     (void*)c->q32, c->q16})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
@@ -337,7 +337,7 @@ int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const voi
     DeviceGuard dg(c->device);
     qw::DecodeArgs a{q, nullptr, nullptr, nullptr, nullptr, nullptr, (uint16_t*)kcache, (uint16_t*)vcache,
                      c->part_o, c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, kv_cap};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, 0, kv_cap};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, false, QWATTN_F32, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -364,7 +364,7 @@ int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const voi
     DeviceGuard dg(c->device);
     qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
                      c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, kv_cap};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, 0, kv_cap};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -390,12 +390,14 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     pick_split(c, pos + n, n, n_split, &chunk, &used);
     DeviceGuard dg(c->device);
     // up to 8 query rows the combine runs inside the attend launch; the 16-row-slice kernel (verify) is
-    // followed by the combine kernel
-    const bool one = n * G <= 8;
+    // followed by the combine kernel. In-launch combiners wait for other workgroups: at most half the CUs
+    // may hold one, so the others always have room to run
+    const int comb_max = c->n_cu / 2 / g.n_kv_heads;
+    const bool one = n * G <= 8 && comb_max >= 1 && used <= qw::kReadyMaxSplits;
     qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
                      c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), one ? out : nullptr, one ? c->arrive : nullptr,
-                     kv_cap};
+                     qw::kLog2eHost / std::sqrt((float)g.head_dim), one ? out : nullptr, one ? c->ready : nullptr,
+                     comb_max, kv_cap};
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     if (!one) {
         qw::CombineArgs ca{c->part_o, c->part_ml, qg, out, n, g.n_heads, used};
