@@ -32,9 +32,9 @@
 //  - Scores are in log2 units (q pre-multiplied by log2(e)/sqrt(D)), so exponentials are v_exp_f32.
 //  - Fused form: every workgroup normalizes and rotates its own query rows (RMSNorm (1+w) + partial
 //    RoPE, while its first tiles are in flight), and the workgroup whose chunk holds the n new positions
-//    normalizes/rotates their K rows, writes K and V to the cache for later steps, and patches them into
-//    its loaded tiles — so one launch does the work of the reference's qk_norm_rope + attention
-//    dispatches.
+//    normalizes/rotates their K rows, writes K and V to the cache and attends over them (the decode
+//    kernel copies their block once the stores are complete, the verify kernel patches them into its
+//    loaded tiles) — so one launch does the work of the reference's qk_norm_rope + attention dispatches.
 //  - The combine runs one workgroup per (row, 64-dim slice) with every partial load of a batch issued
 //    before any is used.
 #include <atomic>
@@ -630,11 +630,13 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
 // With HBM saturated, issuing a load stalls the issuing wave until earlier requests drain, so a wave that
 // both streams and computes spends most of the stream blocked with data it could be using. Here the
 // workgroup's waves 0-1 only compute and waves 2-3 only stream: loader wave 2 + p copies compute wave
-// p's tiles (tiles p, p + 2, ...) with direct-to-LDS loads into two 32-key slots, patches the new
-// positions (fresh K/V rows, zero V past the last position) into the slot that holds them, and publishes
-// each tile through an LDS counter; the compute wave copies the slot into registers, frees it at once and
-// computes, so two tiles per pair are in flight while one is being computed. Spin waits are bounded, so
-// every wave exits even if a counter were never reached.
+// p's tiles (tiles p, p + 2, ...) with direct-to-LDS loads into two 32-key slots and publishes each tile
+// through an LDS counter; the compute wave copies the slot into registers, frees it at once and
+// computes, so two tiles per pair are in flight while one is being computed. The new positions are
+// appended to the caches in the prologue and a tile holding them is copied only after those stores are
+// acknowledged, so it arrives complete (no patching in LDS: LDS stores crawl while the first copies
+// land); V past the last position is zeroed in registers. Spin waits are bounded, so every wave exits
+// even if a counter were never reached.
 template <int D, int FUSED, int IN_DT>
 __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     constexpr int NKS = D / 32, NDT = D / 16, RMAX = 8, BLKE = kBlk * D;
@@ -652,7 +654,6 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     f16* ring = reinterpret_cast<f16*>(smem);                 // [NCW][2][TILE_E]
     f16* s_q = ring + NCW * 2 * TILE_E;                        // Q fragments (hi rows 0-7, lo rows 8-15)
-    f16* s_new = s_q + NKS * 64 * 8;                           // new rows: [K, V][8][D]
     // tile counters in a separate LDS object: an access the compiler cannot tell apart from the
     // direct-to-LDS copies' destination makes it wait for every outstanding copy first
     __shared__ int s_cnt[2 * NCW];
@@ -681,12 +682,13 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     const bool loader = wave >= NCW;
     const int pr = loader ? wave - NCW : wave;                        // pair
     const int ntp = ntile_wg > pr ? (ntile_wg - pr + NCW - 1) / NCW : 0;  // tiles pr, pr + NCW, ...
-    const int new_lo = FUSED ? a.pos : maxlen;                        // first position not read from the cache
+    // first new position: the prologue appends the new rows to the caches, and a tile holding any of them
+    // is copied only once those stores are complete (after the prologue), so it arrives whole
+    const int new_lo = FUSED ? a.pos : maxlen;
     if (tid < 2 * NCW) ready[tid] = 0;  // ready[] and freed[] (published by the barrier below)
 
     // ---- loaders: the first two tiles of the pair go out at once ---------------------------------
-    const int load_end = min(ke, new_lo);
-    const int nload = load_end > kb ? ((load_end - 1) >> 5) - (kb >> 5) + 1 : 0;
+    const int nload = ke > kb ? ((ke - 1) >> 5) - (kb >> 5) + 1 : 0;
     const int bstride = BLKE * 2;  // bytes between consecutive blocks of one head
     const size_t part0 = kv_part(kb, kvh, a.cap, D);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
@@ -694,9 +696,8 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.vc) + part0, (short)0, nload * bstride, 0x00020000);
     auto slot = [&](int i) { return ring + (pr * 2 + (i & 1)) * TILE_E; };
-    // the pair's i-th tile, last block first: the block with the new positions is then the first one
-    // its loader patches, while the other tiles are still on their way, not the last one at the end
-    auto tile_of = [&](int i) { return pr + NCW * (ntp - 1 - i); };
+    auto tile_of = [&](int i) { return pr + NCW * i; };        // the pair's i-th tile of the workgroup
+    auto has_new = [&](int i) { return FUSED && kb + 32 * tile_of(i) + 32 > new_lo; };  // holds new positions
     auto dma = [&](int i) {  // the pair's i-th tile into slot i & 1 (range-checked: past nload, zeros)
         f16* dst = slot(i);
         const int off = tile_of(i) * bstride + lane * 16;
@@ -818,21 +819,22 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                     const size_t part = kv_part(p, kvh, a.cap, D);
                     f16* kw = reinterpret_cast<f16*>(a.kc) + part;
                     f16* vw = reinterpret_cast<f16*>(a.vc) + part;
-                    const int pb = p & (kBlk - 1), nr = p - new_lo;  // new_lo = pos: row index of the new rows
+                    const int pb = p & (kBlk - 1);
 #pragma unroll
                     for (int jj = 0; jj < DPL2; jj++) {
                         const int d = d0 + jj;
-                        const f16 kh = (f16)y[jj];
-                        const f16 vh = (f16)nv[ps][jj];
-                        s_new[nr * D + d] = kh;
-                        s_new[(8 + nr) * D + d] = vh;
-                        kw[k_off(pb, d)] = kh;
-                        vw[v_off(pb, d)] = vh;
+                        kw[k_off(pb, d)] = (f16)y[jj];
+                        vw[v_off(pb, d)] = (f16)nv[ps][jj];
                     }
                 }
             }
+            // the appended rows are complete (in this XCD's L2, which the copies of their tiles read)
+            // before the barrier below, after which those tiles are copied. Waiting here beats every
+            // alternative measured: stores issued now are acknowledged only behind the copies in flight,
+            // and any wave that waits for them later stalls a tile instead.
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): s_q, s_new and the counters are in LDS
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): s_q and the counters are in LDS
     } else {
         // wait until the compute waves' row loads are issued, then put the first two tiles in flight
         // behind them: issued any earlier, the copies would queue the row loads behind the whole stream
@@ -841,11 +843,13 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
-        if (ntp > 0) dma(0);
-        if (ntp > 1) dma(1);
+        // a tile holding new positions waits until they are appended (after the prologue); such tiles
+        // are the pair's last, so the copies still go out in tile order
+        if (ntp > 0 && !has_new(0)) dma(0);
+        if (ntp > 1 && !has_new(1)) dma(1);
     }
-    // a bare barrier: the LDS writes above are complete (the compute waves waited for them), and a
-    // fenced one would also wait for the copies in flight and the cache-row stores
+    // a bare barrier: the LDS writes and cache-row stores above are complete (the compute waves waited
+    // for them), and a fenced one would also wait for the copies in flight
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
@@ -858,42 +862,12 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (loader) {
-        // ---- stream the pair's tiles; publish each once landed (and patched) -----------------------
+        // ---- stream the pair's tiles; publish each once landed -------------------------------------
+        if (ntp > 0 && has_new(0)) dma(0);  // the tiles the prologue held back, in tile order
+        if (ntp > 1 && has_new(1)) dma(1);
         for (int i = 0; i < ntp; i++) {
             if (i + 1 < ntp) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PIECES));  // tile i landed, i+1 may not
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            const int tb = kb + 32 * tile_of(i);
-            if (tb + 32 > new_lo) {
-                // keys from new_lo on: the new rows (fused) where they exist, else V = 0 over whatever the
-                // copy brought (stale or unwritten cache memory never reaches the sums; K needs no
-                // clearing there, those scores are masked).
-                f16* sl = slot(i);
-                const int k_from = max(new_lo - tb, 0);               // first patched key of the block
-                const int k_new_end = FUSED ? min(maxlen - tb, 32) : k_from;  // new keys: [k_from, k_new_end)
-                const int n_new = k_new_end - k_from;
-                // K of the new keys: (key, 8-dim group) pieces of 16 bytes, row layout -> block layout
-                for (int idx = lane; idx < n_new * (D / 8); idx += 64) {
-                    const int key = k_from + idx / (D / 8), d8 = (idx % (D / 8)) * 8;
-                    *reinterpret_cast<f16x8*>(&sl[k_off(key, d8)]) =
-                        *reinterpret_cast<const f16x8*>(&s_new[(tb + key - new_lo) * D + d8]);
-                }
-                // V: zeros over keys [k_from, 32) (whole 8-key groups as 16-byte stores, the partial group
-                // key by key), then the new keys' values; one wave's LDS stores land in issue order. Plain
-                // loops on purpose: this runs once per launch, and unrolled select code would be fetched
-                // cold into the instruction cache at several microseconds.
-                const int g_from = k_from >> 3;
-#pragma nounroll
-                for (int d = lane; d < D; d += 64) {
-#pragma nounroll
-                    for (int key = k_from; key < (g_from + 1) * 8 && key < 32; key++) sl[BLKE + v_off(key, d)] = (f16)0.f;
-#pragma nounroll
-                    for (int gg = g_from + 1; gg < 4; gg++) *reinterpret_cast<f16x8*>(&sl[BLKE + v_off(gg * 8, d)]) = f16x8{};
-#pragma nounroll
-                    for (int key = k_from; key < k_new_end; key++)
-                        sl[BLKE + v_off(key, d)] = s_new[(8 + tb + key - new_lo) * D + d];
-                }
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the patch is in LDS
-            }
             // publish: the waits above already order the tile before the counter, and a release store
             // would also wait for the next tile's loads (the whole load counter), halving the pipeline
             {
@@ -903,6 +877,9 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                 asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(i + 1) : "memory");
             }
             if (i + 2 < ntp) {
+                // a tile with new positions (the pair's last) goes out only once the appends are complete:
+                // wait for everything this wave has in flight
+
                 // wait for the compute wave to free the slot; read through inline assembly as well, since
                 // an LDS read the compiler can see would first wait for all of this wave's copies
                 const uint32_t faddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&freed[pr]));
@@ -940,6 +917,17 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             __hip_atomic_store(&freed[pr], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
             const int tb = kb + 32 * tile_of(i);
+            if (tb + 32 > maxlen) {
+                // keys from maxlen on: their scores are masked, but V there is whatever the cache memory
+                // holds (P = 0 there, and 0 * NaN is not 0): zero it. V fragment dt: lane (c, g) holds
+                // keys 8 g .. 8 g + 7 of dim 16 dt + c, two keys per 32-bit word
+                const int nvk = min(max(maxlen - tb - 8 * g, 0), 8);
+                u32x4 keep;
+#pragma unroll
+                for (int w = 0; w < 4; w++) keep[w] = (2 * w < nvk ? 0xFFFFu : 0u) | (2 * w + 1 < nvk ? 0xFFFF0000u : 0u);
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) vt[dt] = as_h8(as_u4(vt[dt]) & keep);
+            }
             // scores: sc[s][i] is key tb + 8g + 4s + i of column c (fp16 hi in columns 0-7, lo in 8-15)
             f32x4 sc[2];
 #pragma unroll
@@ -1048,7 +1036,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
 
 template <int D>
 constexpr size_t decode_ld_lds() {
-    return (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2 + (size_t)2 * 8 * D * 2;
+    return (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2;  // ring + Q fragments
 }
 
 template <int D, int FUSED, int IN_DT>
