@@ -146,10 +146,12 @@ int qwattn_decode_partial(qwattn_ctx* ctx, void* stream, const void* qg, const v
 
 /* All three of the reference's decode dispatches (src/qwen4_vk.cpp:968-992: qk_norm_rope,
  * attention, attn_combine): qwattn_decode_partial followed, inside the same kernel, by the log-sum-exp
- * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. The last workgroups of each KV
- * head to finish merge the split partials; arrival counters in the context re-arm themselves at the end
- * of every launch, so the call allocates and clears nothing and can be captured into a graph. Calls on
- * one context must not overlap (one stream, or ordered streams). Same limits as qwattn_decode_partial
+ * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. The workgroups of the last
+ * splits of each KV head merge the split partials once every split's ready flag (in the context, tagged
+ * with a per-launch epoch) is set; nothing needs clearing between launches, so the call allocates and
+ * clears nothing and can be captured into a graph. Calls on one context must not overlap (one stream,
+ * or ordered streams). The merge order is fixed, so the output does not depend on which workgroup
+ * finishes first. Same limits as qwattn_decode_partial
  * (n <= 8, n * NH/NKV <= 32: decode and MTP verify); one launch for n * NH/NKV <= 8, above that (verify)
  * the attend launch is followed by the combine launch. */
 int qwattn_decode(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
