@@ -124,7 +124,7 @@ __device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int S = a.n_split;
     int* epoch = a.ready + kvh;  // e: this launch's epoch, the word + 1 (read at the kernel start)
-    int* flags = a.ready + ready_flags_at(a.NKV) + (size_t)kvh * ready_stride(S);
+    int* flags = a.ready + ready_flags_at(a.NKV) + (size_t)kvh * kReadyMaxSplits;
     for (int i = tid; i < S; i += 256) s_seen[i] = 0;
     // the partials went out as device-coherent stores: once every wave's stores are acknowledged they are
     // visible to every workgroup's device-coherent loads, so completing them is the whole release (no

@@ -42,7 +42,7 @@ struct DecodeArgs {
     float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
     float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
                           // the same launch (nullptr: partials only, for a separate combine)
-    int* ready;           // with out: epoch words and ready flags (ready_ints(NKV, n_split) ints, zero at first)
+    int* ready;           // with out: epoch words and ready flags (ready_ints(NKV) ints, zero at first)
     int comb_max;         // with out: combining workgroups per KV head at most (NKV * comb_max <= CUs / 2)
     int cap;              // capacity (positions) of the caches kc, vc
 };
@@ -50,12 +50,12 @@ hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, h
 
 // Splits at most of the one-launch decode (its combiners track the splits in LDS)
 constexpr int kReadyMaxSplits = 2048;
-// Layout of DecodeArgs::ready (ints): the KV heads' epoch words first, then per KV head one flag per
-// split; the flags start on a 128-byte line and every head's flags take whole lines.
+// Layout of DecodeArgs::ready (ints): the KV heads' epoch words first, then per KV head a fixed region
+// of kReadyMaxSplits flags (line-aligned). A head keeps its word and region whatever the splits of a
+// launch, so every flag location only ever holds epochs of its own head, all below the head's current one.
 __host__ __device__ constexpr int ready_flags_at(int NKV) { return (NKV + 31) / 32 * 32; }
-__host__ __device__ constexpr int ready_stride(int n_split) { return (n_split + 31) / 32 * 32; }
-__host__ __device__ constexpr size_t ready_ints(int NKV, int max_splits) {
-    return (size_t)ready_flags_at(NKV) + (size_t)NKV * ready_stride(max_splits);
+__host__ __device__ constexpr size_t ready_ints(int NKV) {
+    return (size_t)ready_flags_at(NKV) + (size_t)NKV * kReadyMaxSplits;
 }
 
 struct CombineArgs {

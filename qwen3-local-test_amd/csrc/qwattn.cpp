@@ -173,7 +173,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->rope, sizeof(float) * rope_n) == hipSuccess &&
               hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
               hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
-              hipMalloc(&c->ready, sizeof(int) * qw::ready_ints(NKV, cfg->max_splits)) == hipSuccess &&
+              hipMalloc(&c->ready, sizeof(int) * qw::ready_ints(NKV)) == hipSuccess &&
               hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess;
     if (!ok) {
         qwattn_destroy(c);
@@ -185,7 +185,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     if (hipMemcpy(c->inv_freq, inv.data(), sizeof(float) * inv.size(), hipMemcpyHostToDevice) != hipSuccess ||
         (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
         hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
-        hipMemset(c->ready, 0, sizeof(int) * qw::ready_ints(NKV, cfg->max_splits)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipMemset(c->ready, 0, sizeof(int) * qw::ready_ints(NKV)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
     }

@@ -323,8 +323,8 @@ def test_decode_one_launch_equals_two_launches(qw):
     changing token counts (decode n=1 on the loader-wave kernel, verify n=4 on two 16-row slices) and
     split counts (fewer splits than combine units, one split, many), each output matches
     decode_partial + combine to fp32 rounding (the two merges visit the splits in different orders).
-    A wrong re-arm of the arrival counters would leave a later call with no combiner or too early a
-    one."""
+    The one-launch calls use the context's ready flags with changing split counts: a flag left by one
+    call that passed for a later call's epoch would let its combiners merge stale partials."""
     s, pos = QWEN3_NEXT, 3000
     cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, 4, "f32", 77)
     ctx = make_ctx(qw, s, max_ctx=cap)
@@ -342,8 +342,8 @@ def test_decode_one_launch_equals_two_launches(qw):
 
 def test_decode_one_launch_graph_replays(qw):
     """Captured into a HIP graph, the one-launch decode gives the eager result on every replay, with
-    eager work and synchronizations in between (the counters re-arm inside the kernel; nothing is
-    cleared by a memset node)."""
+    eager work and synchronizations in between (each launch advances its own epoch inside the kernel;
+    nothing is cleared by a memset node)."""
     s, pos, n = QWEN3_NEXT, 8190, 1
     cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 91)
     ctx = make_ctx(qw, s, max_ctx=cap)
