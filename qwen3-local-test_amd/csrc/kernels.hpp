@@ -76,8 +76,17 @@ struct PrefillArgs {
     int pos, n, NH, NKV;
     float q_scale;
     int cap;              // capacity (positions) of the caches kc, vc
+    float* part;          // [NKV][npairs][2 halves][4 waves][pf_part_floats(D)]: partials of split query tiles
+    int* cnt;             // [NKV][npairs][4 waves] arrival counters, zero between launches
+    int npairs;           // query-tile pairs per KV head: (query tiles) / 2
 };
+// Floats of one wave's prefill partial: 64 lanes x (D/2 accumulator values + max and sum).
+__host__ __device__ constexpr int pf_part_floats(int D) { return 64 * (D / 2 + 2); }
+// Query tiles of an n-token prefill with GQA group G (128 query rows per tile).
+__host__ __device__ constexpr int pf_query_tiles(int n, int G) { return (n + 128 / G - 1) / (128 / G); }
 hipError_t launch_prefill(const PrefillArgs& a, int D, int q_dtype, int in_dtype, hipStream_t s);
+// out[i] = fp16(q[i] * scale), i < n (n a multiple of 4): the prefill operand from fp32 queries
+hipError_t launch_q_f16(const float* q, void* out, float scale, size_t n, hipStream_t s);
 
 hipError_t launch_rope_table(float* rope, const float* inv_freq, int n_pos, int R, hipStream_t s);
 

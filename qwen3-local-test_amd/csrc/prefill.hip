@@ -21,7 +21,12 @@
 //    the last position are zeroed in LDS, so stale or unwritten cache memory never reaches the sum.
 //  - Softmax in log2 units with a lazy rescale (the reference max moves only when a row's max grows by
 //    more than 2^8); tiles below every row's causal limit skip the mask, tiles past it are skipped.
-//  - Workgroups are issued longest-first (last tokens first) to shorten the causal tail.
+//  - Causal balance: query tile qt sees ceil((pos + 16(qt+1)) / 64) key tiles (33 to 64 at 2048 on
+//    2048), and with one workgroup per CU the launch lasts as long as the longest one. Tiles are paired
+//    instead, short qt with long n_qt-1-qt: one workgroup runs the long tile's keys [x, end), the other
+//    its first x tiles and then the whole short tile, with x chosen so both get half the pair's tiles.
+//    The two halves of the long tile are merged by whichever wave finishes its half last (per-wave
+//    arrival counters, log-sum-exp merge of the stored partial), so no workgroup ever waits on another.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -42,6 +47,7 @@ struct PfCfg {
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Matrix-instruction order of one pipeline step of N slots: QK^T and P.V steps alternate. Slot i is a
 // QK^T step (index slot_qk) or a P.V step (index slot_pv); without P.V only the QK^T slots issue.
@@ -64,8 +70,19 @@ constexpr int slot_nth(int n, bool pv, int u) {
 
 }  // namespace
 
-template <int D, int Q_DT, int IN_DT>
-__global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
+// Key tiles of query tile qt: keys [0, pos + last token of the tile + 1) in 64-key tiles.
+__device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, int qt) {
+    return (a.pos + min(a.n - 1, (qt + 1) * tok_per_blk - 1) + 1 + PF_KT - 1) / PF_KT;
+}
+
+// One segment of a workgroup's schedule: query tile qt (128 rows of KV head kvh) against key tiles
+// [lo, hi). slot < 0: the tile's whole key range; the normalized, gated rows go to the output.
+// slot >= 0: one of the two halves of a split tile. Each wave stores its unnormalized partial
+// (accumulator, reference max, sum) in the pair's slot and counts its arrival, unless the partner wave
+// has already arrived; the wave that arrives second merges the two and writes the rows, then clears
+// the counter for the next launch.
+template <int D, int IN_DT>
+__device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot) {
     using C = PfCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, BLKE = C::BLKE, TILEE = C::TILEE, LOADS = C::LOADS;
     constexpr float TAU = 8.f;
@@ -74,15 +91,15 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     auto sK = [&](int b) { return reinterpret_cast<f16*>(smem) + (size_t)b * TILEE; };
     auto sV = [&](int b) { return reinterpret_cast<f16*>(smem) + (size_t)(2 + b) * TILEE; };
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    // the thread index through an empty asm: lane-derived values are computed per segment instead of
+    // being hoisted out of the kernel's segment loop, where they would stay live through the tile loop
+    int tid_ = threadIdx.x;
+    asm volatile("" : "+v"(tid_));
+    const int tid = tid_, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: copy addresses stay scalar
     const int col = lane & 31, half = lane >> 5;
     const int G = a.NH / a.NKV;
     const int tok_per_blk = PF_ROWS / G;
-    const int n_qt = (a.n + tok_per_blk - 1) / tok_per_blk;
-    // longest first: the last query tiles have the most keys
-    const int kvh = blockIdx.x % a.NKV;
-    const int qt = n_qt - 1 - (int)(blockIdx.x / a.NKV);
     const int t0 = qt * tok_per_blk;
 
     // this lane's query row (B-operand column) and its causal limit
@@ -90,14 +107,9 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     const int t = t0 + r / G, h = kvh * G + r % G;
     const bool row_ok = t < a.n;
     const int len = row_ok ? a.pos + t + 1 : 0;
-    // the wave's and the workgroup's key ranges
+    // the wave's first token: keys below its limit need no mask
     const int t_wave_first = t0 + wave * 32 / G;
-    const bool wave_live = t_wave_first < a.n;
-    const int t_wave_last = min(a.n - 1, t0 + (wave * 32 + 31) / G);
-    const int wave_end = wave_live ? a.pos + t_wave_last + 1 : 0;
     const int wave_nomask = a.pos + t_wave_first + 1;  // keys below this are visible to every row of the wave
-    const int blk_end = a.pos + min(a.n - 1, t0 + tok_per_blk - 1) + 1;
-    const int n_tiles = (blk_end + PF_KT - 1) / PF_KT;
     const int maxlen = a.pos + a.n;
 
     // ---- Q^T operand in registers: lane holds row `col`, dims 16*ks + 8*half .. +8 ----------------
@@ -107,15 +119,7 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
         // every load issued before the first use, so the row's fetches overlap
 #pragma unroll
         for (int ks = 0; ks < NKS; ks++) {
-            f16x8 v;
-            if constexpr (Q_DT == 2) {
-                v = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qoff + 16 * ks);
-            } else {
-                float x[8];
-                load_vec<0, 8>(a.q, qoff + 16 * ks, x);
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[i] = (f16)(x[i] * a.q_scale);
-            }
+            const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qoff + 16 * ks);
             qop[ks] = row_ok ? v : f16x8{};
         }
         // the Q fragments are only ever matrix-instruction operands: keep them in accumulation registers,
@@ -292,23 +296,28 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
         l_run = l_run * corr + (ps[0] + ps[1]);
     };
 
-    // Software pipeline over the workgroup's key tiles (every wave runs every tile; rows past their
-    // causal limit see all-masked tiles). Staging: K tiles run two ahead of their use and V tiles one,
-    // in two buffers each, with one barrier per iteration.
-    if (n_tiles > 0) copy_tile(rk, sK(0), 0);
-    if (n_tiles > 1) copy_tile(rk, sK(1), 1);
+    // Software pipeline over the segment's key tiles [lo, hi) (every wave runs every tile; rows past
+    // their causal limit see all-masked tiles). Staging: K tiles run two ahead of their use and V tiles
+    // one, in two buffers each (tile kt in buffer kt & 1), with one barrier per iteration. The buffers
+    // are free here: the previous segment's last barrier follows its last K read, and its last V tile
+    // is only overwritten after the first barrier of the loop below.
+    copy_tile(rk, sK(lo & 1), lo);
+    if (lo + 1 < hi) copy_tile(rk, sK((lo + 1) & 1), lo + 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    if (n_tiles > 0) qk_only(sK(0) + koff_lane);
+    qk_only(sK(lo & 1) + koff_lane);
 
-    for (int kt = 0; kt < n_tiles; kt++) {
+    // one tile iteration; the first (QK^T only, no P.V) is peeled off by hand so that the loop body is
+    // the full step alone
+    auto iter = [&](auto do_pv, int kt) __attribute__((always_inline)) {
+        constexpr bool DO_PV = decltype(do_pv)::value;
         sc[0] = sn[0];
         sc[1] = sn[1];
         // this wave's copies are complete; after the barrier every wave's are, and every wave is done
         // with the buffers this iteration's copies overwrite (K tile kt, V tile kt-2)
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
-        if (kt >= 1 && kt * PF_KT > maxlen) {
+        if (DO_PV && kt * PF_KT > maxlen) {
             zero_tail(sV((kt - 1) & 1), kt - 1);
             __syncthreads();
         }
@@ -325,8 +334,7 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
         }
         const f16* Kb = sK((kt + 1) & 1) + koff_lane;  // tile kt+1 (stale past the last tile: unused)
         const f16* Vb = sV((kt + 1) & 1) + voff_lane;  // tile kt-1 (no P.V on the first tile)
-        if (kt == 0) step(std::false_type{}, Kb, Vb, kt);
-        else step(std::true_type{}, Kb, Vb, kt);
+        step(do_pv, Kb, Vb, kt);
         if (any_rescale) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) acc[dt] *= corr;
@@ -336,22 +344,89 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
             pprev[sb][0] = pcur[sb][0];
             pprev[sb][1] = pcur[sb][1];
         }
-    }
+    };
+    iter(std::false_type{}, lo);
+    for (int kt = lo + 1; kt < hi; kt++) iter(std::true_type{}, kt);
     // ---- P.V of the last tile ----
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    if (n_tiles > 0) {
-        if (n_tiles * PF_KT > maxlen) {
-            zero_tail(sV((n_tiles - 1) & 1), n_tiles - 1);
-            __syncthreads();
-        }
-        pv_only(sV((n_tiles - 1) & 1) + voff_lane);
+    if (hi * PF_KT > maxlen) {
+        zero_tail(sV((hi - 1) & 1), hi - 1);
+        __syncthreads();
     }
+    pv_only(sV((hi - 1) & 1) + voff_lane);
 
-    // ---- epilogue: l across the two lane halves, normalize, gate, store ---------------------------
+    // ---- epilogue: l across the two lane halves, merge of a split tile, normalize, gate, store ----
     {
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
         l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    if (slot >= 0) {
+        // a wave's partial: accumulator chunk (dt, q4) of every lane as 1 KB, then (max, sum) per lane;
+        // each half of the tile has its own region (half 1: keys from lo > 0) and reads the other's
+        constexpr int PSTR = pf_part_floats(D);
+        const int own = lo > 0 ? 1 : 0;
+        float* pw = a.part + (((size_t)slot * 2 + own) * 4 + wave) * PSTR;
+        float* pr = a.part + (((size_t)slot * 2 + (1 - own)) * 4 + wave) * PSTR;
+        int* cw = a.cnt + slot * 4 + wave;
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(pw, (short)0, PSTR * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(pr, (short)0, PSTR * 4, 0x00020000);
+        const float mu = m_run == kNegInf ? 0.f : m_run;  // the offset the weights were taken against
+        int other = __builtin_amdgcn_readfirstlane(__hip_atomic_load(cw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (other == 0) {
+            // first (as far as this wave can tell): publish the partial (device-coherent stores,
+            // acknowledged before the arrival is counted), then count
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const f32x4 o = {acc[dt][4 * q4], acc[dt][4 * q4 + 1], acc[dt][4 * q4 + 2], acc[dt][4 * q4 + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(o, rp, ((dt * 4 + q4) * 64 + lane) * 16, 0, kScDevice);
+                }
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, f32x2{mu, l_run}), rp,
+                                                  NDT * 4 * 64 * 16 + lane * 8, 0, kScDevice);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            int old = 0;
+            if (lane == 0) old = __hip_atomic_fetch_add(cw, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            other = __builtin_amdgcn_readfirstlane(old);
+            if (other == 0) return;  // the partner wave merges
+        }
+        // the partner's loads stay behind the count that says its partial is complete
+        asm volatile("" ::: "memory");
+        // second: the partner's partial (published before its count) merged into this wave's, one dim
+        // tile at a time with two more in flight (the whole partial in registers at once would spill)
+        const f32x2 ml2 = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rq, NDT * 4 * 64 * 16 + lane * 8, 0, kScDevice));
+        constexpr int NB = NDT < 3 ? NDT : 3;
+        f32x4 o2[NB][4];
+        auto load_dt = [&](int dt) __attribute__((always_inline)) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+                o2[dt % NB][q4] = __builtin_amdgcn_raw_buffer_load_b128(rq, ((dt * 4 + q4) * 64 + lane) * 16, 0, kScDevice);
+        };
+        static_for<0, NB - 1>([&](auto ic) __attribute__((always_inline)) { load_dt(ic.value); });
+        if (lane == 0) __hip_atomic_store(cw, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // fixed order whichever wave merges: the key-suffix half (lo > 0) is the first term, so the
+        // result does not depend on arrival order
+        const bool own_first = own == 1;
+        const float muf = own_first ? mu : ml2[0], mus = own_first ? ml2[0] : mu;
+        const float lf = own_first ? l_run : ml2[1], ls = own_first ? ml2[1] : l_run;
+        const bool vf = lf > 0.f, vs = ls > 0.f;
+        const float mx = vf ? (vs ? fmaxf(muf, mus) : muf) : mus;
+        const float cf = vf ? exp2_fast(muf - mx) : 0.f, cs = vs ? exp2_fast(mus - mx) : 0.f;
+        l_run = __builtin_fmaf(ls, cs, lf * cf);
+        static_for<0, NDT>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int dt = decltype(ic)::value;
+            if constexpr (dt + NB - 1 < NDT) load_dt(dt + NB - 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float x = acc[dt][4 * q4 + i], y = o2[dt % NB][q4][i];
+                    acc[dt][4 * q4 + i] = __builtin_fmaf(own_first ? y : x, cs, (own_first ? x : y) * cf);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        });
     }
     if (row_ok) {
         const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
@@ -376,12 +451,47 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     }
 }
 
+// Workgroup j of KV head kvh (blockIdx = j * NKV + kvh). Pair p = j / 2 holds query tiles p (short) and
+// n_qt-1-p (long) with T = nl + ns key tiles: j = 2p runs the long tile over [x, nl), j = 2p+1 its
+// first x tiles, then the short tile, x = max(0, nl - ceil(T/2)). With n_qt odd the last workgroup
+// runs the middle tile alone.
+template <int D, int IN_DT>
+__global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
+    const int G = a.NH / a.NKV;
+    const int tok_per_blk = PF_ROWS / G;
+    const int n_qt = (a.n + tok_per_blk - 1) / tok_per_blk;
+    const int kvh = blockIdx.x % a.NKV, j = blockIdx.x / a.NKV;
+    const int np = n_qt / 2;
+    // segments (query tile, key tiles [lo, hi), partial slot) of this workgroup, in order
+    int q0, lo0, hi0, slot0, q1 = 0, hi1 = 0, nseg = 1;
+    if (j >= 2 * np) {  // the middle tile
+        q0 = np, lo0 = 0, hi0 = pf_tiles(a, tok_per_blk, np), slot0 = -1;
+    } else {
+        const int p = j >> 1, ql = n_qt - 1 - p;
+        const int nl = pf_tiles(a, tok_per_blk, ql), ns = pf_tiles(a, tok_per_blk, p);
+        const int x = max(0, nl - (nl + ns + 1) / 2);
+        slot0 = x > 0 ? kvh * a.npairs + p : -1;
+        if ((j & 1) == 0) {
+            q0 = ql, lo0 = x, hi0 = nl;
+        } else if (x > 0) {  // the long tile's prefix first: its partial is published long before the partner ends
+            q0 = ql, lo0 = 0, hi0 = x, q1 = p, hi1 = ns, nseg = 2;
+        } else {
+            q0 = p, lo0 = 0, hi0 = ns;
+        }
+    }
+    // one call site, so the segment body exists once in the code object
+    for (int s = 0; s < nseg; s++)
+        pf_segment<D, IN_DT>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0);
+}
+
 template <int D>
 static hipError_t launch_pf_d(const PrefillArgs& a, int q_dtype, int in_dtype, hipStream_t s) {
     using C = PfCfg<D>;
     const int G = a.NH / a.NKV;
     const int tok = PF_ROWS / G;
     const int n_qt = (a.n + tok - 1) / tok;
+    // the pairs' partial slots and counters are the caller's (sized for npairs pairs per KV head)
+    if (a.n < 1 || a.npairs != n_qt / 2 || (a.npairs > 0 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
     const dim3 grid(n_qt * a.NKV), block(256);
     const size_t shm = 2 * 2 * (size_t)C::TILEE * 2;  // two buffers of a K and a V tile
     auto go = [&](auto kern) {
@@ -390,10 +500,25 @@ static hipError_t launch_pf_d(const PrefillArgs& a, int q_dtype, int in_dtype, h
         hipLaunchKernelGGL(kern, grid, block, shm, s, a);
         return hipGetLastError();
     };
-    if (q_dtype == 2 && in_dtype == 0) return go(k_prefill<D, 2, 0>);
-    if (q_dtype == 2) return go(k_prefill<D, 2, 1>);
-    if (in_dtype == 0) return go(k_prefill<D, 0, 0>);
-    return go(k_prefill<D, 0, 1>);
+    // fp32 queries reach this kernel converted to the fp16 operand (launch_q_f16)
+    if (q_dtype != 2) return hipErrorInvalidValue;
+    return in_dtype == 0 ? go(k_prefill<D, 0>) : go(k_prefill<D, 1>);
+}
+
+// fp16(q * scale): the prefill operand from fp32 queries; n4 groups of 4 values
+__global__ __launch_bounds__(256) void k_q_f16(const f32x4* __restrict__ q, f16x4* __restrict__ o, float scale, size_t n4) {
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const f32x4 v = q[i];
+        o[i] = f16x4{(f16)(v[0] * scale), (f16)(v[1] * scale), (f16)(v[2] * scale), (f16)(v[3] * scale)};
+    }
+}
+
+hipError_t launch_q_f16(const float* q, void* out, float scale, size_t n, hipStream_t s) {
+    if (n % 4) return hipErrorInvalidValue;
+    const size_t n4 = n / 4;
+    const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_q_f16, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const f32x4*>(q), static_cast<f16x4*>(out), scale, n4);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, int D, int q_dtype, int in_dtype, hipStream_t s) {

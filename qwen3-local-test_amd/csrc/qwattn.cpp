@@ -28,6 +28,8 @@ struct qwattn_ctx {
     int* ready = nullptr;        // qwattn_decode: epoch words and per-split ready flags (qw::ready_ints)
     float* q32 = nullptr;        // [max_tokens][NH][D] layer-path query (fp32)
     void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
+    float* pf_part = nullptr;    // prefill: partials of split query tiles (qw::PrefillArgs::part)
+    int* pf_cnt = nullptr;       // prefill: their arrival counters, zero between launches
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
     int last_splits = 0;         // split count of the last qwattn_attend_partial / qwattn_decode_partial
     int last_n = 0;
@@ -169,7 +171,12 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
         return fail(nullptr, QWATTN_EINVAL, "max_splits %d: the split partials would exceed 2 GiB", cfg->max_splits);
     }
     const size_t qn = (size_t)cfg->max_tokens * NH * D;
-    bool ok = hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
+    // prefill pair slots: one per pair of query tiles per KV head at max_tokens (at least one, so the
+    // pointers are never null), 4 waves each; a partial region per half of the split tile
+    const size_t pf_slots = (size_t)NKV * std::max(1, qw::pf_query_tiles(cfg->max_tokens, NH / NKV) / 2) * 4;
+    bool ok = hipMalloc(&c->pf_part, sizeof(float) * 2 * pf_slots * qw::pf_part_floats(D)) == hipSuccess &&
+              hipMalloc(&c->pf_cnt, sizeof(int) * pf_slots) == hipSuccess &&
+              hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
               hipMalloc(&c->rope, sizeof(float) * rope_n) == hipSuccess &&
               hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
               hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
@@ -185,6 +192,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     if (hipMemcpy(c->inv_freq, inv.data(), sizeof(float) * inv.size(), hipMemcpyHostToDevice) != hipSuccess ||
         (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
         hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
+        hipMemset(c->pf_cnt, 0, sizeof(int) * pf_slots) != hipSuccess ||
         hipMemset(c->ready, 0, sizeof(int) * qw::ready_ints(NKV)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
@@ -198,7 +206,7 @@ int qwattn_destroy(qwattn_ctx* c) {
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
     for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ready,
-                    (void*)c->q32, c->q16})
+                    (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
@@ -434,9 +442,16 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     if (rc) return rc;
     const qwattn_config& g = c->cfg;
     DeviceGuard dg(c->device);
+    // n <= max_tokens (check_call), so the pairs fit the slots sized at creation for max_tokens
     qw::PrefillArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, qg, out, pos, n, g.n_heads, g.n_kv_heads,
-                      qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap};
-    HIP_TRY(c, qw::launch_prefill(a, g.head_dim, q_dtype == QWATTN_F16 ? 2 : 0, in_dtype, (hipStream_t)stream));
+                      qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap, c->pf_part, c->pf_cnt,
+                      qw::pf_query_tiles(n, g.n_heads / g.n_kv_heads) / 2};
+    if (q_dtype == QWATTN_F32) {  // the kernel's operand: fp16(q * log2(e)/sqrt(D)) in the context's query buffer
+        HIP_TRY(c, qw::launch_q_f16(static_cast<const float*>(q), c->q16, a.q_scale, (size_t)n * g.n_heads * g.head_dim,
+                                    (hipStream_t)stream));
+        a.q = c->q16;
+    }
+    HIP_TRY(c, qw::launch_prefill(a, g.head_dim, 2, in_dtype, (hipStream_t)stream));
     return QWATTN_OK;
 }
 
