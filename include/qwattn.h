@@ -79,8 +79,9 @@ typedef struct qwattn_config {
     int max_splits;   /* largest split-KV count (the reference caps at 64, src/qwen4_vk.cpp:976-978) */
 } qwattn_config;
 
-/* Creates a context on `device`: checks the shape, allocates the rope table for max_ctx positions
- * and the split-KV partials for max_tokens x NH x max_splits rows, and fills the rope table.
+/* Creates a context on `device`: checks the shape, allocates the rope table for max_ctx positions,
+ * the split-KV partials for max_tokens x NH x max_splits rows, the prefill's pair partials and
+ * arrival counters for max_tokens tokens, and the query buffers; fills the rope table.
  * Replaces the backend constructor's rope upload (src/qwen4_vk.cpp:494-504) and the partials
  * buffer (src/qwen4_vk.cpp:540). */
 int qwattn_create(qwattn_ctx** ctx, int device, const qwattn_config* cfg);
@@ -167,10 +168,14 @@ int qwattn_combine(qwattn_ctx* ctx, void* stream, const void* qg, int in_dtype, 
                    int n_split);
 
 /* Causal chunked prefill on MFMA: out = softmax(q K^T / sqrt(D)) V * sigmoid(gate) for n tokens at
- * positions pos.. pos+n-1 against keys [0, pos+t+1), in one kernel (no split partials). The
- * reference runs prefill chunks through the same split-K shader (src/qwen4_vk.cpp:974-978); this is
- * its matrix-core replacement. `q` is QWATTN_F16 pre-scaled (see qwattn_qk_norm_rope_append) or
- * QWATTN_F32 unscaled (`q_dtype`). */
+ * positions pos.. pos+n-1 against keys [0, pos+t+1), in one kernel. The reference runs prefill
+ * chunks through the same split-K shader (src/qwen4_vk.cpp:974-978); this is its matrix-core
+ * replacement. `q` is QWATTN_F16 pre-scaled (see qwattn_qk_norm_rope_append) or QWATTN_F32 unscaled
+ * (`q_dtype`; converted to the fp16 operand in the context's query buffer by one more launch).
+ * Query tiles are paired short with long; the long tile's key range is split between the pair's two
+ * workgroups and merged in the launch through the context's pair partials and arrival counters,
+ * which are back at zero when the launch ends. The merge order is fixed, so repeated calls give the
+ * same bits. Calls on one context that overlap in time race on those buffers. */
 int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dtype,
                           const void* kcache, const void* vcache, int kv_cap, const void* qg,
                           int in_dtype, float* out, int pos, int n);
