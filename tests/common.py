@@ -57,6 +57,7 @@ class Shape:
 TINY = Shape(4, 1, 64, 16)
 TINY_GGUF = Shape(2, 1, 256, 64)    # tests/make_tiny_gguf.py:10, 151 of the reference
 QWEN3_NEXT = Shape(16, 2, 256, 64)  # src/model.h:15-20 of the reference
+D128 = Shape(8, 2, 128, 32)        # a head_dim-128 layout: the 128-dim kernel variants
 
 
 def rng(seed):

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import QWEN3_NEXT, TINY, TINY_GGUF, Shape, assert_parity, cache_rows, projections
+from common import D128, QWEN3_NEXT, TINY, TINY_GGUF, Shape, assert_parity, cache_rows, projections
 
 pytestmark = pytest.mark.gpu
 
@@ -218,6 +218,8 @@ CASES_FUSED = [
     (QWEN3_NEXT, 16384, 1, 0, "f32"),
     (QWEN3_NEXT, 16384, 1, 64, "bf16"),  # BASELINE config 2 with the reference's 64 splits
     (QWEN3_NEXT, 32768, 4, 0, "f32"),
+    (D128, 4000, 1, 0, "bf16"),
+    (D128, 777, 4, 0, "f32"),
     (QWEN3_NEXT, 32766, 4, 0, "f32"),   # the 4 new keys straddle a 32-key block
     (QWEN3_NEXT, 1000, 3, 7, "bf16"),
     (QWEN3_NEXT, 32768, 1, 0, "f32"),   # the headline shape
@@ -379,6 +381,8 @@ CASES_PF = [
     (QWEN3_NEXT, 0, 300),
     (QWEN3_NEXT, 777, 129),
     (QWEN3_NEXT, 2048, 2048),
+    (TINY, 1000, 200),          # odd tile count, a split tile with D = 64 (two dim tiles)
+    (D128, 1000, 200),          # the same with D = 128
 ]
 
 
