@@ -455,6 +455,40 @@ def test_prefill_entry_parity(qw, oracle, s, pos, n):
         assert_parity(out[t:t + 1], ref, f"{s} pos={pos} n={n} token {t}")
 
 
+def test_prefill_graph_replays(qw):
+    """Captured into a HIP graph, the prefill (with split query tiles: 9 tiles, pairs merged through
+    the context's arrival counters, which each launch leaves at zero) gives the eager bits on every
+    replay, with eager launches and synchronizations in between."""
+    s, pos, n = QWEN3_NEXT, 777, 129
+    cap = capacity(pos + n)
+    k16, v16 = cache_rows(95, pos, s)
+    qg, k, v, qn, kn = projections(96, n, s)
+    qg_d, k_d, v_d = dev(qg).to(torch.bfloat16), dev(k).to(torch.bfloat16), dev(v).to(torch.bfloat16)
+    ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=n)
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    q16 = torch.zeros((n, s.NH, s.D), dtype=torch.float16, device=DEV)
+    ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, q16, pos, n)
+    eager = torch.zeros((n, s.NH, s.D), device=DEV)
+    ctx.attend_prefill(q16, kc, vc, cap, qg_d, eager, pos, n)
+    torch.cuda.synchronize()
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            ctx.attend_prefill(q16, kc, vc, cap, qg_d, out, pos, n, stream=stream)
+    for rep in range(4):
+        print(f"prefill graph replay {rep}", flush=True)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+        ctx.attend_prefill(q16, kc, vc, cap, qg_d, eager, pos, n)  # eager work in between
+        torch.cuda.synchronize()
+
+
 def test_prefill_equals_decodes(qw):
     """A prefill chunk gives the same rows as decoding its tokens one at a time (block-causal vs
     token-causal masks agree)."""
