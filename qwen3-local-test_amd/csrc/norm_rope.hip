@@ -12,7 +12,10 @@
 // squares is a five-step shuffle reduction with no barrier, the rows move in 16-byte loads and stores,
 // every load of the four rows is in flight at once, and the RoPE partner d +- R/2 is (R/2)/(D/32)
 // lanes away. The caches are written in the blocked layout of
-// common.hpp (a key row's 8 consecutive dims are one 16-byte piece).
+// common.hpp (a key row's 8 consecutive dims are one 16-byte piece). V is a plain copy whose blocked
+// layout runs 8 consecutive keys of one dim, so it has lanes of its own (workgroups after the norm
+// ones): a lane loads 8 dims of 8 consecutive positions and writes 8 whole 16-byte pieces; only the
+// partly new groups at the ends of the range are written element by element.
 // The split-KV decode kernel (decode.hip) does the same work inline for its new tokens; this kernel
 // serves prefill chunks and callers of the per-dispatch entry point.
 #include "common.hpp"
@@ -21,6 +24,45 @@
 namespace qw {
 
 constexpr int kNormRows = 4;  // rows per half-wave: every load of the four is issued before any is used
+
+// V groups of a call: 8-position groups overlapping [pos, pos + n)
+__host__ __device__ inline int v_groups(int pos, int n) { return (pos + n - 1) / 8 - pos / 8 + 1; }
+
+// V lane vi: KV head h, 8-position group g (positions 8g .. 8g+7), dims 8c .. 8c+7 (c fastest, so a
+// wave's loads are whole row segments). The 8 x 8 block is transposed in registers: dim d's 8 keys
+// are one 16-byte piece of the blocked layout. Positions outside [pos, pos + n) are neither read
+// (their loads repeat a valid row) nor written.
+template <int D, int IN_DT>
+__device__ __forceinline__ void v_copy(const NormRopeArgs& a, int vi) {
+    constexpr int NC = D / 8;
+    const int ng = v_groups(a.pos, a.n);
+    if (vi >= a.NKV * ng * NC) return;
+    const int c = vi % NC, g = a.pos / 8 + (vi / NC) % ng, h = vi / NC / ng;
+    const int p0 = 8 * g;
+    float x[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int t = min(max(p0 + i - a.pos, 0), a.n - 1);
+        load_vec<IN_DT, 8>(a.v, ((size_t)t * a.NKV + h) * D + 8 * c, x[i]);
+    }
+    f16* vc = reinterpret_cast<f16*>(a.vcache) + kv_part(p0, h, a.cap, D);
+    const int kb0 = p0 & (kBlk - 1);  // a multiple of 8: v_off(kb0, d) starts dim d's 8-key piece
+    const bool whole = p0 >= a.pos && p0 + 8 <= a.pos + a.n;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        f16* dst = vc + v_off(kb0, 8 * c + j);
+        if (whole) {
+            f16x8 o;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] = (f16)x[i][j];
+            *reinterpret_cast<f16x8*>(dst) = o;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (p0 + i >= a.pos && p0 + i < a.pos + a.n) dst[i] = (f16)x[i][j];
+        }
+    }
+}
 
 template <int D, int IN_DT, int Q_DT>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
@@ -32,13 +74,18 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
     const int item0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * NR;
     const int heads = a.NH + a.NKV;
     const int n_items = a.n * heads;
+    const int norm_blocks = (n_items + 8 * NR - 1) / (8 * NR);
+    if ((int)blockIdx.x >= norm_blocks) {
+        v_copy<D, IN_DT>(a, ((int)blockIdx.x - norm_blocks) * 256 + (int)threadIdx.x);
+        return;
+    }
     if (item0 >= n_items) return;  // whole half-wave exits
     const int d0 = hl * DPL;
     const int half_r = a.R >> 1;
     const bool rot = d0 < a.R;  // DPL divides R/2: a lane's dims are all rotated or all not
     const bool lo = d0 < half_r;
 
-    float x[NR][DPL], vv[NR][DPL], cs[NR][2 * DPL];
+    float x[NR][DPL], cs[NR][2 * DPL];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         const int item = min(item0 + r, n_items - 1);  // past the end: the last row again, not stored
@@ -47,7 +94,6 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
         const int h = is_q ? hh : hh - a.NH;
         const size_t src = is_q ? ((size_t)t * a.NH + h) * 2 * D : ((size_t)t * a.NKV + h) * D;
         load_vec<IN_DT, DPL>(is_q ? a.qg : a.k, src + d0, x[r]);
-        if (!is_q) load_vec<IN_DT, DPL>(a.v, ((size_t)t * a.NKV + h) * D + d0, vv[r]);
         if (rot) load_vec<0, 2 * DPL>(a.rope, (size_t)(a.pos + t) * a.R + 2 * (lo ? d0 : d0 - half_r), cs[r]);
     }
     float wq[DPL], wk[DPL];
@@ -97,18 +143,12 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
                 *reinterpret_cast<f16v*>(static_cast<f16*>(a.q_out) + ((size_t)t * a.NH + h) * D + d0) = o;
             }
         } else {
-            const size_t part = kv_part(p, h, a.cap, D);
-            f16* kc = reinterpret_cast<f16*>(a.kcache) + part;
-            f16* vc = reinterpret_cast<f16*>(a.vcache) + part;
-            const int kb = p & (kBlk - 1);
+            f16* kc = reinterpret_cast<f16*>(a.kcache) + kv_part(p, h, a.cap, D);
             // K: the lane's DPL dims are consecutive in the blocked layout (d % 8 runs fastest)
             f16v ko;
 #pragma unroll
             for (int j = 0; j < DPL; j++) ko[j] = (f16)y[j];
-            *reinterpret_cast<f16v*>(kc + k_off(kb, d0)) = ko;
-            // V: consecutive dims are 8 elements apart (8 keys of one dim are contiguous)
-#pragma unroll
-            for (int j = 0; j < DPL; j++) vc[v_off(kb, d0 + j)] = (f16)vv[r][j];
+            *reinterpret_cast<f16v*>(kc + k_off(p & (kBlk - 1), d0)) = ko;
         }
     }
 }
@@ -116,7 +156,8 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
 template <int D>
 static hipError_t launch_d(const NormRopeArgs& a, int in_dtype, int q_dtype, hipStream_t s) {
     const int items = a.n * (a.NH + a.NKV);
-    const dim3 grid((items + 8 * kNormRows - 1) / (8 * kNormRows)), block(256);
+    const int v_lanes = a.NKV * v_groups(a.pos, a.n) * (D / 8);
+    const dim3 grid((items + 8 * kNormRows - 1) / (8 * kNormRows) + (v_lanes + 255) / 256), block(256);
     if (in_dtype == 0 && q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 0>), grid, block, 0, s, a);
     else if (in_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 1>), grid, block, 0, s, a);
     else if (q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 0>), grid, block, 0, s, a);
