@@ -78,9 +78,9 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, i
 // One segment of a workgroup's schedule: query tile qt (128 rows of KV head kvh) against key tiles
 // [lo, hi). slot < 0: the tile's whole key range; the normalized, gated rows go to the output.
 // slot >= 0: one of the two halves of a split tile. Each wave stores its unnormalized partial
-// (accumulator, reference max, sum) in the pair's slot and counts its arrival, unless the partner wave
-// has already arrived; the wave that arrives second merges the two and writes the rows, then clears
-// the counter for the next launch.
+// (accumulator, reference max, sum) in its half's region of the pair's slot and counts its arrival,
+// unless the partner wave has already arrived; the wave that arrives second merges the two (in a fixed
+// order) and writes the rows, then clears the counter for the next launch.
 template <int D, int IN_DT>
 __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot) {
     using C = PfCfg<D>;
