@@ -172,8 +172,10 @@ int qwattn_combine(qwattn_ctx* ctx, void* stream, const void* qg, int in_dtype, 
  * chunks through the same split-K shader (src/qwen4_vk.cpp:974-978); this is its matrix-core
  * replacement. `q` is QWATTN_F16 pre-scaled (see qwattn_qk_norm_rope_append) or QWATTN_F32 unscaled
  * (`q_dtype`; converted to the fp16 operand in the context's query buffer by one more launch).
- * Query tiles are paired short with long; the long tile's key range is split between the pair's two
- * workgroups and merged in the launch through the context's pair partials and arrival counters,
+ * Query tiles are paired short with long, the long tile's key range split between the pair's two
+ * workgroups; when two workgroups per tile fit the CUs (small chunks), every tile's key range is split
+ * over two workgroups instead. Split tiles are merged in the launch through the context's partials
+ * and arrival counters,
  * which are back at zero when the launch ends. The merge order is fixed, so repeated calls give the
  * same bits. Calls on one context that overlap in time race on those buffers. */
 int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dtype,

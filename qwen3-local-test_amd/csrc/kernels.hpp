@@ -76,10 +76,13 @@ struct PrefillArgs {
     int pos, n, NH, NKV;
     float q_scale;
     int cap;              // capacity (positions) of the caches kc, vc
-    float* part;          // [NKV][npairs][2 halves][4 waves][pf_part_floats(D)]: partials of split query tiles
-    int* cnt;             // [NKV][npairs][4 waves] arrival counters, zero between launches
-    int npairs;           // query-tile pairs per KV head: (query tiles) / 2
+    float* part;          // [NKV][slots][2 halves][4 waves][pf_part_floats(D)]: partials of split query tiles
+    int* cnt;             // [NKV][slots][4 waves] arrival counters, zero between launches
+    int slots;            // split tiles per KV head: pf_split_slots(n_qt, split_all)
+    int split_all;        // 0: short and long tiles paired; 1: every tile's keys split over two workgroups
 };
+// Split slots per KV head of a launch with n_qt query tiles per KV head.
+__host__ __device__ constexpr int pf_split_slots(int n_qt, int split_all) { return split_all ? n_qt : n_qt / 2; }
 // Floats of one wave's prefill partial: 64 lanes x (D/2 accumulator values + max and sum).
 __host__ __device__ constexpr int pf_part_floats(int D) { return 64 * (D / 2 + 2); }
 // Query tiles of an n-token prefill with GQA group G (128 query rows per tile).

@@ -27,6 +27,8 @@
 //    its first x tiles and then the whole short tile, with x chosen so both get half the pair's tiles.
 //    The two halves of the long tile are merged by whichever wave finishes its half last (per-wave
 //    arrival counters, log-sum-exp merge of the stored partial), so no workgroup ever waits on another.
+//    Launches small enough that two workgroups per tile fit the CUs split every tile's keys in two
+//    instead (same merge), so chunks of up to ~1,024 tokens still fill the chip.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -464,13 +466,18 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     const int np = n_qt / 2;
     // segments (query tile, key tiles [lo, hi), partial slot) of this workgroup, in order
     int q0, lo0, hi0, slot0, q1 = 0, hi1 = 0, nseg = 1;
-    if (j >= 2 * np) {  // the middle tile
+    if (a.split_all) {  // two workgroups per tile, longest tiles first: keys [x, nt) and [0, x)
+        const int qt = n_qt - 1 - (j >> 1);
+        const int nt = pf_tiles(a, tok_per_blk, qt), x = nt / 2;
+        if (x == 0 && (j & 1)) return;  // a one-tile range is not split: the partner runs it whole
+        q0 = qt, lo0 = (j & 1) ? 0 : x, hi0 = (j & 1) ? x : nt, slot0 = x > 0 ? kvh * a.slots + qt : -1;
+    } else if (j >= 2 * np) {  // the middle tile
         q0 = np, lo0 = 0, hi0 = pf_tiles(a, tok_per_blk, np), slot0 = -1;
     } else {
         const int p = j >> 1, ql = n_qt - 1 - p;
         const int nl = pf_tiles(a, tok_per_blk, ql), ns = pf_tiles(a, tok_per_blk, p);
         const int x = max(0, nl - (nl + ns + 1) / 2);
-        slot0 = x > 0 ? kvh * a.npairs + p : -1;
+        slot0 = x > 0 ? kvh * a.slots + p : -1;
         if ((j & 1) == 0) {
             q0 = ql, lo0 = x, hi0 = nl;
         } else if (x > 0) {  // the long tile's prefix first: its partial is published long before the partner ends
@@ -490,9 +497,10 @@ static hipError_t launch_pf_d(const PrefillArgs& a, int q_dtype, int in_dtype, h
     const int G = a.NH / a.NKV;
     const int tok = PF_ROWS / G;
     const int n_qt = (a.n + tok - 1) / tok;
-    // the pairs' partial slots and counters are the caller's (sized for npairs pairs per KV head)
-    if (a.n < 1 || a.npairs != n_qt / 2 || (a.npairs > 0 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
-    const dim3 grid(n_qt * a.NKV), block(256);
+    // the split tiles' partial slots and counters are the caller's (sized for `slots` per KV head)
+    if (a.n < 1 || a.slots != pf_split_slots(n_qt, a.split_all) || (a.slots > 0 && (!a.part || !a.cnt)))
+        return hipErrorInvalidValue;
+    const dim3 grid((a.split_all ? 2 : 1) * n_qt * a.NKV), block(256);
     const size_t shm = 2 * 2 * (size_t)C::TILEE * 2;  // two buffers of a K and a V tile
     auto go = [&](auto kern) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);

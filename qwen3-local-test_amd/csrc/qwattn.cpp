@@ -30,6 +30,7 @@ struct qwattn_ctx {
     void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
     float* pf_part = nullptr;    // prefill: partials of split query tiles (qw::PrefillArgs::part)
     int* pf_cnt = nullptr;       // prefill: their arrival counters, zero between launches
+    int pf_slots_per_head = 0;   // prefill: split slots per KV head in pf_part / pf_cnt
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
     int last_splits = 0;         // split count of the last qwattn_attend_partial / qwattn_decode_partial
     int last_n = 0;
@@ -171,9 +172,12 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
         return fail(nullptr, QWATTN_EINVAL, "max_splits %d: the split partials would exceed 2 GiB", cfg->max_splits);
     }
     const size_t qn = (size_t)cfg->max_tokens * NH * D;
-    // prefill pair slots: one per pair of query tiles per KV head at max_tokens (at least one, so the
-    // pointers are never null), 4 waves each; a partial region per half of the split tile
-    const size_t pf_slots = (size_t)NKV * std::max(1, qw::pf_query_tiles(cfg->max_tokens, NH / NKV) / 2) * 4;
+    // prefill split slots per KV head: a pair of query tiles each (paired schedule) or a tile each (split
+    // schedule, only while two workgroups per tile fit the CUs), at least one so the pointers are never
+    // null; 4 waves each, a partial region per half of the split tile
+    const int qt_max = qw::pf_query_tiles(cfg->max_tokens, NH / NKV);
+    c->pf_slots_per_head = std::max(1, std::max(qt_max / 2, std::min(qt_max, c->n_cu / (2 * NKV))));
+    const size_t pf_slots = (size_t)NKV * c->pf_slots_per_head * 4;
     bool ok = hipMalloc(&c->pf_part, sizeof(float) * 2 * pf_slots * qw::pf_part_floats(D)) == hipSuccess &&
               hipMalloc(&c->pf_cnt, sizeof(int) * pf_slots) == hipSuccess &&
               hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
@@ -442,10 +446,15 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     if (rc) return rc;
     const qwattn_config& g = c->cfg;
     DeviceGuard dg(c->device);
-    // n <= max_tokens (check_call), so the pairs fit the slots sized at creation for max_tokens
+    // Few query tiles (two workgroups per tile still fit the CUs): every tile's keys are split over two
+    // workgroups; otherwise short and long tiles are paired. Either way the split tiles fit the slots
+    // sized at creation (n <= max_tokens by check_call; split_all only when 2 * n_qt * NKV <= n_cu).
+    const int n_qt = qw::pf_query_tiles(n, g.n_heads / g.n_kv_heads);
+    const int split_all = 2 * n_qt * g.n_kv_heads <= c->n_cu ? 1 : 0;
     qw::PrefillArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, qg, out, pos, n, g.n_heads, g.n_kv_heads,
                       qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap, c->pf_part, c->pf_cnt,
-                      qw::pf_query_tiles(n, g.n_heads / g.n_kv_heads) / 2};
+                      qw::pf_split_slots(n_qt, split_all), split_all};
+    if (a.slots > c->pf_slots_per_head) return fail(c, QWATTN_EINVAL, "prefill: %d split slots > %d", a.slots, c->pf_slots_per_head);
     if (q_dtype == QWATTN_F32) {  // the kernel's operand: fp16(q * log2(e)/sqrt(D)) in the context's query buffer
         HIP_TRY(c, qw::launch_q_f16(static_cast<const float*>(q), c->q16, a.q_scale, (size_t)n * g.n_heads * g.head_dim,
                                     (hipStream_t)stream));
