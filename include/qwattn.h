@@ -80,7 +80,7 @@ typedef struct qwattn_config {
 } qwattn_config;
 
 /* Creates a context on `device`: checks the shape, allocates the rope table for max_ctx positions,
- * the split-KV partials for max_tokens x NH x max_splits rows, the prefill's pair partials and
+ * the split-KV partials for max_tokens x NH x max_splits rows, the prefill's split-tile partials and
  * arrival counters for max_tokens tokens, and the query buffers; fills the rope table.
  * Replaces the backend constructor's rope upload (src/qwen4_vk.cpp:494-504) and the partials
  * buffer (src/qwen4_vk.cpp:540). */
