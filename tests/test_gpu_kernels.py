@@ -382,6 +382,7 @@ CASES_PF = [
     (QWEN3_NEXT, 777, 129),
     (QWEN3_NEXT, 2048, 2048),
     (QWEN3_NEXT, 1500, 1100),   # paired schedule (69 tiles x 2 KV heads > 256 CUs / 2), odd tile count
+    (QWEN3_NEXT, 1024, 1024),   # split schedule at its limit on 256 CUs (64 tiles x 2 KV heads x 2)
     (TINY, 1000, 200),          # odd tile count, a split tile with D = 64 (two dim tiles)
     (D128, 1000, 200),          # the same with D = 128
 ]
