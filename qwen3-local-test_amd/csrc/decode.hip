@@ -676,8 +676,11 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(comb ? a.ready + kvh : a.ready, (short)0, comb ? 4 : 0, 0x00020000);
         epoch_word = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, kScDevice);
     }
-    const int kb = z * a.chunk;
-    const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, kb + a.chunk);
+    // The last chunk also appends the new rows; when it is longer than the others (the split leaves a
+    // short remainder there) its first tile goes to the chunk before it. Tiles stay block-aligned.
+    const int shift = (a.n_split >= 2 && maxlen - (a.n_split - 1) * a.chunk > a.chunk) ? 32 : 0;
+    const int kb = z * a.chunk + (z == a.n_split - 1 ? shift : 0);
+    const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, z * a.chunk + a.chunk + (z == a.n_split - 2 ? shift : 0));
     const int ntile_wg = (ke - kb + 31) >> 5;
     const bool loader = wave >= NCW;
     const int pr = loader ? wave - NCW : wave;                        // pair
