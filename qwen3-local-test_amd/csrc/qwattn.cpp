@@ -108,7 +108,8 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
 // n_split = 0 picks one workgroup per CU: chunk = maxlen / (CUs per KV head and row slice) rounded down
 // to the tile,
 // and a remainder of at most a quarter chunk — typically the one new position of a decode step — is
-// absorbed by the last chunk instead of costing a second round of workgroups.
+// absorbed by the last chunk instead of costing a second round of workgroups (the one-launch decode
+// kernel then moves that chunk's first tile to the chunk before it, as the last one also appends).
 void pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int* chunk, int* used) {
     const int maxs = c->cfg.max_splits;
     const int rows = n * (c->cfg.n_heads / c->cfg.n_kv_heads);
