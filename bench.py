@@ -429,7 +429,7 @@ def main():
                             "kernel_us": head["us_main"]}
     pf = results.get("prefill_2k_on_2k")
     if pf:
-        line["prefill_roofline"] = {"bound": "mfma", "kernel": "k_prefill<256,f16,bf16>",
+        line["prefill_roofline"] = {"bound": "mfma", "kernel": "k_prefill<256,1> (fp16 query operand, bf16 gate; paired schedule, grid 256)",
                                     "achieved": round(pf["algorithmic_flops"] / (pf["us_main"] * 1e-6) / 1e12, 2),
                                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                                     "frac": round(pf["frac_mfma_kernel"], 4),
