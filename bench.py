@@ -142,6 +142,7 @@ class Workload:
 
 
 _SLEEP_PER_MS = None
+KERNEL_BATCHES = 50  # batches of 16 launches timed for the dominant kernel's duration (median reported)
 
 
 def gpu_sleep(ms):
@@ -168,7 +169,7 @@ def run_workload(wl, steps, warmup, graph):
         wl.step(i % wl.slots)
     torch.cuda.synchronize()
     if graph:
-        # one graph holds one step per slot; replaying it runs `slots` steps
+        # one graph holds exactly `steps` layer steps, rotating over the slots; one replay is the timed run
         wl.step(0)
         torch.cuda.synchronize()
         ref_out = wl.out.clone()
@@ -177,24 +178,21 @@ def run_workload(wl, steps, warmup, graph):
         with torch.cuda.stream(s):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
-                for i in range(wl.slots):
-                    wl.step(i)
+                for i in range(steps):
+                    wl.step(i % wl.slots)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
-        reps = max(1, (steps + wl.slots - 1) // wl.slots)
-        for _ in range(2):
-            g.replay()
+        g.replay()  # untimed: the graph's first replay uploads it
         torch.cuda.synchronize()
         # a replay that computed something else than the eager step would show here
         wl.step(0)
         torch.cuda.synchronize()
         if not torch.equal(wl.out, ref_out):
             raise RuntimeError(f"{wl.name}: eager output changed after graph replays")
-        timed_steps = reps * wl.slots
+        timed_steps = steps
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(reps):
-            g.replay()
+        g.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         del g
@@ -222,9 +220,10 @@ def run_workload(wl, steps, warmup, graph):
         raise RuntimeError(f"{wl.name}: non-finite attention output")
     # the dominant kernel's launch duration: batches of 16 back-to-back launches between two events on
     # the library's stream, queued behind a GPU sleep (an event between every two launches would add its
-    # own cost to each figure); the mean per launch includes the in-stream gap between launches
+    # own cost to each figure); the mean per launch includes the in-stream gap between launches. The
+    # figure is the median over KERNEL_BATCHES batches.
     per_launch = []
-    for b in range(max(2, steps // 16)):
+    for b in range(KERNEL_BATCHES):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         gpu_sleep(2.0)
         e0.record()
@@ -234,7 +233,8 @@ def run_workload(wl, steps, warmup, graph):
         torch.cuda.synchronize()
         per_launch.append(e0.elapsed_time(e1) * 1e3 / 16)
     r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all),
-         "us_main": statistics.mean(per_launch), "us_main_batches": len(per_launch)}
+         "us_main": statistics.median(per_launch), "us_main_batches": len(per_launch),
+         "us_main_min": min(per_launch)}
     if wl.split:
         if wl.one_launch:
             r.update({"kernel": "k_decode_ld (fused norm+rope+append+split attend+combine, one launch)",
@@ -390,6 +390,8 @@ def main():
             r["frac_mfma_step"] = fl / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
             r["frac_mfma_kernel"] = fl / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
             r["algorithmic_flops"] = fl
+        if n * (NH // NKV) <= 32:
+            r["splits_requested"] = n_split or "auto"
         results[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)
 

@@ -58,6 +58,8 @@ extern "C" {
 #define QWATTN_ENOMEM -3  /* device allocation failed */
 #define QWATTN_ERANGE -4  /* position/context overflow ("context overflow" in the reference) */
 #define QWATTN_ESTATE -5  /* call out of order (e.g. no KV cache allocated) */
+#define QWATTN_ETIMEOUT -6 /* a bounded wait inside an earlier decode launch gave up: that launch's output
+                              is not valid (reported once, by the next call or qwattn_sync_status) */
 
 #define QWATTN_F32 0
 #define QWATTN_BF16 1
@@ -70,7 +72,7 @@ typedef struct qwattn_ctx qwattn_ctx;
 typedef struct qwattn_config {
     int n_heads;      /* NH: query heads (16 for Qwen3-Next) */
     int n_kv_heads;   /* NKV: key/value heads (2); NH % NKV == 0 */
-    int head_dim;     /* D: 64 or 256 */
+    int head_dim;     /* D: 64, 128 or 256 */
     int rope_dim;     /* R: rotated leading dims per head, even, <= D */
     float rope_theta; /* 1e7 */
     float rms_eps;    /* 1e-6 */
@@ -88,6 +90,19 @@ int qwattn_create(qwattn_ctx** ctx, int device, const qwattn_config* cfg);
 int qwattn_destroy(qwattn_ctx* ctx);
 /* Text of the last error on ctx (or of the last failed qwattn_create when ctx is NULL). */
 const char* qwattn_last_error(const qwattn_ctx* ctx);
+/* Waits for `stream` and returns the status of the decode launches queued on it so far: QWATTN_OK, or
+ * QWATTN_ETIMEOUT once when a bounded in-kernel wait gave up. The decode kernels' waits (the in-launch
+ * combine waiting for every split's ready flag, the loader/compute hand-offs) are bounded so that every
+ * kernel ends; a wait that gives up stores a code into a host-visible word of the context, which this
+ * call and every later kernel entry point report (once) instead of returning silently wrong output.
+ * No reference counterpart: the Vulkan backend's fence waits either complete or throw
+ * (src/vk_common.h:306-350). */
+int qwattn_sync_status(qwattn_ctx* ctx, void* stream);
+/* Test hook of the bounded waits (no reference counterpart). spin_max: polls before the in-launch
+ * combine's flag wait gives up (0 = the default, seconds of polling). epoch_skew: added to the epoch the
+ * combine waits for; nonzero makes every flag look stale, so the wait gives up after spin_max polls while
+ * every kernel still ends normally. Production code leaves both at 0. */
+int qwattn_set_wait_limits(qwattn_ctx* ctx, int spin_max, int epoch_skew);
 int qwattn_get_config(const qwattn_ctx* ctx, qwattn_config* cfg);
 /* Device address of the context's rope table ([max_ctx][R/2][2] fp32). */
 int qwattn_rope_table(const qwattn_ctx* ctx, const float** rope);
@@ -124,8 +139,12 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* ctx, void* stream, const void* qg, co
 
 /* Split-KV causal GQA attention partials (reference: shaders/attention.comp, pipeline
  * attention_kv16, dispatched at src/qwen4_vk.cpp:985-988 with PcAttn). Token t attends to keys
- * [0, pos+t+1); the keys [0, pos+n) are cut into `n_split` chunks (0 = automatic: one workgroup per
- * CU), and each workgroup serves all NH/NKV query heads of all n tokens of one KV head for one chunk,
+ * [0, pos+t+1); the keys [0, pos+n) are cut into `n_split` chunks of whole 32-key blocks (0 =
+ * automatic: one workgroup per CU). A requested count is used as given, capped at max_splits and at
+ * ceil((pos+n)/32), so that every chunk holds at least one block; of the nb = ceil((pos+n)/32) blocks the
+ * first nb % n_split chunks hold one block more than the others. The reference cuts ceil(len/n_split)
+ * keys per chunk (src/qwen4_vk.cpp:974-978); both splits give the same output up to fp32 rounding.
+ * Each workgroup serves all NH/NKV query heads of all n tokens of one KV head for one chunk,
  * so every K/V row is read from HBM once. `q` is the normalized, rotated query [n][NH][D] fp32 (the
  * reference's q_out) and rows [pos, pos+n) must already be in the caches. Requires n * NH/NKV <= 32
  * (decode n=1, MTP verify n<=4 at NH/NKV=8). Partials (running max in log2 units, sum, unnormalized
@@ -191,10 +210,12 @@ int qwattn_prefill(qwattn_ctx* ctx, void* stream, const void* qg, const void* k,
 
 /* The whole attention body between the projections, for one full-attention layer `slot` of the
  * context's caches (reference: the dispatches of Qwen4Vulkan::attention, src/qwen4_vk.cpp:968-992;
- * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): for n <= 8 and
- * n <= 8 and n * NH/NKV <= 32 qwattn_decode; otherwise qwattn_prefill (or norm + rope + append,
- * split attend and combine when n * NH/NKV <= 32). `n_split`
- * as in qwattn_attend_partial. */
+ * Qwen4Cpu::attention src/qwen4_cpu.cpp:306-372 without the projections): qwattn_decode when
+ * n <= 8 and n * NH/NKV <= 32 (decode, MTP verify); norm + rope + append, split attend and combine
+ * when n > 8 and n * NH/NKV <= 32 (small GQA groups); qwattn_prefill otherwise. `n_split` as in
+ * qwattn_attend_partial. Rollback after a rejected speculative draft (the reference's accept(keep),
+ * src/qwen4_vk.cpp:286-300) needs no call: the next pass is made at the smaller pos, and the rows
+ * beyond it are overwritten as they are appended again. */
 int qwattn_layer_attention(qwattn_ctx* ctx, void* stream, int slot, const void* qg, const void* k,
                            const void* v, int in_dtype, const float* qn, const float* kn, float* out,
                            int pos, int n, int n_split);

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libqwattn.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "qwattn.h")
 
-OK, EINVAL, EHIP, ENOMEM, ERANGE, ESTATE = 0, -1, -2, -3, -4, -5
+OK, EINVAL, EHIP, ENOMEM, ERANGE, ESTATE, ETIMEOUT = 0, -1, -2, -3, -4, -5, -6
 F32, BF16, F16 = 0, 1, 2
 LOG2E = 1.4426950408889634
 
@@ -66,6 +66,8 @@ def load_library():
         "qwattn_attend_prefill": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I],
         "qwattn_prefill": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
+        "qwattn_sync_status": [_P, _P],
+        "qwattn_set_wait_limits": [_P, _I, _I],
     }
     for name, args in sig.items():
         f = getattr(lib, name)
@@ -222,7 +224,8 @@ class Attention:
                                                    _ptr(vcache), kv_cap, _ptr(qg), _DT[qg.dtype], _ptr(out), pos, n))
 
     def prefill(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
-        """K/V norm + rope + append, then the MFMA prefill normalizing its own query rows (two launches)."""
+        """Norm + rope + append of the chunk (queries into the context's fp16 buffer, pre-scaled), then the
+        MFMA prefill on that buffer: two launches."""
         self._check(self.lib.qwattn_prefill(
             self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
             _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n))
@@ -234,6 +237,14 @@ class Attention:
             self.combine(qg, out, n, used, stream)
         else:
             self.attend_prefill(q, kcache, vcache, kv_cap, qg, out, pos, n, stream)
+
+    def sync_status(self, stream=None):
+        """Waits for the stream; raises QwattnError(ETIMEOUT) once if a bounded in-kernel wait gave up."""
+        self._check(self.lib.qwattn_sync_status(self.h, _stream(stream)))
+
+    def set_wait_limits(self, spin_max=0, epoch_skew=0):
+        """Test hook of the decode kernels' bounded waits (0, 0 = production defaults)."""
+        self._check(self.lib.qwattn_set_wait_limits(self.h, spin_max, epoch_skew))
 
     def layer_attention(self, slot, qg, k, v, qn, kn, out, pos, n, n_split=0, stream=None):
         self._check(self.lib.qwattn_layer_attention(self.h, _stream(stream), slot, _ptr(qg), _ptr(k), _ptr(v),

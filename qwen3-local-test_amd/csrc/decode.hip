@@ -68,6 +68,27 @@ __device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x
 // bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// Key range [kb, ke) of split z: whole 32-key blocks, split z holding the blocks
+// [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr)) of the ceil(maxlen/32) that hold keys (the host keeps
+// cq >= 1, so no split is empty). The first cr splits are one block longer, so the last split, whose
+// workgroup also appends the new rows, is never the longest.
+__device__ __forceinline__ void split_keys(const DecodeArgs& a, int z, int maxlen, int& kb, int& ke) {
+    const int b0 = z * a.cq + min(z, a.cr);
+    const int b1 = b0 + a.cq + (z < a.cr ? 1 : 0);
+    kb = b0 * kBlk;
+    ke = min(maxlen, b1 * kBlk);
+}
+
+// A bounded wait gave up: the launch's output is not valid. The code goes to the host-visible error word
+// (the first code stored wins: a later one does not overwrite it).
+__device__ __forceinline__ void report_wait(const DecodeArgs& a, int code) {
+    if (a.err != nullptr) {
+        int expected = 0;
+        __hip_atomic_compare_exchange_strong(a.err, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 
 // Merges a batch of split partials (m, l, o) into the running (M, L, O) (attn_combine.comp:17-26: the
 // max over the splits with keys, then each partial weighted by exp2(m - max)), in a fixed order and
@@ -116,9 +137,10 @@ __device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int
     constexpr int NSL = 64 / NCOL;         // split lanes per wave (4)
     constexpr int BATCH = 32 / NSL;        // splits a lane takes per batch of 32 (8)
     static_assert(D % UD == 0, "head_dim must be a multiple of 64");
-    constexpr int SPIN_MAX = 1 << 20;
+    constexpr int WAIT_MAX = 1 << 26;      // merging waves: a bound the poller's own bound keeps unreached
     __shared__ float s_wave[4][NCOL][6];            // each wave's (M, L, O) per column
     __shared__ unsigned char s_seen[kReadyMaxSplits];  // split's flag seen set by the polling wave
+    __shared__ int s_done;                          // the polling wave has finished (every flag seen, or gave up)
     // wave index through readfirstlane: the compiler then knows it (and the split range and buffer
     // descriptors derived from it) to be wave-uniform, and keeps the descriptors in scalar registers
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -126,6 +148,7 @@ __device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int
     int* epoch = a.ready + kvh;  // e: this launch's epoch, the word + 1 (read at the kernel start)
     int* flags = a.ready + ready_flags_at(a.NKV) + (size_t)kvh * kReadyMaxSplits;
     for (int i = tid; i < S; i += 256) s_seen[i] = 0;
+    if (tid == 0) s_done = 0;
     // the partials went out as device-coherent stores: once every wave's stores are acknowledged they are
     // visible to every workgroup's device-coherent loads, so completing them is the whole release (no
     // cache write-back)
@@ -147,35 +170,45 @@ __device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int
     if (wave == 0) gate_of(ci, gate);  // issued now, in by the time the partials are
     // LDS accesses the compiler cannot see: one it can see makes it wait for every outstanding load first
     const uint32_t seen_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_seen));
+    const uint32_t done_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&s_done));
     // waves 0-2: a third of the splits each (the polling wave takes none)
     const int Q3 = (S + 2) / 3;
     const int zb = wave < 3 ? min(S, wave * Q3) : S, ze = wave < 3 ? min(S, zb + Q3) : S;
     if (wave == 3) {
-        // the polling wave: lane l watches the flags l + 64 j (j < 8 per round of loads)
+        // the polling wave: lane l watches the flags l + 64 j (j < 8 per round of loads). Its wait is
+        // bounded (a.spin_max rounds per 512 flags); when it gives up, the launch reports kWaitCombineFlags
+        // and the merge below runs on whatever the partials hold (the host returns QWATTN_ETIMEOUT).
+        const int want = e + a.epoch_skew;
         const int J = (S + 63) / 64;
+        bool gave_up = false;
         for (int j0 = 0; j0 < J; j0 += 8) {
             unsigned todo = 0;  // bit k: flag lane + 64 (j0 + k) not seen yet
 #pragma unroll
             for (int k = 0; k < 8; k++)
                 if (j0 + k < J && lane + 64 * (j0 + k) < S) todo |= 1u << k;
             for (int spin = 0; __ballot(todo != 0) != 0; spin++) {
+                const bool last = spin >= a.spin_max;
                 int f[8];
 #pragma unroll
                 for (int k = 0; k < 8; k++)
                     f[k] = (todo >> k) & 1 ? __hip_atomic_load(flags + lane + 64 * (j0 + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
 #pragma unroll
                 for (int k = 0; k < 8; k++)
-                    if (((todo >> k) & 1) && (f[k] == e || spin >= SPIN_MAX)) {
+                    if (((todo >> k) & 1) && (f[k] == want || last)) {
+                        gave_up |= f[k] != want;
                         asm volatile("ds_write_b8 %0, %1" ::"v"(seen_at + lane + 64 * (j0 + k)), "v"(1) : "memory");
                         todo &= ~(1u << k);
                     }
                 if (todo != 0) __builtin_amdgcn_s_sleep(1);
             }
         }
+        if (__ballot(gave_up) != 0 && lane == 0) report_wait(a, kWaitCombineFlags);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1" ::"v"(done_at), "v"(1) : "memory");
     } else {
-        // waves 0-2 wait until the polling wave has seen the flags of all their splits: lane l checks the
-        // splits zb + l + 64 j (a short loop of LDS reads only)
-        for (int spin = 0; spin < 4 * SPIN_MAX; spin++) {
+        // waves 0-2 wait until the polling wave has seen the flags of all their splits (lane l checks the
+        // splits zb + l + 64 j: a short loop of LDS reads only), or until it has finished: its own wait is
+        // bounded, so these waits end with it
+        for (int spin = 0;; spin++) {
             int missing = 0;
             for (int zz = zb + lane; zz < ze; zz += 64) {
                 uint32_t sn;
@@ -183,6 +216,13 @@ __device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int
                 missing |= sn == 0;
             }
             if (__ballot(missing) == 0) break;
+            uint32_t dn;
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(dn) : "v"(done_at) : "memory");
+            if (__builtin_amdgcn_readfirstlane(dn) != 0) break;
+            if (spin >= WAIT_MAX) {  // unreachable while the poller's bound holds; reported, never silent
+                if (lane == 0) report_wait(a, kWaitCombineSeen);
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
     }
@@ -274,8 +314,8 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     const int r0 = blockIdx.z * RMAX;                  // first query row of this slice
     const int rows = min(RMAX, a.n * G - r0);          // query rows of this workgroup
     const int maxlen = a.pos + a.n;
-    const int kb = z * a.chunk;
-    const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, kb + a.chunk);
+    int kb, ke;
+    split_keys(a, z, maxlen, kb, ke);
     const int ntile_wg = (ke - kb + 31) >> 5;
     const int ntile = ntile_wg > wave ? (ntile_wg - wave + 3) >> 2 : 0;  // tiles wave, wave + 4, ...
     const int new_lo = FUSED ? a.pos : maxlen;        // first position not read from the cache
@@ -636,7 +676,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
 // appended to the caches in the prologue and a tile holding them is copied only after those stores are
 // acknowledged, so it arrives complete (no patching in LDS: LDS stores crawl while the first copies
 // land); V past the last position is zeroed in registers. Spin waits are bounded, so every wave exits
-// even if a counter were never reached.
+// even if a counter were never reached; a wait that gives up is reported through DecodeArgs::err.
 template <int D, int FUSED, int IN_DT>
 __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     constexpr int NKS = D / 32, NDT = D / 16, RMAX = 8, BLKE = kBlk * D;
@@ -676,11 +716,8 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(comb ? a.ready + kvh : a.ready, (short)0, comb ? 4 : 0, 0x00020000);
         epoch_word = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, kScDevice);
     }
-    // The last chunk also appends the new rows; when it is longer than the others (the split leaves a
-    // short remainder there) its first tile goes to the chunk before it. Tiles stay block-aligned.
-    const int shift = (a.n_split >= 2 && maxlen - (a.n_split - 1) * a.chunk > a.chunk) ? 32 : 0;
-    const int kb = z * a.chunk + (z == a.n_split - 1 ? shift : 0);
-    const int ke = z == a.n_split - 1 ? maxlen : min(maxlen, z * a.chunk + a.chunk + (z == a.n_split - 2 ? shift : 0));
+    int kb, ke;
+    split_keys(a, z, maxlen, kb, ke);
     const int ntile_wg = (ke - kb + 31) >> 5;
     const bool loader = wave >= NCW;
     const int pr = loader ? wave - NCW : wave;                        // pair
@@ -886,10 +923,14 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                 // wait for the compute wave to free the slot; read through inline assembly as well, since
                 // an LDS read the compiler can see would first wait for all of this wave's copies
                 const uint32_t faddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&freed[pr]));
-                for (int spin = 0; spin < SPIN_MAX; spin++) {
+                for (int spin = 0;; spin++) {
                     int f;
                     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(f) : "v"(faddr) : "memory");
                     if (__builtin_amdgcn_readfirstlane(f) >= i + 1) break;
+                    if (spin >= SPIN_MAX) {
+                        if (lane == 0) report_wait(a, kWaitRingLoad);
+                        break;
+                    }
                     __builtin_amdgcn_s_sleep(1);
                 }
                 dma(i + 2);
@@ -903,10 +944,14 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
 #pragma unroll
         for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
         for (int i = 0; i < ntp; i++) {
-            for (int spin = 0; __hip_atomic_load(&ready[pr], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1 &&
-                               spin < SPIN_MAX;
-                 spin++)
+            for (int spin = 0; __hip_atomic_load(&ready[pr], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1;
+                 spin++) {
+                if (spin >= SPIN_MAX) {
+                    if (lane == 0) report_wait(a, kWaitRingCompute);
+                    break;
+                }
                 __builtin_amdgcn_s_sleep(1);
+            }
             const f16* sl = slot(i);
             f16x8 kt[NKS][2], vt[NDT];
 #pragma unroll

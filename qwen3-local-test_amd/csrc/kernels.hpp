@@ -38,14 +38,27 @@ struct DecodeArgs {
     uint16_t* vc;         // blocked V cache
     float* part_o;        // [n*NH][n_split][D]
     float* part_ml;       // [n*NH][n_split][2]: running max (log2 units), sum
-    int pos, n, NH, NKV, R, chunk, n_split;
+    int pos, n, NH, NKV, R;
+    int cq, cr;           // split z holds the 32-key blocks [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr))
+    int n_split;
     float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
     float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
                           // the same launch (nullptr: partials only, for a separate combine)
     int* ready;           // with out: epoch words and ready flags (ready_ints(NKV) ints, zero at first)
     int comb_max;         // with out: combining workgroups per KV head at most (NKV * comb_max <= CUs / 2)
     int cap;              // capacity (positions) of the caches kc, vc
+    int* err;             // a bounded wait that gives up stores its kWait* code here (nullptr: not reported)
+    int spin_max;         // polls of the in-launch combine's flag wait before it gives up
+    int epoch_skew;       // added to the epoch the combine waits for: 0, or nonzero to force the give-up path
 };
+
+// Codes a kernel stores into DecodeArgs::err when a bounded wait gives up (the launch's output is then
+// not valid; the host reports QWATTN_ETIMEOUT)
+constexpr int kWaitCombineFlags = 1;  // the in-launch combine's poller: a split's ready flag never came
+constexpr int kWaitCombineSeen = 2;   // a merging wave: the poller's marks never came
+constexpr int kWaitRingLoad = 3;      // a loader wave: its compute wave never released a slot
+constexpr int kWaitRingCompute = 4;   // a compute wave: its loader wave never published a tile
+constexpr int kSpinDefault = 1 << 22; // default DecodeArgs::spin_max (seconds of polling)
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 
 // Splits at most of the one-launch decode (its combiners track the splits in LDS)

@@ -36,6 +36,10 @@ struct qwattn_ctx {
     int last_n = 0;
     std::vector<uint16_t*> kc, vc;
     int kv_cap = 0;
+    int* wait_err_host = nullptr;  // pinned host word a kernel's bounded wait writes when it gives up
+    int* wait_err_dev = nullptr;   // its device address
+    int spin_max = qw::kSpinDefault;
+    int epoch_skew = 0;
     std::string err;
 };
 
@@ -92,6 +96,18 @@ int check_shape(qwattn_ctx* c, const qwattn_config& g) {
     return QWATTN_OK;
 }
 
+// A bounded in-kernel wait of an earlier launch gave up: report it once (QWATTN_ETIMEOUT) and clear it.
+int take_wait_error(qwattn_ctx* c) {
+    if (!c->wait_err_host) return QWATTN_OK;
+    const int code = __atomic_exchange_n(c->wait_err_host, 0, __ATOMIC_ACQ_REL);
+    if (code == 0) return QWATTN_OK;
+    static const char* what[] = {"", "a split's ready flag never arrived at the in-launch combine",
+                                 "the combine's merging waves never saw the poller's marks",
+                                 "a loader wave's slot was never released", "a compute wave's tile was never published"};
+    return fail(c, QWATTN_ETIMEOUT, "a bounded wait in an earlier decode launch gave up (%s); its output is not valid",
+                code >= 1 && code <= 4 ? what[code] : "unknown wait");
+}
+
 int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
     if (n < 1) return fail(c, QWATTN_EINVAL, "n = %d", n);
     if (pos < 0) return fail(c, QWATTN_EINVAL, "pos = %d", pos);
@@ -99,41 +115,44 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
     if ((long long)pos + n > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow (%d + %d > %d)", pos, n, c->cfg.max_ctx);
     if ((long long)pos + n > kv_cap) return fail(c, QWATTN_ERANGE, "context overflow: %d + %d rows exceed the K/V cache capacity %d", pos, n, kv_cap);
     if (kv_cap % 32) return fail(c, QWATTN_EINVAL, "K/V cache capacity %d is not a multiple of 32", kv_cap);
-    return QWATTN_OK;
+    return take_wait_error(c);
 }
 
-// Split of the key axis [0, maxlen) for the decode kernel: `chunk` keys per workgroup (a multiple of
-// the 32-key tile), `used` chunks, the last one ending at maxlen. A requested count n_split > 0 follows
-// the reference (chunk = ceil(maxlen / n_split), src/qwen4_vk.cpp:974-978, rounded up to the tile).
-// n_split = 0 picks one workgroup per CU: chunk = maxlen / (CUs per KV head and row slice) rounded down
-// to the tile,
-// and a remainder of at most a quarter chunk — typically the one new position of a decode step — is
-// absorbed by the last chunk instead of costing a second round of workgroups (the one-launch decode
-// kernel then moves that chunk's first tile to the chunk before it, as the last one also appends).
-void pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int* chunk, int* used) {
-    const int maxs = c->cfg.max_splits;
+// Split of the key axis [0, maxlen) for the decode kernels into S chunks of whole 32-key blocks: of the
+// nb = ceil(maxlen / 32) blocks that hold keys, chunk z takes [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr))
+// with cq = nb / S, cr = nb % S (the first cr chunks one block longer). A requested count n_split > 0 is
+// used as given (the reference's 64, src/qwen4_vk.cpp:974-978, or BASELINE's 1,024), capped at max_splits
+// and at nb: a chunk holds at least one block. n_split = 0 picks one workgroup per CU: CUs / (NKV x the
+// decode kernel's 16-row slices) chunks.
+struct Split {
+    int S, cq, cr;
+};
+
+Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split) {
+    const int nb = (maxlen + 31) / 32;
     const int rows = n * (c->cfg.n_heads / c->cfg.n_kv_heads);
     const int slices = rows <= 8 ? 1 : (rows + 15) / 16;  // the decode kernel's 16-row slices (grid.z)
-    int ch, S;
-    if (n_split > 0) {
-        S = std::min(n_split, maxs);
-        ch = (maxlen + S - 1) / S;
-        ch = (ch + 31) / 32 * 32;
-        S = (maxlen + ch - 1) / ch;
-    } else {
-        const int target = std::max(1, c->n_cu / (c->cfg.n_kv_heads * slices));
-        ch = std::max(32, maxlen / target / 32 * 32);
-        S = std::max(1, maxlen / ch);
-        if (maxlen - S * ch > ch / 4) S++;
-        if (S > maxs) {
-            ch = (maxlen + maxs - 1) / maxs;
-            ch = (ch + 31) / 32 * 32;
-            S = (maxlen + ch - 1) / ch;
-        }
-    }
-    *chunk = ch;
-    *used = S;
+    int S = n_split > 0 ? n_split : std::max(1, c->n_cu / (c->cfg.n_kv_heads * slices));
+    S = std::max(1, std::min({S, c->cfg.max_splits, nb}));
+    return Split{S, nb / S, nb % S};
 }
+
+// Arguments of the decode kernels: shape, split and the context's partials and wait settings.
+qw::DecodeArgs decode_args(const qwattn_ctx* c, const void* q, const void* knew, const void* vnew, const float* qn,
+                           const float* kn, const float* rope, const void* kcache, const void* vcache, int kv_cap, int pos, int n,
+                           const Split& sp) {
+    const qwattn_config& g = c->cfg;
+    qw::DecodeArgs a{};
+    a.q = q, a.knew = knew, a.vnew = vnew, a.qn = qn, a.kn = kn, a.rope = rope;
+    a.kc = (uint16_t*)kcache, a.vc = (uint16_t*)vcache, a.part_o = c->part_o, a.part_ml = c->part_ml;
+    a.pos = pos, a.n = n, a.NH = g.n_heads, a.NKV = g.n_kv_heads, a.R = g.rope_dim;
+    a.cq = sp.cq, a.cr = sp.cr, a.n_split = sp.S;
+    a.eps = g.rms_eps, a.q_scale = qw::kLog2eHost / std::sqrt((float)g.head_dim);
+    a.out = nullptr, a.ready = nullptr, a.comb_max = 0, a.cap = kv_cap;
+    a.err = c->wait_err_dev, a.spin_max = c->spin_max, a.epoch_skew = c->epoch_skew;
+    return a;
+}
+
 
 }  // namespace
 
@@ -186,7 +205,9 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
               hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
               hipMalloc(&c->ready, sizeof(int) * qw::ready_ints(NKV)) == hipSuccess &&
-              hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess;
+              hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess &&
+              hipHostMalloc(&c->wait_err_host, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
+              hipHostGetDevicePointer((void**)&c->wait_err_dev, c->wait_err_host, 0) == hipSuccess;
     if (!ok) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_ENOMEM, "out of device memory creating the context");
@@ -202,6 +223,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
     }
+    *c->wait_err_host = 0;
     *out = c;
     return QWATTN_OK;
 }
@@ -215,7 +237,23 @@ int qwattn_destroy(qwattn_ctx* c) {
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
+    if (c->wait_err_host) (void)hipHostFree(c->wait_err_host);
     delete c;
+    return QWATTN_OK;
+}
+
+int qwattn_sync_status(qwattn_ctx* c, void* stream) {
+    if (!c) return QWATTN_EINVAL;
+    DeviceGuard dg(c->device);
+    HIP_TRY(c, hipStreamSynchronize((hipStream_t)stream));
+    return take_wait_error(c);
+}
+
+int qwattn_set_wait_limits(qwattn_ctx* c, int spin_max, int epoch_skew) {
+    if (!c) return QWATTN_EINVAL;
+    if (spin_max < 0) return fail(c, QWATTN_EINVAL, "qwattn_set_wait_limits: spin_max %d", spin_max);
+    c->spin_max = spin_max ? spin_max : qw::kSpinDefault;
+    c->epoch_skew = epoch_skew;
     return QWATTN_OK;
 }
 
@@ -345,12 +383,11 @@ int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const voi
     const int G = g.n_heads / g.n_kv_heads;
     if (n * G > 32)
         return fail(c, QWATTN_EINVAL, "qwattn_attend_partial: n * NH/NKV = %d > 32 rows (use the prefill kernel)", n * G);
-    int chunk = 0, used = 0;
-    pick_split(c, pos + n, n, n_split, &chunk, &used);
+    const Split sp = pick_split(c, pos + n, n, n_split);
+    const int used = sp.S;
     DeviceGuard dg(c->device);
-    qw::DecodeArgs a{q, nullptr, nullptr, nullptr, nullptr, nullptr, (uint16_t*)kcache, (uint16_t*)vcache,
-                     c->part_o, c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, 0, kv_cap};
+    const qw::DecodeArgs a = decode_args(c, q, nullptr, nullptr, nullptr, nullptr, nullptr, kcache, vcache, kv_cap,
+                                         pos, n, sp);
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, false, QWATTN_F32, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -372,12 +409,11 @@ int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const voi
     if (n * G > 32 || n > 8)
         return fail(c, QWATTN_EINVAL, "qwattn_decode_partial: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
                     "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
-    int chunk = 0, used = 0;
-    pick_split(c, pos + n, n, n_split, &chunk, &used);
+    const Split sp = pick_split(c, pos + n, n, n_split);
+    const int used = sp.S;
     DeviceGuard dg(c->device);
-    qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
-                     c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), nullptr, nullptr, 0, kv_cap};
+    const qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n,
+                                         sp);
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
@@ -399,18 +435,16 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     if (n * G > 32 || n > 8)
         return fail(c, QWATTN_EINVAL, "qwattn_decode: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
                     "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
-    int chunk = 0, used = 0;
-    pick_split(c, pos + n, n, n_split, &chunk, &used);
+    const Split sp = pick_split(c, pos + n, n, n_split);
+    const int used = sp.S;
     DeviceGuard dg(c->device);
     // up to 8 query rows the combine runs inside the attend launch; the 16-row-slice kernel (verify) is
     // followed by the combine kernel. In-launch combiners wait for other workgroups: at most half the CUs
     // may hold one, so the others always have room to run
     const int comb_max = c->n_cu / 2 / g.n_kv_heads;
     const bool one = n * G <= 8 && comb_max >= 1 && used <= qw::kReadyMaxSplits;
-    qw::DecodeArgs a{qg, k, v, qn, kn, rope ? rope : c->rope, (uint16_t*)kcache, (uint16_t*)vcache, c->part_o,
-                     c->part_ml, pos, n, g.n_heads, g.n_kv_heads, g.rope_dim, chunk, used, g.rms_eps,
-                     qw::kLog2eHost / std::sqrt((float)g.head_dim), one ? out : nullptr, one ? c->ready : nullptr,
-                     comb_max, kv_cap};
+    qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
+    if (one) a.out = out, a.ready = c->ready, a.comb_max = comb_max;
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     if (!one) {
         qw::CombineArgs ca{c->part_o, c->part_ml, qg, out, n, g.n_heads, used};
@@ -431,6 +465,7 @@ int qwattn_combine(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, fl
     if (n != c->last_n || n_split != c->last_splits)
         return fail(c, QWATTN_EINVAL, "qwattn_combine: n=%d splits=%d do not match the last partials (n=%d splits=%d)", n,
                     n_split, c->last_n, c->last_splits);
+    if (int rc = take_wait_error(c)) return rc;
     DeviceGuard dg(c->device);
     qw::CombineArgs a{c->part_o, c->part_ml, qg, out, n, c->cfg.n_heads, n_split};
     HIP_TRY(c, qw::launch_combine(a, c->cfg.head_dim, in_dtype, (hipStream_t)stream));
