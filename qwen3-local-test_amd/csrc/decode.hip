@@ -113,183 +113,117 @@ __device__ __forceinline__ void merge_batch(float& M, float& L, f32x4& O, const 
     M = mx;
 }
 
-// In-launch log-sum-exp combine (attn_combine.comp:13-29), run at the end of every workgroup of the
-// one-launch decode once its partials are stored. Each workgroup reads its KV head's epoch word, and once
-// its partial stores are acknowledged it sets its split's flag to epoch + 1 (this launch's epoch). The
-// workgroups of the last NC = min(units, n_split, comb_max) splits of a head are its combiners; the work
-// is cut into units of one query row x 64 dims and combiner c merges units c, c + NC, .... In a combiner,
-// wave 3 polls the head's flags (bounded; every lane a flag per 64 splits, one load per 64 flags) and
-// marks each split it sees set in LDS, while waves 0-2, a third of the splits each, wait on those marks
-// (LDS reads only, so the flag lines see one poller per combiner). Then every wave loads its partials,
-// lane (column c, split lane j) the splits j + 4k of each batch of 32, all loads of a batch issued before
-// any is used, merges them in split order, and the split lanes and then the waves merge in a fixed order,
-// so the result does not depend on arrival order. At most comb_max workgroups of a head wait, the host
-// keeps NKV * comb_max at half the CUs or below, and they wait only for workgroups that never wait, so
-// every wait ends. Each combiner then stores the launch's epoch into the head's epoch word: every
-// workgroup of the head read the word before setting its flag, so this launch's flags can never pass for
-// the next launch's, and no clearing pass is needed (none is recorded into a captured graph). Launches
-// that share the flag array must not overlap.
+// In-launch log-sum-exp combine of the one-launch decode (attn_combine.comp:13-29): the workgroups
+// first in the grid, one per output row (t, h), each merge that row's split partials while the others
+// stream K/V. A streaming workgroup stores its rows' unnormalized o[D] (device-coherent stores), waits
+// for them to be acknowledged, then stores each row's record (m, l, epoch tag): a record carrying this
+// launch's tag guarantees the row's o is visible. The combining workgroup takes the splits in windows of
+// kCombSlots: wave w owns the kCombGroup splits [wb + 32 w, wb + 32 w + 32) of window wb, lane j < 32
+// polling split wb + 32 w + j's record (one 16-byte device-coherent load per round); each split that
+// has arrived has its o row loaded straight into the wave's registers (one coalesced load, D/64 dims a
+// lane). Once its group is complete the wave takes the group's max and weights (wave reductions, the
+// weights broadcast through LDS) and its weighted sum over all D dims; the window's four group results
+// then meet in LDS and merge into the running (M, L, O) in group order — a fixed order, so the result
+// does not depend on which split arrives first. Splits with l = 0 are skipped. The epoch: see
+// kEpochStep. Every wait is bounded (a.spin_max polling rounds); a combiner that gives up reports
+// kWaitCombineFlags and merges whatever its registers hold. Combiners wait only for streaming
+// workgroups, which never wait, and the host keeps them at half the CUs or below, so every wait ends.
 template <int D, int IN_DT>
-__device__ __forceinline__ void combine_ready(const DecodeArgs& a, int rows, int G, int kvh, int z, int e) {
-    constexpr int UD = 64;                 // dims of a unit
-    constexpr int NUD = D / UD;            // units per row
-    constexpr int NCOL = UD / 4;           // float4 columns of a unit (16)
-    constexpr int NSL = 64 / NCOL;         // split lanes per wave (4)
-    constexpr int BATCH = 32 / NSL;        // splits a lane takes per batch of 32 (8)
-    static_assert(D % UD == 0, "head_dim must be a multiple of 64");
-    constexpr int WAIT_MAX = 1 << 26;      // merging waves: a bound the poller's own bound keeps unreached
-    __shared__ float s_wave[4][NCOL][6];            // each wave's (M, L, O) per column
-    __shared__ unsigned char s_seen[kReadyMaxSplits];  // split's flag seen set by the polling wave
-    __shared__ int s_done;                          // the polling wave has finished (every flag seen, or gave up)
-    // wave index through readfirstlane: the compiler then knows it (and the split range and buffer
-    // descriptors derived from it) to be wave-uniform, and keeps the descriptors in scalar registers
+__device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* smem, int r) {
+    constexpr int NS = kCombSlots, GS = kCombGroup, DL = D / 64;
+    static_assert(NS == 4 * GS && GS == 32, "one group of 32 splits per wave and window");
+    typedef float fDL __attribute__((ext_vector_type(DL)));
+    float* s_go = reinterpret_cast<float*>(smem);  // [4][D] the window's group sums
+    float* s_gm = s_go + 4 * D;                     // [4] group maxima (log2 units)
+    float* s_gl = s_gm + 4;                         // [4] group sums of l
+    float* s_w = s_gl + 4;                          // [4][GS] each group's weights
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int S = a.n_split;
-    int* epoch = a.ready + kvh;  // e: this launch's epoch, the word + 1 (read at the kernel start)
-    int* flags = a.ready + ready_flags_at(a.NKV) + (size_t)kvh * kReadyMaxSplits;
-    for (int i = tid; i < S; i += 256) s_seen[i] = 0;
-    if (tid == 0) s_done = 0;
-    // the partials went out as device-coherent stores: once every wave's stores are acknowledged they are
-    // visible to every workgroup's device-coherent loads, so completing them is the whole release (no
-    // cache write-back)
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    __syncthreads();
-    if (tid == 0) __hip_atomic_store(flags + z, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int units = rows * NUD;
-    const int NC = min(min(units, S), a.comb_max);
-    const int ci = z - (S - NC);
-    if (ci < 0) return;
-    const int col = lane % NCOL, sl = lane / NCOL;
-    auto gate_of = [&](int u, float (&gt)[4]) {  // the output gate of unit u: wave 0 applies it
-        const int r = u / NUD, t = r / G, h = kvh * G + r % G;
-        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D + (u % NUD) * UD + col * 4;
+    const int S = a.n_split, G = a.NH / a.NKV;
+    const int t = r / a.NH, h = r % a.NH, kvh = h / G;
+    const unsigned long long cnt = __hip_atomic_load(a.ep + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned want = (unsigned)(cnt / kEpochStep) + 1u + (unsigned)a.epoch_skew;
+    const float gate = tid < D ? load_in<IN_DT>(a.q, ((size_t)t * a.NH + h) * 2 * D + D + tid) : 0.f;
+    const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(a.rec + (size_t)r * S * 4, (short)0, S * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + (size_t)r * S * D, (short)0, S * D * 4, 0x00020000);
+    int spins = 0;
+    bool gave_up = false;
+    float M = kNegInf, L = 0.f, O = 0.f;  // thread tid < D: running state of dim tid
+    for (int wb = 0; wb < S; wb += NS) {
+        const int z0 = wb + wave * GS;                 // this wave's first split (wave-uniform)
+        const int nz = max(0, min(GS, S - z0));        // its splits in this window
+        const int z = z0 + lane;
+        bool pend = lane < nz;                         // lane j: split z0 + j not arrived yet
+        float mj = kNegInf, lj = 0.f;
+        fDL ov[GS];
+        while (__ballot(pend) != 0) {
+            const f32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(rrec, (pend ? z : 0) * 16, 0, kScDevice);
+            const bool last = ++spins > a.spin_max;
+            const bool got = pend && (__float_as_uint(rv[2]) == want || last);
+            gave_up |= got && __float_as_uint(rv[2]) != want;
+            if (got) mj = rv[0], lj = rv[1];
+            pend = pend && !got;
+            const unsigned long long b = __ballot(got);
+            // each arrived split's o row: one coalesced load into its register slot (a uniform branch per
+            // split keeps the register index static)
 #pragma unroll
-        for (int i = 0; i < 4; i++) gt[i] = load_in<IN_DT>(a.q, gb + i);
-    };
-    float gate[4] = {0.f, 0.f, 0.f, 0.f};
-    if (wave == 0) gate_of(ci, gate);  // issued now, in by the time the partials are
-    // LDS accesses the compiler cannot see: one it can see makes it wait for every outstanding load first
-    const uint32_t seen_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_seen));
-    const uint32_t done_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&s_done));
-    // waves 0-2: a third of the splits each (the polling wave takes none)
-    const int Q3 = (S + 2) / 3;
-    const int zb = wave < 3 ? min(S, wave * Q3) : S, ze = wave < 3 ? min(S, zb + Q3) : S;
-    if (wave == 3) {
-        // the polling wave: lane l watches the flags l + 64 j (j < 8 per round of loads). Its wait is
-        // bounded (a.spin_max rounds per 512 flags); when it gives up, the launch reports kWaitCombineFlags
-        // and the merge below runs on whatever the partials hold (the host returns QWATTN_ETIMEOUT).
-        const int want = e + a.epoch_skew;
-        const int J = (S + 63) / 64;
-        bool gave_up = false;
-        for (int j0 = 0; j0 < J; j0 += 8) {
-            unsigned todo = 0;  // bit k: flag lane + 64 (j0 + k) not seen yet
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                if (j0 + k < J && lane + 64 * (j0 + k) < S) todo |= 1u << k;
-            for (int spin = 0; __ballot(todo != 0) != 0; spin++) {
-                const bool last = spin >= a.spin_max;
-                int f[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++)
-                    f[k] = (todo >> k) & 1 ? __hip_atomic_load(flags + lane + 64 * (j0 + k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-#pragma unroll
-                for (int k = 0; k < 8; k++)
-                    if (((todo >> k) & 1) && (f[k] == want || last)) {
-                        gave_up |= f[k] != want;
-                        asm volatile("ds_write_b8 %0, %1" ::"v"(seen_at + lane + 64 * (j0 + k)), "v"(1) : "memory");
-                        todo &= ~(1u << k);
-                    }
-                if (todo != 0) __builtin_amdgcn_s_sleep(1);
+            for (int j = 0; j < GS; j++) {
+                if ((b >> j) & 1) {
+                    const int off = ((z0 + j) * D + lane * DL) * 4;
+                    if constexpr (DL == 4) ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, kScDevice);
+                    else if constexpr (DL == 2) ov[j] = __builtin_bit_cast(fDL, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, kScDevice));
+                    else ov[j] = __builtin_bit_cast(fDL, __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, kScDevice));
+                }
             }
+            if (b == 0) __builtin_amdgcn_s_sleep(1);
         }
-        if (__ballot(gave_up) != 0 && lane == 0) report_wait(a, kWaitCombineFlags);
-        asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1" ::"v"(done_at), "v"(1) : "memory");
-    } else {
-        // waves 0-2 wait until the polling wave has seen the flags of all their splits (lane l checks the
-        // splits zb + l + 64 j: a short loop of LDS reads only), or until it has finished: its own wait is
-        // bounded, so these waits end with it
-        for (int spin = 0;; spin++) {
-            int missing = 0;
-            for (int zz = zb + lane; zz < ze; zz += 64) {
-                uint32_t sn;
-                asm volatile("ds_read_u8 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(sn) : "v"(seen_at + zz) : "memory");
-                missing |= sn == 0;
-            }
-            if (__ballot(missing) == 0) break;
-            uint32_t dn;
-            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(dn) : "v"(done_at) : "memory");
-            if (__builtin_amdgcn_readfirstlane(dn) != 0) break;
-            if (spin >= WAIT_MAX) {  // unreachable while the poller's bound holds; reported, never silent
-                if (lane == 0) report_wait(a, kWaitCombineSeen);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // the group's max and weights: lane j < nz holds split z0 + j's (m, l)
+        const bool use = lane < nz && lj > 0.f;
+        float mg = use ? mj : kNegInf;
+#pragma unroll
+        for (int x = 1; x < 32; x <<= 1) mg = fmaxf(mg, __shfl_xor(mg, x, 64));
+        const float w = use ? exp2_fast(mj - mg) : 0.f;
+        float lg = lj * w;
+#pragma unroll
+        for (int x = 1; x < 32; x <<= 1) lg += __shfl_xor(lg, x, 64);
+        // the weights to every lane through LDS (broadcast reads): lane j < 32 holds split z0 + j's
+        if (lane < GS) s_w[wave * GS + lane] = w;
+        float wv[GS];
+#pragma unroll
+        for (int j = 0; j < GS; j += 4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&s_w[wave * GS + j]);
+            wv[j] = x[0], wv[j + 1] = x[1], wv[j + 2] = x[2], wv[j + 3] = x[3];
         }
-    }
-    // every partial of the head is visible from here on: merge the units
-    for (int u = ci; u < units; u += NC) {
-        const int r = u / NUD, t = r / G, h = kvh * G + r % G;
-        const int d0 = (u % NUD) * UD + col * 4;
-        if (u != ci && wave == 0) gate_of(u, gate);
-        const size_t row = ((size_t)t * a.NH + h) * S;
-        // device-coherent loads: the other workgroups' stores, never a stale line of this XCD's L2
-        const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + row * 2, (short)0, S * 8, 0x00020000);
-        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + row * D, (short)0, S * D * 4, 0x00020000);
-        float M = kNegInf, L = 0.f;
-        f32x4 O = {0.f, 0.f, 0.f, 0.f};
-        for (int b0 = zb; b0 < ze; b0 += 32) {  // wave-uniform; every load of a batch is issued before any is used
-            float m[BATCH], l[BATCH];
-            f32x4 o[BATCH];
+        fDL og = {};
 #pragma unroll
-            for (int k = 0; k < BATCH; k++) {
-                const int zz = min(b0 + sl + NSL * k, ze - 1);
-                const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, zz * 8, 0, kScDevice));
-                m[k] = ml[0];
-                l[k] = ml[1];
-                o[k] = __builtin_amdgcn_raw_buffer_load_b128(ro, (zz * D + d0) * 4, 0, kScDevice);
-            }
-            __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the first wait
-            unsigned keys = 0;
-#pragma unroll
-            for (int k = 0; k < BATCH; k++) keys |= (b0 + sl + NSL * k < ze && l[k] > 0.f ? 1u : 0u) << k;
-            merge_batch(M, L, O, m, l, o, keys);
-        }
-        auto merge = [&](float Mo, float Lo, f32x4 Oo) {  // L = 0: nothing to merge
-            const float mn = fmaxf(M, Mo);
-            const float cf = L > 0.f ? exp2_fast(M - mn) : 0.f, co = Lo > 0.f ? exp2_fast(Mo - mn) : 0.f;
-            L = L * cf + Lo * co;
-            O = O * cf + Oo * co;
-            M = mn;
-        };
-#pragma unroll
-        for (int x = NCOL; x < 64; x <<= 1) {  // the wave's split lanes
-            f32x4 Oo;
-#pragma unroll
-            for (int i = 0; i < 4; i++) Oo[i] = __shfl_xor(O[i], x, 64);
-            merge(__shfl_xor(M, x, 64), __shfl_xor(L, x, 64), Oo);
-        }
-        if (sl == 0 && wave > 0 && wave < 3) {
-            s_wave[wave][col][0] = M, s_wave[wave][col][1] = L;
-#pragma unroll
-            for (int i = 0; i < 4; i++) s_wave[wave][col][2 + i] = O[i];
+        for (int j = 0; j < GS; j++)
+            if (j < nz) og += ov[j] * wv[j];  // splits past S hold nothing (their registers are never loaded)
+        *reinterpret_cast<fDL*>(&s_go[wave * D + lane * DL]) = og;
+        if (lane == 0) {
+            s_gm[wave] = mg;
+            s_gl[wave] = lg;
         }
         __syncthreads();
-        if (wave == 0 && sl == 0) {  // waves 1 and 2, in order
+        if (tid < D) {
 #pragma unroll
-            for (int w = 1; w < 3; w++)
-                merge(s_wave[w][col][0], s_wave[w][col][1],
-                      f32x4{s_wave[w][col][2], s_wave[w][col][3], s_wave[w][col][4], s_wave[w][col][5]});
-            const float inv = 1.0f / L;
-            f32x4 res;
-#pragma unroll
-            for (int i = 0; i < 4; i++) res[i] = O[i] * inv * sigmoid(gate[i]);
-            *reinterpret_cast<f32x4*>(&a.out[((size_t)t * a.NH + h) * D + d0]) = res;
+            for (int gi = 0; gi < 4; gi++) {  // the window's groups in order
+                const float gl = s_gl[gi];
+                if (gl > 0.f) {
+                    const float gm = s_gm[gi], mn = fmaxf(M, gm);
+                    const float cf = L > 0.f ? exp2_fast(M - mn) : 0.f, cg = exp2_fast(gm - mn);
+                    L = L * cf + gl * cg;
+                    O = O * cf + s_go[gi * D + tid] * cg;
+                    M = mn;
+                }
+            }
         }
-        __syncthreads();  // s_wave is rewritten by the next unit
+        __syncthreads();  // s_go is rewritten by the next window
     }
-    // every flag of the head has been seen by the polling wave: advance the head's epoch (every combiner
-    // stores the same value)
-    if (tid == 0) __hip_atomic_store(epoch, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < D) a.out[((size_t)t * a.NH + h) * D + tid] = O / L * sigmoid(gate);
+    if (__ballot(gave_up) != 0 && lane == 0) report_wait(a, kWaitCombineFlags);
+    if (tid == 0)  // this combiner is done: its share of the head's epoch step (see kEpochStep)
+        __hip_atomic_fetch_add(a.ep + kvh, (unsigned long long)(kEpochStep / (a.ncomb / a.NKV)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int FUSED, int IN_DT>
@@ -687,7 +621,6 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     constexpr float TAU = 8.f;
     constexpr int TILE_E = 2 * BLKE;        // a slot: the K part then the V part of one block
     constexpr int PIECES = BLKE * 2 / 1024;  // 1 KB direct loads per part
-    constexpr int OSTRIDE = D + 4;
     constexpr int SPIN_MAX = 1 << 22;
     static_assert(2 * PIECES <= 63, "one tile's loads must fit the load counter");
 
@@ -699,48 +632,58 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     __shared__ int s_cnt[2 * NCW];
     int* ready = s_cnt;        // [NCW] tiles published per pair
     int* freed = s_cnt + NCW;  // [NCW] tiles released per pair
-    __shared__ float sM[NCW][RMAX], sL[NCW][RMAX], sF[NCW][RMAX];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = lane & 15, g = lane >> 4;
-    const int z = blockIdx.x, kvh = blockIdx.y;
+    // one-launch decode: the first a.ncomb workgroups of the grid combine, one output row each
+    const bool one = FUSED && a.out != nullptr;
+    if constexpr (FUSED) {
+        if (one && (int)blockIdx.x < a.ncomb) {
+            combine_row<D, IN_DT>(a, smem, blockIdx.x);
+            return;
+        }
+    }
+    const int sidx = blockIdx.x - (one ? a.ncomb : 0);
+    const int kvh = sidx / a.n_split, z = sidx - kvh * a.n_split;
     const int G = a.NH / a.NKV;
     const int rows = min(RMAX, a.n * G);
     const int maxlen = a.pos + a.n;
-    // the in-launch combine's epoch word of this KV head, read now (device-coherent, unconditionally: a
+    // one-launch: this launch's epoch tag (see kEpochStep), read now (device-coherent, unconditionally: a
     // zero-sized range without the combine reads 0 and touches no memory) so that its latency hides behind
-    // the prologue; it must be read before this workgroup sets its ready flag
-    int epoch_word = 0;
+    // the prologue; it must be read before this workgroup stores its records
+    unsigned epoch = 0;
     if constexpr (FUSED) {
-        const bool comb = a.out != nullptr;
-        const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(comb ? a.ready + kvh : a.ready, (short)0, comb ? 4 : 0, 0x00020000);
-        epoch_word = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, kScDevice);
+        const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(one ? a.ep + kvh : a.ep, (short)0, one ? 8 : 0, 0x00020000);
+        const unsigned long long cnt = __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(rep, 0, 0, kScDevice));
+        epoch = (unsigned)(cnt / kEpochStep) + 1u;
     }
-    int kb, ke;
-    split_keys(a, z, maxlen, kb, ke);
-    const int ntile_wg = (ke - kb + 31) >> 5;
+    // ---- this split's tiles: blocks z, z + S, z + 2S, ... of the nb blocks of the head that hold keys
+    // (strided: at every step the splits of a head read neighbouring blocks, so the cache is swept front to
+    // back, which streams faster than one contiguous range per workgroup)
+    const int S = a.n_split;
+    const int nb = (maxlen + 31) >> 5;
+    const int ntile = z < nb ? (nb - 1 - z) / S + 1 : 0;
     const bool loader = wave >= NCW;
-    const int pr = loader ? wave - NCW : wave;                        // pair
-    const int ntp = ntile_wg > pr ? (ntile_wg - pr + NCW - 1) / NCW : 0;  // tiles pr, pr + NCW, ...
+    const int pr = loader ? wave - NCW : 0;                 // loader p streams the tiles p, p + 2, ... of pair p
+    const int ntp = ntile > pr ? (ntile - pr + 1) / 2 : 0;  // its tile count
     // first new position: the prologue appends the new rows to the caches, and a tile holding any of them
     // is copied only once those stores are complete (after the prologue), so it arrives whole
     const int new_lo = FUSED ? a.pos : maxlen;
-    if (tid < 2 * NCW) ready[tid] = 0;  // ready[] and freed[] (published by the barrier below)
+    if (tid < 2 * NCW) s_cnt[tid] = 0;  // ready[] and freed[] (published by the barrier below)
 
-    // ---- loaders: the first two tiles of the pair go out at once ---------------------------------
-    const int nload = ke > kb ? ((ke - 1) >> 5) - (kb >> 5) + 1 : 0;
-    const int bstride = BLKE * 2;  // bytes between consecutive blocks of one head
-    const size_t part0 = kv_part(kb, kvh, a.cap, D);
+    const int bstride = BLKE * 2;  // bytes between consecutive blocks of one head (nb * bstride < 2^31: host-checked)
+    const size_t head0 = kv_part(0, kvh, a.cap, D);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.kc) + part0, (short)0, nload * bstride, 0x00020000);
+        const_cast<uint16_t*>(a.kc) + head0, (short)0, nb * bstride, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.vc) + part0, (short)0, nload * bstride, 0x00020000);
-    auto slot = [&](int i) { return ring + (pr * 2 + (i & 1)) * TILE_E; };
-    auto tile_of = [&](int i) { return pr + NCW * i; };        // the pair's i-th tile of the workgroup
-    auto has_new = [&](int i) { return FUSED && kb + 32 * tile_of(i) + 32 > new_lo; };  // holds new positions
-    auto dma = [&](int i) {  // the pair's i-th tile into slot i & 1 (range-checked: past nload, zeros)
-        f16* dst = slot(i);
-        const int off = tile_of(i) * bstride + lane * 16;
+        const_cast<uint16_t*>(a.vc) + head0, (short)0, nb * bstride, 0x00020000);
+    auto blk_of = [&](int t) { return z + S * t; };
+    // tile t: loader t & 1, its (t >> 1)-th tile, in that loader's slot (t >> 1) & 1
+    auto slot_of = [&](int t) { return ring + ((t & 1) * 2 + ((t >> 1) & 1)) * TILE_E; };
+    auto has_new = [&](int t) { return FUSED && kBlk * blk_of(t) + kBlk > new_lo; };  // holds new positions
+    auto dma = [&](int t) {  // tile t into its slot
+        f16* dst = slot_of(t);
+        const int off = blk_of(t) * bstride + lane * 16;
 #pragma unroll
         for (int j = 0; j < PIECES; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(dst + j * 512), 16,
@@ -750,11 +693,18 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(dst + BLKE + j * 512),
                                                      16, off + j * 1024, 0, 0, 0);
     };
+    // new rows this workgroup appends: those in blocks it owns (the n <= 8 new rows span at most two blocks)
+    int t_lo = 0, t_hi = 0;
+    if constexpr (FUSED) {
+        const int B0 = a.pos >> 5, B1 = (maxlen - 1) >> 5;
+        const bool own0 = B0 % S == z, own1 = B1 % S == z;
+        t_lo = own0 ? 0 : kBlk * B1 - a.pos;
+        t_hi = own1 ? a.n : min(a.n, kBlk * (B0 + 1) - a.pos);
+        if (!own0 && !own1) t_lo = t_hi = 0;
+    }
     // ---- compute waves: query rows (and, fused, the new K/V rows) normalized and rotated ------------
     // Two rows per compute wave per pass, 32 lanes per row, DPL2 dims per lane.
     const int hw = lane >> 5, hl = lane & 31, d0 = hl * DPL2;
-    const int t_lo = FUSED ? max(a.pos, kb) - a.pos : 0;
-    const int t_hi = FUSED ? max(t_lo, min(maxlen, ke) - a.pos) : 0;
     const int half_r = a.R >> 1;
     const bool rot = FUSED && d0 < a.R;  // lanes whose DPL2 dims are rotated (R/2 is a multiple of DPL2)
     auto issue_row = [&](float (&x)[DPL2], float (&cv)[2 * DPL2], const void* src, size_t off, int p, bool valid) {
@@ -885,8 +835,8 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         asm volatile("" ::: "memory");
         // a tile holding new positions waits until they are appended (after the prologue); such tiles
         // are the pair's last, so the copies still go out in tile order
-        if (ntp > 0 && !has_new(0)) dma(0);
-        if (ntp > 1 && !has_new(1)) dma(1);
+        if (ntp > 0 && !has_new(pr)) dma(pr);
+        if (ntp > 1 && !has_new(pr + 2)) dma(pr + 2);
     }
     // a bare barrier: the LDS writes and cache-row stores above are complete (the compute waves waited
     // for them), and a fenced one would also wait for the copies in flight
@@ -902,27 +852,21 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (loader) {
-        // ---- stream the pair's tiles; publish each once landed -------------------------------------
-        if (ntp > 0 && has_new(0)) dma(0);  // the tiles the prologue held back, in tile order
-        if (ntp > 1 && has_new(1)) dma(1);
+        // ---- stream this pair's tiles; publish each once landed --------------------------------------
+        if (ntp > 0 && has_new(pr)) dma(pr);  // the tiles the prologue held back, in tile order
+        if (ntp > 1 && has_new(pr + 2)) dma(pr + 2);
+        const uint32_t raddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&ready[pr]));
+        const uint32_t faddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&freed[pr]));
         for (int i = 0; i < ntp; i++) {
             if (i + 1 < ntp) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PIECES));  // tile i landed, i+1 may not
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            // publish: the waits above already order the tile before the counter, and a release store
-            // would also wait for the next tile's loads (the whole load counter), halving the pipeline
-            {
-                // an LDS store the compiler can see would wait for the next tile's loads too (it cannot
-                // tell the counter from the copies' destination); the waits above already order it
-                const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&ready[pr]));
-                asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(i + 1) : "memory");
-            }
+            // publish: the waits above already order the tile before the counter; an LDS store the compiler
+            // can see would also wait for the next tile's copies (it cannot tell the counter from their
+            // destination), halving the pipeline
+            asm volatile("ds_write_b32 %0, %1" ::"v"(raddr), "v"(i + 1) : "memory");
             if (i + 2 < ntp) {
-                // a tile with new positions (the pair's last) goes out only once the appends are complete:
-                // wait for everything this wave has in flight
-
-                // wait for the compute wave to free the slot; read through inline assembly as well, since
-                // an LDS read the compiler can see would first wait for all of this wave's copies
-                const uint32_t faddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&freed[pr]));
+                // wait for the compute wave to free the slot (read through inline assembly as well: an LDS
+                // read the compiler can see would first wait for every copy of this wave)
                 for (int spin = 0;; spin++) {
                     int f;
                     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(f) : "v"(faddr) : "memory");
@@ -933,18 +877,20 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                     }
                     __builtin_amdgcn_s_sleep(1);
                 }
-                dma(i + 2);
+                dma(pr + 2 * (i + 2));
             }
         }
     } else {
-        // ---- compute the pair's tiles from the slots ----------------------------------------------
+        // ---- compute wave p takes the pair's tiles p, p + 2, ... from the slots ------------------------
         const int rcol = c & 7;
-        const int lim = rcol < rows ? min(a.pos + rcol / G + 1, ke) : 0;
+        const int lim = rcol < rows ? a.pos + rcol / G + 1 : 0;
         f16x8 qreg[NKS];
 #pragma unroll
         for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
-        for (int i = 0; i < ntp; i++) {
-            for (int spin = 0; __hip_atomic_load(&ready[pr], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1;
+        const int ntc = ntile > wave ? (ntile - wave + 1) / 2 : 0;
+        for (int i = 0; i < ntc; i++) {
+            const int t = wave + 2 * i;
+            for (int spin = 0; __hip_atomic_load(&ready[wave], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1;
                  spin++) {
                 if (spin >= SPIN_MAX) {
                     if (lane == 0) report_wait(a, kWaitRingCompute);
@@ -952,7 +898,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
-            const f16* sl = slot(i);
+            const f16* sl = slot_of(t);
             f16x8 kt[NKS][2], vt[NDT];
 #pragma unroll
             for (int kk = 0; kk < NKS; kk++)
@@ -962,9 +908,9 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             for (int dt = 0; dt < NDT; dt++) vt[dt] = *reinterpret_cast<const f16x8*>(sl + BLKE + (dt * 64 + lane) * 8);
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile is in registers, the slot is free
             asm volatile("" ::: "memory");
-            __hip_atomic_store(&freed[pr], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(&freed[wave], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
-            const int tb = kb + 32 * tile_of(i);
+            const int tb = kBlk * blk_of(t);
             if (tb + 32 > maxlen) {
                 // keys from maxlen on: their scores are masked, but V there is whatever the cache memory
                 // holds (P = 0 there, and 0 * NaN is not 0): zero it. V fragment dt: lane (c, g) holds
@@ -1022,69 +968,67 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) acc[dt] = mfma16(vt[dt], pop, acc[dt]);
         }
-    }
-
-    // ---- merge the compute waves (the ring is dead once every wave is here) ---------------------
-    __syncthreads();
-    float* sO = reinterpret_cast<float*>(ring);
-    if (!loader) {
-        float l = l_run;
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        // the lane's column sum, and the hi + lo columns of each query row added: lanes of column c < 8
+        // hold query row c, dims 16 dt + 4 g .. + 3 of fragment dt
+        l_run += __shfl_xor(l_run, 16, 64);
+        l_run += __shfl_xor(l_run, 32, 64);
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[dt][e] += xor8(acc[dt][e]);
-        if (c < 8) {
+    }
+
+    // ---- merge the two compute waves: wave 1 hands its (m, l, o) to wave 0 through LDS (the ring is
+    // dead once every wave is here), wave 0 merges in registers and stores the split's partial rows.
+    // Device-coherent stores (they reach the point every XCD reads from): the combining workgroups of the
+    // one-launch decode read them from other XCDs without any cache-wide write-back
+    float* sO = reinterpret_cast<float*>(ring);  // [RMAX][D]
+    float* sML = sO + RMAX * D;                   // [RMAX][2]
+    __syncthreads();
+    if (wave == 1 && c < 8) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-                *reinterpret_cast<f32x4*>(&sO[(wave * RMAX + c) * OSTRIDE + dt * 16 + g * 4]) = acc[dt];
-            if (g == 0) {
-                sM[wave][c] = m_run;
-                sL[wave][c] = l;
-            }
-        }
+        for (int dt = 0; dt < NDT; dt++) *reinterpret_cast<f32x4*>(&sO[c * D + dt * 16 + g * 4]) = acc[dt];
+        if (g == 0) sML[2 * c] = m_run, sML[2 * c + 1] = l_run;
     }
     __syncthreads();
-    if (tid < rows) {
-        const int r = tid;
-        float M = kNegInf;
+    if (wave == 0 && c < rows) {
+        const float m1 = sML[2 * c], l1 = sML[2 * c + 1];
+        const float M = fmaxf(l_run > 0.f ? m_run : kNegInf, l1 > 0.f ? m1 : kNegInf);
+        const float f0 = l_run > 0.f ? exp2_fast(m_run - M) : 0.f, f1 = l1 > 0.f ? exp2_fast(m1 - M) : 0.f;
+        const float L = l_run * f0 + l1 * f1;
+        const int t = c / G, h = kvh * G + c % G;
+        const int row = (t * a.NH + h) * S + z;  // the host keeps the partial buffer below 2 GiB
+        const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o, (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
-        for (int w = 0; w < NCW; w++)
-            if (sL[w][r] > 0.f) M = fmaxf(M, sM[w][r]);
-        float L = 0.f;
-#pragma unroll
-        for (int w = 0; w < NCW; w++) {
-            const float f = sL[w][r] > 0.f ? exp2_fast(sM[w][r] - M) : 0.f;
-            sF[w][r] = f;
-            L += sL[w][r] * f;
+        for (int dt = 0; dt < NDT; dt++) {
+            const f32x4 o1 = *reinterpret_cast<const f32x4*>(&sO[c * D + dt * 16 + g * 4]);
+            __builtin_amdgcn_raw_buffer_store_b128(acc[dt] * f0 + o1 * f1, rpo, (row * D + dt * 16 + g * 4) * 4, 0, kScDevice);
         }
-        const int t = r / G, h = kvh * G + r % G;
-        const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
-        // device-coherent stores (they reach the point every XCD reads from): the in-launch combine reads
-        // them from other workgroups without any cache-wide write-back
-        __hip_atomic_store(&a.part_ml[row * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&a.part_ml[row * 2 + 1], L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!one && g == 0) {
+            a.part_ml[(size_t)row * 2] = M;
+            a.part_ml[(size_t)row * 2 + 1] = L;
+        }
+        m_run = M, l_run = L;
     }
-    __syncthreads();
-    const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o, (short)0, 0x7fffffff, 0x00020000);
-    for (int idx = tid; idx < rows * (D / 4); idx += 256) {
-        const int r = idx / (D / 4), d = (idx % (D / 4)) * 4;
-        f32x4 o = *reinterpret_cast<const f32x4*>(&sO[r * OSTRIDE + d]) * sF[0][r];
-#pragma unroll
-        for (int w = 1; w < NCW; w++) o += *reinterpret_cast<const f32x4*>(&sO[(w * RMAX + r) * OSTRIDE + d]) * sF[w][r];
-        const int t = r / G, h = kvh * G + r % G;
-        const int row = (t * a.NH + h) * a.n_split + z;  // the host keeps the partial buffer below 2 GiB
-        __builtin_amdgcn_raw_buffer_store_b128(o, rpo, (row * D + d) * 4, 0, kScDevice);
-    }
-    if constexpr (FUSED) {
-        if (a.out != nullptr) combine_ready<D, IN_DT>(a, rows, G, kvh, z, epoch_word + 1);
+    if (one && wave == 0) {
+        // the records go out once every o store of the wave is acknowledged (the wait counts the wave's
+        // memory operations): a record with this launch's tag is the combiner's guarantee that its row's o
+        // is visible device-wide
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        if (g == 0 && c < rows) {
+            const int t = c / G, h = kvh * G + c % G;
+            const int row = (t * a.NH + h) * S + z;
+            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(a.rec, (short)0, 0x7fffffff, 0x00020000);
+            __builtin_amdgcn_raw_buffer_store_b128(f32x4{m_run, l_run, __uint_as_float(epoch), 0.f}, rr, row * 16, 0, kScDevice);
+        }
     }
 }
 
 template <int D>
 constexpr size_t decode_ld_lds() {
-    return (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2;  // ring + Q fragments
+    const size_t stream = (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2;  // ring + Q fragments
+    const size_t comb = (size_t)4 * (D + 2 + kCombGroup) * 4;  // combiner: a window's group sums, maxima, sums, weights
+    return stream > comb ? stream : comb;
 }
 
 template <int D, int FUSED, int IN_DT>
@@ -1092,8 +1036,8 @@ static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
     const dim3 block(256);
     // the in-launch combine: fused (it needs the gate), at most 8 rows (the 16-row kernel has no
-    // registers left for it) and at most kReadyMaxSplits splits
-    if (a.out != nullptr && (!FUSED || rows > 8 || a.n_split > kReadyMaxSplits || a.comb_max < 1))
+    // registers left for it), one combining workgroup per output row
+    if (a.out != nullptr && (!FUSED || rows > 8 || a.ncomb != a.n * a.NH || !a.ep || !a.rec))
         return hipErrorInvalidValue;
     if (rows <= 8) {
         auto kern = k_decode_ld<D, FUSED, IN_DT>;
@@ -1109,7 +1053,8 @@ static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
             if (e != hipSuccess) return e;
             raised.fetch_or(bit, std::memory_order_acq_rel);
         }
-        hipLaunchKernelGGL(kern, dim3(a.n_split, a.NKV, 1), block, shm, s, a);
+        const int ncomb = a.out != nullptr ? a.ncomb : 0;
+        hipLaunchKernelGGL(kern, dim3(ncomb + a.n_split * a.NKV), block, shm, s, a);
     }
     else hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), block, 0, s, a);
     return hipGetLastError();

@@ -44,8 +44,9 @@ struct DecodeArgs {
     float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
     float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
                           // the same launch (nullptr: partials only, for a separate combine)
-    int* ready;           // with out: epoch words and ready flags (ready_ints(NKV) ints, zero at first)
-    int comb_max;         // with out: combining workgroups per KV head at most (NKV * comb_max <= CUs / 2)
+    unsigned long long* ep;  // with out: per KV head, the launch counter the epochs come from (zero at first)
+    float* rec;           // with out: [n*NH][n_split][4] split records (m, l, epoch tag, 0)
+    int ncomb;            // with out: combining workgroups, one per output row (n * NH), first in the grid
     int cap;              // capacity (positions) of the caches kc, vc
     int* err;             // a bounded wait that gives up stores its kWait* code here (nullptr: not reported)
     int spin_max;         // polls of the in-launch combine's flag wait before it gives up
@@ -54,22 +55,19 @@ struct DecodeArgs {
 
 // Codes a kernel stores into DecodeArgs::err when a bounded wait gives up (the launch's output is then
 // not valid; the host reports QWATTN_ETIMEOUT)
-constexpr int kWaitCombineFlags = 1;  // the in-launch combine's poller: a split's ready flag never came
-constexpr int kWaitCombineSeen = 2;   // a merging wave: the poller's marks never came
+constexpr int kWaitCombineFlags = 1;  // a combining workgroup: a split's record never came
 constexpr int kWaitRingLoad = 3;      // a loader wave: its compute wave never released a slot
 constexpr int kWaitRingCompute = 4;   // a compute wave: its loader wave never published a tile
 constexpr int kSpinDefault = 1 << 22; // default DecodeArgs::spin_max (seconds of polling)
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 
-// Splits at most of the one-launch decode (its combiners track the splits in LDS)
-constexpr int kReadyMaxSplits = 2048;
-// Layout of DecodeArgs::ready (ints): the KV heads' epoch words first, then per KV head a fixed region
-// of kReadyMaxSplits flags (line-aligned). A head keeps its word and region whatever the splits of a
-// launch, so every flag location only ever holds epochs of its own head, all below the head's current one.
-__host__ __device__ constexpr int ready_flags_at(int NKV) { return (NKV + 31) / 32 * 32; }
-__host__ __device__ constexpr size_t ready_ints(int NKV) {
-    return (size_t)ready_flags_at(NKV) + (size_t)NKV * kReadyMaxSplits;
-}
+// One-launch decode: each combining workgroup adds kEpochStep / (combiners per KV head) to its head's
+// counter when done, so a launch whose combiners have all finished advances the counter by exactly
+// kEpochStep whatever their number (1..8), and floor(counter / kEpochStep) + 1 is the epoch of the next
+// launch — also for a participant that reads the counter after some combiners of its own launch are done.
+constexpr unsigned kEpochStep = 840;  // lcm(1, ..., 8)
+constexpr int kCombSlots = 128;       // split partials a combining workgroup stages in LDS at once
+constexpr int kCombGroup = 32;        // splits merged together (in a fixed order) once all are staged
 
 struct CombineArgs {
     const float* part_o;

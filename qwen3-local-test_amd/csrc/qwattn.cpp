@@ -25,7 +25,8 @@ struct qwattn_ctx {
     float* rope = nullptr;       // [max_ctx][R/2][2]
     float* part_o = nullptr;     // [split_rows][max_splits][D]
     float* part_ml = nullptr;    // [split_rows][max_splits][2]
-    int* ready = nullptr;        // qwattn_decode: epoch words and per-split ready flags (qw::ready_ints)
+    unsigned long long* ep = nullptr;  // qwattn_decode: per KV head launch counters (epochs, qw::kEpochStep)
+    float* rec = nullptr;        // qwattn_decode: [split_rows][max_splits][4] split records (m, l, tag, 0)
     float* q32 = nullptr;        // [max_tokens][NH][D] layer-path query (fp32)
     void* q16 = nullptr;         // [max_tokens][NH][D] layer-path query (fp16, pre-scaled)
     float* pf_part = nullptr;    // prefill: partials of split query tiles (qw::PrefillArgs::part)
@@ -101,8 +102,7 @@ int take_wait_error(qwattn_ctx* c) {
     if (!c->wait_err_host) return QWATTN_OK;
     const int code = __atomic_exchange_n(c->wait_err_host, 0, __ATOMIC_ACQ_REL);
     if (code == 0) return QWATTN_OK;
-    static const char* what[] = {"", "a split's ready flag never arrived at the in-launch combine",
-                                 "the combine's merging waves never saw the poller's marks",
+    static const char* what[] = {"", "a split's record never arrived at the in-launch combine", "",
                                  "a loader wave's slot was never released", "a compute wave's tile was never published"};
     return fail(c, QWATTN_ETIMEOUT, "a bounded wait in an earlier decode launch gave up (%s); its output is not valid",
                 code >= 1 && code <= 4 ? what[code] : "unknown wait");
@@ -115,6 +115,9 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
     if ((long long)pos + n > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow (%d + %d > %d)", pos, n, c->cfg.max_ctx);
     if ((long long)pos + n > kv_cap) return fail(c, QWATTN_ERANGE, "context overflow: %d + %d rows exceed the K/V cache capacity %d", pos, n, kv_cap);
     if (kv_cap % 32) return fail(c, QWATTN_EINVAL, "K/V cache capacity %d is not a multiple of 32", kv_cap);
+    // the kernels address one KV head's part of a cache with 32-bit byte offsets
+    if ((long long)kv_cap * c->cfg.head_dim * 2 >= (1ll << 31))
+        return fail(c, QWATTN_EINVAL, "K/V cache capacity %d: a KV head's part exceeds 2 GiB", kv_cap);
     return take_wait_error(c);
 }
 
@@ -122,17 +125,17 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
 // nb = ceil(maxlen / 32) blocks that hold keys, chunk z takes [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr))
 // with cq = nb / S, cr = nb % S (the first cr chunks one block longer). A requested count n_split > 0 is
 // used as given (the reference's 64, src/qwen4_vk.cpp:974-978, or BASELINE's 1,024), capped at max_splits
-// and at nb: a chunk holds at least one block. n_split = 0 picks one workgroup per CU: CUs / (NKV x the
-// decode kernel's 16-row slices) chunks.
+// and at nb: a chunk holds at least one block. n_split = 0 picks one workgroup per CU: (CUs - `reserve`,
+// the one-launch decode's combining workgroups) / (NKV x the decode kernel's 16-row slices) chunks.
 struct Split {
     int S, cq, cr;
 };
 
-Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split) {
+Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int reserve = 0) {
     const int nb = (maxlen + 31) / 32;
     const int rows = n * (c->cfg.n_heads / c->cfg.n_kv_heads);
     const int slices = rows <= 8 ? 1 : (rows + 15) / 16;  // the decode kernel's 16-row slices (grid.z)
-    int S = n_split > 0 ? n_split : std::max(1, c->n_cu / (c->cfg.n_kv_heads * slices));
+    int S = n_split > 0 ? n_split : std::max(1, (c->n_cu - reserve) / (c->cfg.n_kv_heads * slices));
     S = std::max(1, std::min({S, c->cfg.max_splits, nb}));
     return Split{S, nb / S, nb % S};
 }
@@ -148,7 +151,7 @@ qw::DecodeArgs decode_args(const qwattn_ctx* c, const void* q, const void* knew,
     a.pos = pos, a.n = n, a.NH = g.n_heads, a.NKV = g.n_kv_heads, a.R = g.rope_dim;
     a.cq = sp.cq, a.cr = sp.cr, a.n_split = sp.S;
     a.eps = g.rms_eps, a.q_scale = qw::kLog2eHost / std::sqrt((float)g.head_dim);
-    a.out = nullptr, a.ready = nullptr, a.comb_max = 0, a.cap = kv_cap;
+    a.out = nullptr, a.ep = nullptr, a.rec = nullptr, a.ncomb = 0, a.cap = kv_cap;
     a.err = c->wait_err_dev, a.spin_max = c->spin_max, a.epoch_skew = c->epoch_skew;
     return a;
 }
@@ -204,7 +207,8 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->rope, sizeof(float) * rope_n) == hipSuccess &&
               hipMalloc(&c->part_o, sizeof(float) * part * D) == hipSuccess &&
               hipMalloc(&c->part_ml, sizeof(float) * part * 2) == hipSuccess &&
-              hipMalloc(&c->ready, sizeof(int) * qw::ready_ints(NKV)) == hipSuccess &&
+              hipMalloc(&c->ep, sizeof(unsigned long long) * NKV) == hipSuccess &&
+              hipMalloc(&c->rec, sizeof(float) * 4 * part) == hipSuccess &&
               hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess &&
               hipHostMalloc(&c->wait_err_host, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
               hipHostGetDevicePointer((void**)&c->wait_err_dev, c->wait_err_host, 0) == hipSuccess;
@@ -219,7 +223,8 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
         (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
         hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
         hipMemset(c->pf_cnt, 0, sizeof(int) * pf_slots) != hipSuccess ||
-        hipMemset(c->ready, 0, sizeof(int) * qw::ready_ints(NKV)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipMemset(c->ep, 0, sizeof(unsigned long long) * NKV) != hipSuccess ||
+        hipMemset(c->rec, 0, sizeof(float) * 4 * part) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
         return fail(nullptr, QWATTN_EHIP, "initializing the rope table failed");
     }
@@ -232,7 +237,7 @@ int qwattn_destroy(qwattn_ctx* c) {
     if (!c) return QWATTN_OK;
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
-    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ready,
+    for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ep, (void*)c->rec,
                     (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
@@ -435,16 +440,17 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     if (n * G > 32 || n > 8)
         return fail(c, QWATTN_EINVAL, "qwattn_decode: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
                     "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
-    const Split sp = pick_split(c, pos + n, n, n_split);
+    // up to 8 query rows per KV head the combine runs inside the attend launch, in one combining
+    // workgroup per output row (first in the grid); the 16-row-slice kernel (verify) is followed by the
+    // combine kernel. Combining workgroups wait for the streaming ones: at most half the CUs may hold one,
+    // so the others always have room to run
+    const int ncomb = n * g.n_heads;
+    const bool one = n * G <= 8 && 2 * ncomb <= c->n_cu;
+    const Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0);
     const int used = sp.S;
     DeviceGuard dg(c->device);
-    // up to 8 query rows the combine runs inside the attend launch; the 16-row-slice kernel (verify) is
-    // followed by the combine kernel. In-launch combiners wait for other workgroups: at most half the CUs
-    // may hold one, so the others always have room to run
-    const int comb_max = c->n_cu / 2 / g.n_kv_heads;
-    const bool one = n * G <= 8 && comb_max >= 1 && used <= qw::kReadyMaxSplits;
     qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
-    if (one) a.out = out, a.ready = c->ready, a.comb_max = comb_max;
+    if (one) a.out = out, a.ep = c->ep, a.rec = c->rec, a.ncomb = ncomb;
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     if (!one) {
         qw::CombineArgs ca{c->part_o, c->part_ml, qg, out, n, g.n_heads, used};
