@@ -968,54 +968,68 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) acc[dt] = mfma16(vt[dt], pop, acc[dt]);
         }
-        // the lane's column sum, and the hi + lo columns of each query row added: lanes of column c < 8
-        // hold query row c, dims 16 dt + 4 g .. + 3 of fragment dt
-        l_run += __shfl_xor(l_run, 16, 64);
+        l_run += __shfl_xor(l_run, 16, 64);  // the column's sum over the lane groups
         l_run += __shfl_xor(l_run, 32, 64);
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[dt][e] += xor8(acc[dt][e]);
     }
 
-    // ---- merge the two compute waves: wave 1 hands its (m, l, o) to wave 0 through LDS (the ring is
-    // dead once every wave is here), wave 0 merges in registers and stores the split's partial rows.
-    // Device-coherent stores (they reach the point every XCD reads from): the combining workgroups of the
-    // one-launch decode read them from other XCDs without any cache-wide write-back
-    float* sO = reinterpret_cast<float*>(ring);  // [RMAX][D]
-    float* sML = sO + RMAX * D;                   // [RMAX][2]
+    // ---- merge the two compute waves: each hands the other the raw accumulators of the other's half of
+    // the dims (and its running max and sum) through LDS (the ring is dead once every wave is here), then
+    // merges its own half in registers, adds each query row's hi and lo columns and stores its half of the
+    // split's partial rows. Device-coherent stores (they reach the point every XCD reads from): the
+    // combining workgroups of the one-launch decode read them from other XCDs without any cache-wide
+    // write-back
+    constexpr int NDH = NDT / NCW;                // 16-dim fragments per compute wave
+    float* sO = reinterpret_cast<float*>(ring);   // [NCW][NDH][64 lanes][4]
+    float* sML = sO + NCW * NDH * 256;             // [NCW][16 columns][2]
     __syncthreads();
-    if (wave == 1 && c < 8) {
+    // W: this compute wave (a compile-time constant, so every register index below is static)
+    auto hand_over = [&](auto W) {
+        constexpr int OT = 1 - decltype(W)::value;
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) *reinterpret_cast<f32x4*>(&sO[c * D + dt * 16 + g * 4]) = acc[dt];
-        if (g == 0) sML[2 * c] = m_run, sML[2 * c + 1] = l_run;
-    }
+        for (int j = 0; j < NDH; j++)  // the other wave's half, in lane order
+            *reinterpret_cast<f32x4*>(&sO[((OT * NDH + j) * 64 + lane) * 4]) = acc[OT * NDH + j];
+        if (g == 0) sML[(decltype(W)::value * 16 + c) * 2] = m_run, sML[(decltype(W)::value * 16 + c) * 2 + 1] = l_run;
+    };
+    if (wave == 0) hand_over(std::integral_constant<int, 0>{});
+    else if (wave == 1) hand_over(std::integral_constant<int, 1>{});
     __syncthreads();
-    if (wave == 0 && c < rows) {
-        const float m1 = sML[2 * c], l1 = sML[2 * c + 1];
+    auto merge_store = [&](auto W) {
+        constexpr int WV = decltype(W)::value;
+        const float m1 = sML[((1 - WV) * 16 + c) * 2], l1 = sML[((1 - WV) * 16 + c) * 2 + 1];
         const float M = fmaxf(l_run > 0.f ? m_run : kNegInf, l1 > 0.f ? m1 : kNegInf);
         const float f0 = l_run > 0.f ? exp2_fast(m_run - M) : 0.f, f1 = l1 > 0.f ? exp2_fast(m1 - M) : 0.f;
         const float L = l_run * f0 + l1 * f1;
-        const int t = c / G, h = kvh * G + c % G;
-        const int row = (t * a.NH + h) * S + z;  // the host keeps the partial buffer below 2 GiB
-        const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o, (short)0, 0x7fffffff, 0x00020000);
+        f32x4 o[NDH];
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            const f32x4 o1 = *reinterpret_cast<const f32x4*>(&sO[c * D + dt * 16 + g * 4]);
-            __builtin_amdgcn_raw_buffer_store_b128(acc[dt] * f0 + o1 * f1, rpo, (row * D + dt * 16 + g * 4) * 4, 0, kScDevice);
+        for (int j = 0; j < NDH; j++) {
+            const f32x4 o1 = *reinterpret_cast<const f32x4*>(&sO[((WV * NDH + j) * 64 + lane) * 4]);
+            o[j] = acc[WV * NDH + j] * f0 + o1 * f1;  // columns c and c ^ 8 (one query row) share f0, f1
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[j][e] += xor8(o[j][e]);
         }
-        if (!one && g == 0) {
-            a.part_ml[(size_t)row * 2] = M;
-            a.part_ml[(size_t)row * 2 + 1] = L;
+        if (c < rows) {  // lanes of column c < 8 hold query row c: dims 16 dt + 4 g .. + 3 of fragment dt
+            const int t = c / G, h = kvh * G + c % G;
+            const int row = (t * a.NH + h) * S + z;  // the host keeps the partial buffer below 2 GiB
+            const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o, (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < NDH; j++)
+                __builtin_amdgcn_raw_buffer_store_b128(o[j], rpo, (row * D + (WV * NDH + j) * 16 + g * 4) * 4, 0, kScDevice);
+            if (!one && WV == 0 && g == 0) {
+                a.part_ml[(size_t)row * 2] = M;
+                a.part_ml[(size_t)row * 2 + 1] = L;
+            }
         }
         m_run = M, l_run = L;
-    }
-    if (one && wave == 0) {
-        // the records go out once every o store of the wave is acknowledged (the wait counts the wave's
-        // memory operations): a record with this launch's tag is the combiner's guarantee that its row's o
-        // is visible device-wide
+    };
+    if (wave == 0) merge_store(std::integral_constant<int, 0>{});
+    else if (wave == 1) merge_store(std::integral_constant<int, 1>{});
+    if (one) {
+        // the records go out once every o store of the workgroup is acknowledged (the wait counts the
+        // wave's memory operations, the barrier joins both compute waves): a record with this launch's tag
+        // is the combiner's guarantee that its row's o is visible device-wide
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        if (g == 0 && c < rows) {
+        __syncthreads();
+        if (wave == 0 && g == 0 && c < rows) {
             const int t = c / G, h = kvh * G + c % G;
             const int row = (t * a.NH + h) * S + z;
             const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(a.rec, (short)0, 0x7fffffff, 0x00020000);
