@@ -79,6 +79,13 @@ __device__ __forceinline__ void split_keys(const DecodeArgs& a, int z, int maxle
     ke = min(maxlen, b1 * kBlk);
 }
 
+// Tag of a split record of the one-launch decode: the launch's epoch and the KV head. A head's epoch only
+// grows, and the head is part of the tag, so a record left by an earlier launch — whatever its head, split
+// count or row layout was — never carries the tag a combiner waits for.
+__device__ __forceinline__ unsigned long long rec_tag(unsigned long long epoch, int kvh) {
+    return (epoch << 5) | (unsigned)kvh;  // NKV <= 32 (host-checked)
+}
+
 // A bounded wait gave up: the launch's output is not valid. The code goes to the host-visible error word
 // (the first code stored wins: a later one does not overwrite it).
 __device__ __forceinline__ void report_wait(const DecodeArgs& a, int code) {
@@ -116,7 +123,7 @@ __device__ __forceinline__ void merge_batch(float& M, float& L, f32x4& O, const 
 // In-launch log-sum-exp combine of the one-launch decode (attn_combine.comp:13-29): the workgroups
 // first in the grid, one per output row (t, h), each merge that row's split partials while the others
 // stream K/V. A streaming workgroup stores its rows' unnormalized o[D] (device-coherent stores), waits
-// for them to be acknowledged, then stores each row's record (m, l, epoch tag): a record carrying this
+// for them to be acknowledged, then stores each row's record (m, l, 64-bit tag): a record carrying this
 // launch's tag guarantees the row's o is visible. The combining workgroup takes the splits in windows of
 // kCombSlots: wave w owns the kCombGroup splits [wb + 32 w, wb + 32 w + 32) of window wb, lane j < 32
 // polling split wb + 32 w + j's record (one 16-byte device-coherent load per round); each split that
@@ -141,7 +148,8 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
     const int S = a.n_split, G = a.NH / a.NKV;
     const int t = r / a.NH, h = r % a.NH, kvh = h / G;
     const unsigned long long cnt = __hip_atomic_load(a.ep + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned want = (unsigned)(cnt / kEpochStep) + 1u + (unsigned)a.epoch_skew;
+    // this launch's record tag (see rec_tag), skewed by the test hook
+    const unsigned long long want = rec_tag(cnt / kEpochStep + 1u + (unsigned long long)(long long)a.epoch_skew, kvh);
     const float gate = tid < D ? load_in<IN_DT>(a.q, ((size_t)t * a.NH + h) * 2 * D + D + tid) : 0.f;
     const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(a.rec + (size_t)r * S * 4, (short)0, S * 16, 0x00020000);
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + (size_t)r * S * D, (short)0, S * D * 4, 0x00020000);
@@ -158,8 +166,9 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
         while (__ballot(pend) != 0) {
             const f32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(rrec, (pend ? z : 0) * 16, 0, kScDevice);
             const bool last = ++spins > a.spin_max;
-            const bool got = pend && (__float_as_uint(rv[2]) == want || last);
-            gave_up |= got && __float_as_uint(rv[2]) != want;
+            const bool match = (__float_as_uint(rv[2]) | ((unsigned long long)__float_as_uint(rv[3]) << 32)) == want;
+            const bool got = pend && (match || last);
+            gave_up |= got && !match;
             if (got) mj = rv[0], lj = rv[1];
             pend = pend && !got;
             const unsigned long long b = __ballot(got);
@@ -651,11 +660,11 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     // one-launch: this launch's epoch tag (see kEpochStep), read now (device-coherent, unconditionally: a
     // zero-sized range without the combine reads 0 and touches no memory) so that its latency hides behind
     // the prologue; it must be read before this workgroup stores its records
-    unsigned epoch = 0;
+    unsigned long long tag = 0;
     if constexpr (FUSED) {
         const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(one ? a.ep + kvh : a.ep, (short)0, one ? 8 : 0, 0x00020000);
         const unsigned long long cnt = __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(rep, 0, 0, kScDevice));
-        epoch = (unsigned)(cnt / kEpochStep) + 1u;
+        tag = rec_tag(cnt / kEpochStep + 1u, kvh);
     }
     // ---- this split's tiles: blocks z, z + S, z + 2S, ... of the nb blocks of the head that hold keys
     // (strided: at every step the splits of a head read neighbouring blocks, so the cache is swept front to
@@ -1033,7 +1042,8 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             const int t = c / G, h = kvh * G + c % G;
             const int row = (t * a.NH + h) * S + z;
             const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(a.rec, (short)0, 0x7fffffff, 0x00020000);
-            __builtin_amdgcn_raw_buffer_store_b128(f32x4{m_run, l_run, __uint_as_float(epoch), 0.f}, rr, row * 16, 0, kScDevice);
+            __builtin_amdgcn_raw_buffer_store_b128(f32x4{m_run, l_run, __uint_as_float((unsigned)tag), __uint_as_float((unsigned)(tag >> 32))},
+                                                   rr, row * 16, 0, kScDevice);
         }
     }
 }

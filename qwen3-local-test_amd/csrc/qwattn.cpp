@@ -91,6 +91,7 @@ int check_shape(qwattn_ctx* c, const qwattn_config& g) {
     const int G = g.n_heads / g.n_kv_heads;
     if (G > 32 || 128 % G)
         return fail(c, QWATTN_EINVAL, "GQA group %d not supported (a power of two <= 32)", G);
+    if (g.n_kv_heads > 32) return fail(c, QWATTN_EINVAL, "%d KV heads: at most 32 are supported", g.n_kv_heads);
     if (g.max_ctx <= 0 || g.max_tokens <= 0 || g.max_splits <= 0 || g.max_ctx > (1 << 26))
         return fail(c, QWATTN_EINVAL, "bad limits (max_ctx %d, max_tokens %d, max_splits %d)", g.max_ctx, g.max_tokens, g.max_splits);
     if (!(g.rms_eps >= 0.f) || !(g.rope_theta > 0.f)) return fail(c, QWATTN_EINVAL, "bad eps/theta");
@@ -108,16 +109,22 @@ int take_wait_error(qwattn_ctx* c) {
                 code >= 1 && code <= 4 ? what[code] : "unknown wait");
 }
 
-int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
+// Position and capacity checks of a call (c may be NULL: the text then goes to qwattn_last_error(NULL)).
+int check_range(qwattn_ctx* c, const qwattn_config& g, int pos, int n, int kv_cap) {
     if (n < 1) return fail(c, QWATTN_EINVAL, "n = %d", n);
     if (pos < 0) return fail(c, QWATTN_EINVAL, "pos = %d", pos);
-    if (n > c->cfg.max_tokens) return fail(c, QWATTN_EINVAL, "n = %d exceeds max_tokens %d", n, c->cfg.max_tokens);
-    if ((long long)pos + n > c->cfg.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow (%d + %d > %d)", pos, n, c->cfg.max_ctx);
+    if (n > g.max_tokens) return fail(c, QWATTN_EINVAL, "n = %d exceeds max_tokens %d", n, g.max_tokens);
+    if ((long long)pos + n > g.max_ctx) return fail(c, QWATTN_ERANGE, "context overflow (%d + %d > %d)", pos, n, g.max_ctx);
     if ((long long)pos + n > kv_cap) return fail(c, QWATTN_ERANGE, "context overflow: %d + %d rows exceed the K/V cache capacity %d", pos, n, kv_cap);
     if (kv_cap % 32) return fail(c, QWATTN_EINVAL, "K/V cache capacity %d is not a multiple of 32", kv_cap);
     // the kernels address one KV head's part of a cache with 32-bit byte offsets
-    if ((long long)kv_cap * c->cfg.head_dim * 2 >= (1ll << 31))
+    if ((long long)kv_cap * g.head_dim * 2 >= (1ll << 31))
         return fail(c, QWATTN_EINVAL, "K/V cache capacity %d: a KV head's part exceeds 2 GiB", kv_cap);
+    return QWATTN_OK;
+}
+
+int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
+    if (int rc = check_range(c, c->cfg, pos, n, kv_cap)) return rc;
     return take_wait_error(c);
 }
 
@@ -131,27 +138,40 @@ struct Split {
     int S, cq, cr;
 };
 
-Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int reserve = 0) {
+Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, int reserve = 0) {
     const int nb = (maxlen + 31) / 32;
-    const int rows = n * (c->cfg.n_heads / c->cfg.n_kv_heads);
+    const int rows = n * (g.n_heads / g.n_kv_heads);
     const int slices = rows <= 8 ? 1 : (rows + 15) / 16;  // the decode kernel's 16-row slices (grid.z)
-    int S = n_split > 0 ? n_split : std::max(1, (c->n_cu - reserve) / (c->cfg.n_kv_heads * slices));
-    S = std::max(1, std::min({S, c->cfg.max_splits, nb}));
+    int S = n_split > 0 ? n_split : std::max(1, (n_cu - reserve) / (g.n_kv_heads * slices));
+    S = std::max(1, std::min({S, g.max_splits, nb}));
     return Split{S, nb / S, nb % S};
 }
 
-// Arguments of the decode kernels: shape, split and the context's partials and wait settings.
-qw::DecodeArgs decode_args(const qwattn_ctx* c, const void* q, const void* knew, const void* vnew, const float* qn,
-                           const float* kn, const float* rope, const void* kcache, const void* vcache, int kv_cap, int pos, int n,
-                           const Split& sp) {
-    const qwattn_config& g = c->cfg;
+Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int reserve = 0) {
+    return pick_split(c->n_cu, c->cfg, maxlen, n, n_split, reserve);
+}
+
+// Arguments of the decode kernels: shape and split (partials and wait settings: decode_args below).
+qw::DecodeArgs decode_shape_args(const qwattn_config& g, const void* q, const void* knew, const void* vnew,
+                                 const float* qn, const float* kn, const float* rope, const void* kcache,
+                                 const void* vcache, int kv_cap, int pos, int n, const Split& sp) {
     qw::DecodeArgs a{};
     a.q = q, a.knew = knew, a.vnew = vnew, a.qn = qn, a.kn = kn, a.rope = rope;
-    a.kc = (uint16_t*)kcache, a.vc = (uint16_t*)vcache, a.part_o = c->part_o, a.part_ml = c->part_ml;
+    a.kc = (uint16_t*)kcache, a.vc = (uint16_t*)vcache, a.part_o = nullptr, a.part_ml = nullptr;
     a.pos = pos, a.n = n, a.NH = g.n_heads, a.NKV = g.n_kv_heads, a.R = g.rope_dim;
     a.cq = sp.cq, a.cr = sp.cr, a.n_split = sp.S;
     a.eps = g.rms_eps, a.q_scale = qw::kLog2eHost / std::sqrt((float)g.head_dim);
     a.out = nullptr, a.ep = nullptr, a.rec = nullptr, a.ncomb = 0, a.cap = kv_cap;
+    a.err = nullptr, a.spin_max = qw::kSpinDefault, a.epoch_skew = 0;
+    return a;
+}
+
+// ... with the context's partials and wait settings.
+qw::DecodeArgs decode_args(const qwattn_ctx* c, const void* q, const void* knew, const void* vnew, const float* qn,
+                           const float* kn, const float* rope, const void* kcache, const void* vcache, int kv_cap, int pos, int n,
+                           const Split& sp) {
+    qw::DecodeArgs a = decode_shape_args(c->cfg, q, knew, vnew, qn, kn, rope, kcache, vcache, kv_cap, pos, n, sp);
+    a.part_o = c->part_o, a.part_ml = c->part_ml;
     a.err = c->wait_err_dev, a.spin_max = c->spin_max, a.epoch_skew = c->epoch_skew;
     return a;
 }
