@@ -220,6 +220,23 @@ int qwattn_layer_attention(qwattn_ctx* ctx, void* stream, int slot, const void* 
                            const void* v, int in_dtype, const float* qn, const float* kn, float* out,
                            int pos, int n, int n_split);
 
+/* qwattn_decode without a context and without allocating: no reference counterpart. It is for callers
+ * that cannot allocate device memory — code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same work, kernels and results as qwattn_decode for the same shape and splits, but the
+ * per-KV-head launch counters, split records and split partials live in a library-static scratch array of
+ * 32 MiB per GPU (held until the process ends) instead of a context; the call allocates nothing and
+ * frees nothing. `cfg` gives the shape and limits as for qwattn_create (max_splits caps the split count;
+ * the rope table is the caller's, e.g. filled once by qwattn_fill_rope). A split count whose partials do
+ * not fit the scratch (n * NH rows x splits x (D + 6) floats beyond about 32 MiB) is rejected with
+ * QWATTN_EINVAL. `wait_status` (device int, may be NULL): a kernel whose bounded wait gives up stores a
+ * nonzero code there (left untouched otherwise; the caller clears it). Errors are reported through
+ * qwattn_last_error(NULL). Calls that overlap in time on one GPU share the scratch and race: issue them
+ * on one stream, or ordered streams. */
+int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, const void* qg, const void* k,
+                          const void* v, int in_dtype, const float* qn, const float* kn, const float* rope,
+                          void* kcache, void* vcache, int kv_cap, float* out, int pos, int n, int n_split,
+                          int* wait_status, int* used_splits);
+
 #ifdef __cplusplus
 }
 #endif

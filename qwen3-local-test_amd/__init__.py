@@ -67,6 +67,8 @@ def load_library():
         "qwattn_prefill": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
         "qwattn_sync_status": [_P, _P],
+        "qwattn_decode_noalloc": [_I, _P, ctypes.POINTER(Config), _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I,
+                                  _I, _P, ctypes.POINTER(_I)],
         "qwattn_set_wait_limits": [_P, _I, _I],
     }
     for name, args in sig.items():
@@ -249,6 +251,19 @@ class Attention:
     def layer_attention(self, slot, qg, k, v, qn, kn, out, pos, n, n_split=0, stream=None):
         self._check(self.lib.qwattn_layer_attention(self.h, _stream(stream), slot, _ptr(qg), _ptr(k), _ptr(v),
                                                     _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(out), pos, n, n_split))
+
+
+def decode_noalloc(cfg, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, n_split=0, wait_status=None,
+                   device=0, stream=None):
+    """qwattn_decode without a context or allocation (library-static scratch); returns the split count."""
+    lib = load_library()
+    used = ctypes.c_int()
+    rc = lib.qwattn_decode_noalloc(device, _stream(stream), ctypes.byref(cfg), _ptr(qg), _ptr(k), _ptr(v),
+                                   _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope), _ptr(kcache), _ptr(vcache), kv_cap,
+                                   _ptr(out), pos, n, n_split, _ptr(wait_status), ctypes.byref(used))
+    if rc:
+        raise QwattnError(rc, lib.qwattn_last_error(None).decode())
+    return used.value
 
 
 class _DeviceArray:

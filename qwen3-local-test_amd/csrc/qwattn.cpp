@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -558,6 +559,98 @@ int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg
     }
     return qwattn_prefill(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
                           pos, n);
+}
+
+// ---- the decode without allocation ------------------------------------------------------------------
+// qwattn_decode_noalloc keeps what qwattn_decode keeps in the context — the per-KV-head launch counters,
+// the split records and the split partials — in `scratch`, one static array per GPU the library runs on,
+// held until the process ends. Layout: [0, 256) the launch counters (32 u64, one per KV head index; they
+// only grow and are never cleared: static device memory starts at zero), then the records and the
+// partials of the call, laid out per call. In host code `scratch` names a host-side stand-in: its device
+// address, per device, comes from hipGetSymbolAddress (scratch_base) and only that address is used.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+constexpr size_t kScratchData = 256;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_at[kMaxDevices] = {};  // device address of `scratch`, per device (nullptr: not yet)
+int g_scratch_cu[kMaxDevices] = {};            // the device's compute units
+
+// Device address of `scratch` on `device` (made current by the caller) and its CU count, looked up on the
+// first call on that device (the device must be a gfx950).
+int scratch_base(int device, unsigned char** base, int* n_cu) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_at[device]) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+            return fail(nullptr, QWATTN_EHIP, "hipGetDeviceProperties failed on device %d", device);
+        if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+            return fail(nullptr, QWATTN_EINVAL, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+        void* at = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&at, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !at)
+            return fail(nullptr, QWATTN_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+        g_scratch_cu[device] = prop.multiProcessorCount;
+        g_scratch_at[device] = static_cast<unsigned char*>(at);
+    }
+    *base = g_scratch_at[device];
+    *n_cu = g_scratch_cu[device];
+    return QWATTN_OK;
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+}  // namespace
+
+int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, const void* qg, const void* k,
+                          const void* v, int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
+                          void* vcache, int kv_cap, float* out, int pos, int n, int n_split, int* wait_status,
+                          int* used_splits) {
+    if (!cfg) return fail(nullptr, QWATTN_EINVAL, "qwattn_decode_noalloc: null config");
+    const qwattn_config& g = *cfg;
+    if (int rc = check_shape(nullptr, g)) return rc;
+    if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || !out || (!rope && g.rope_dim))
+        return fail(nullptr, QWATTN_EINVAL, "qwattn_decode_noalloc: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(nullptr, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    if (int rc = check_range(nullptr, g, pos, n, kv_cap)) return rc;
+    const int G = g.n_heads / g.n_kv_heads;
+    if (n * G > 32 || n > 8)
+        return fail(nullptr, QWATTN_EINVAL, "qwattn_decode_noalloc: n = %d tokens (n * NH/NKV = %d) exceeds the fused "
+                    "decode kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev || device >= kMaxDevices)
+        return fail(nullptr, QWATTN_EINVAL, "device %d not available (%d devices)", device, ndev);
+    DeviceGuard dg(device);
+    unsigned char* base = nullptr;
+    int n_cu = 0;
+    if (int rc = scratch_base(device, &base, &n_cu)) return rc;
+    const int ncomb = n * g.n_heads;
+    const bool one = n * G <= 8 && 2 * ncomb <= n_cu;
+    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, one ? ncomb : 0);
+    const size_t parts = (size_t)ncomb * sp.S;  // split partial rows
+    const size_t rec_b = align256(parts * 16), ml_b = align256(parts * 8), o_b = align256(parts * g.head_dim * 4);
+    if (kScratchData + rec_b + ml_b + o_b > kScratchBytes)
+        return fail(nullptr, QWATTN_EINVAL, "qwattn_decode_noalloc: %d splits x %d rows of %d dims need %zu bytes of "
+                    "partials, more than its %zu-byte scratch (ask for fewer splits)", sp.S, ncomb, g.head_dim,
+                    rec_b + ml_b + o_b, kScratchBytes - kScratchData);
+    qw::DecodeArgs a = decode_shape_args(g, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, pos, n, sp);
+    a.rec = reinterpret_cast<float*>(base + kScratchData);
+    a.part_ml = reinterpret_cast<float*>(base + kScratchData + rec_b);
+    a.part_o = reinterpret_cast<float*>(base + kScratchData + rec_b + ml_b);
+    a.err = wait_status;
+    if (one) a.out = out, a.ep = reinterpret_cast<unsigned long long*>(base), a.ncomb = ncomb;
+    else a.rec = nullptr;
+    hipError_t e = qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream);
+    if (e == hipSuccess && !one) {
+        qw::CombineArgs ca{a.part_o, a.part_ml, qg, out, n, g.n_heads, sp.S};
+        e = qw::launch_combine(ca, g.head_dim, in_dtype, (hipStream_t)stream);
+    }
+    if (e != hipSuccess) return fail(nullptr, QWATTN_EHIP, "qwattn_decode_noalloc: launch failed: %s", hipGetErrorString(e));
+    if (used_splits) *used_splits = sp.S;
+    return QWATTN_OK;
 }
 
 }  // extern "C"
