@@ -91,7 +91,9 @@ class Workload:
         self.kn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.split = n * (NH // NKV) <= 32 and n <= 8
         self.one_launch = n * (NH // NKV) <= 8  # decode: the combine runs inside the attend launch
-        self.q = None if self.split else torch.zeros((n, NH, D), device="cuda", dtype=torch.float16)
+        # prefill: the kernel normalizes the query rows itself (the layer entry point's path for this
+        # rope width), so no query buffer
+        self.q = None
         self.out = torch.zeros((n, NH, D), device="cuda")
         self.rope = self.att.rope_table()
         self.used = None
@@ -116,15 +118,15 @@ class Workload:
             ev[1].record()
             a.combine(self.qg, self.out, self.n, self.used)
         else:
-            a.qk_norm_rope_append(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.q,
+            a.qk_norm_rope_append(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, None,
                                   self.pos, self.n)
             ev[1].record()
-            a.attend_prefill(self.q, kc, vc, cap, self.qg, self.out, self.pos, self.n)
+            a.attend_prefill_qg(self.qg, self.qn, self.rope, kc, vc, cap, self.out, self.pos, self.n)
         ev[2].record()
 
     def main_only(self, slot):
         """The dominant kernel alone (it is idempotent: the fused decode rewrites the same new rows, the
-        prefill reads the queries the last norm dispatch left)."""
+        prefill reads the projection output and the rows the last K/V append left)."""
         a = self.att
         kc, vc, cap = self.slot_views[slot]
         if self.one_launch:
@@ -134,7 +136,7 @@ class Workload:
             a.decode_partial(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.pos, self.n,
                              self.n_split)
         else:
-            a.attend_prefill(self.q, kc, vc, cap, self.qg, self.out, self.pos, self.n)
+            a.attend_prefill_qg(self.qg, self.qn, self.rope, kc, vc, cap, self.out, self.pos, self.n)
 
     def close(self):
         self.slot_views = []
@@ -244,7 +246,8 @@ def run_workload(wl, steps, warmup, graph):
                       "us_main_each_event": statistics.mean(k_first), "us_combine": statistics.mean(k_second),
                       "splits": wl.used})
     else:
-        r.update({"kernel": "k_prefill", "us_norm_rope": statistics.mean(k_first),
+        r.update({"kernel": "k_prefill (query rows normalized and rotated in the kernel)",
+                  "us_kv_norm_rope_append": statistics.mean(k_first),
                   "us_main_each_event": statistics.mean(k_second)})
     return r
 
@@ -422,7 +425,9 @@ def main():
         "workloads": results,
     }
     if head:
-        line["roofline"] = {"bound": "hbm", "kernel": "k_decode_ld<256,1,0> (one-launch decode, grid 128x2)",
+        line["roofline"] = {"bound": "hbm",
+                            "kernel": f"k_decode_ld<256,1,0> (one launch: {NH} combining + {head['splits']}x{NKV} "
+                                      "streaming workgroups)",
                             "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                             "frac": round(head["frac_hbm_kernel"], 4),
@@ -431,7 +436,9 @@ def main():
                             "kernel_us": head["us_main"]}
     pf = results.get("prefill_2k_on_2k")
     if pf:
-        line["prefill_roofline"] = {"bound": "mfma", "kernel": "k_prefill<256,1> (fp16 query operand, bf16 gate; paired schedule, grid 256)",
+        line["prefill_roofline"] = {"bound": "mfma",
+                                    "kernel": "k_prefill<256,1,true> (query rows normalized and rotated in the "
+                                              "kernel from bf16 projections, bf16 gate; paired schedule, grid 256)",
                                     "achieved": round(pf["algorithmic_flops"] / (pf["us_main"] * 1e-6) / 1e12, 2),
                                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                                     "frac": round(pf["frac_mfma_kernel"], 4),

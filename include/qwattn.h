@@ -130,8 +130,9 @@ int qwattn_kv_slot(const qwattn_ctx* ctx, int slot, void** kcache, void** vcache
  * position p = pos + t and each head: y = x * rsqrt(mean(x^2) + eps) * (1 + w), rotate-half RoPE on
  * the first R dims from `rope` row p; query heads write q_out[t][h], key heads write K cache row p
  * and V is copied to V cache row p. `q_dtype` is QWATTN_F32 (the reference's q_out) or QWATTN_F16
- * (prefill operand: fp16, pre-multiplied by log2(e)/sqrt(D)). `kv_cap` is the caches' capacity;
- * pos + n must not exceed it. */
+ * (prefill operand: fp16, pre-multiplied by log2(e)/sqrt(D)). `q_out` may be NULL: then only the key
+ * and value rows are normalized, rotated and appended (qwattn_attend_prefill_qg does the query rows
+ * itself). `kv_cap` is the caches' capacity; pos + n must not exceed it. */
 int qwattn_qk_norm_rope_append(qwattn_ctx* ctx, void* stream, const void* qg, const void* k,
                                const void* v, int in_dtype, const float* qn, const float* kn,
                                const float* rope, void* kcache, void* vcache, int kv_cap, void* q_out,
@@ -201,9 +202,21 @@ int qwattn_attend_prefill(qwattn_ctx* ctx, void* stream, const void* q, int q_dt
                           const void* kcache, const void* vcache, int kv_cap, const void* qg,
                           int in_dtype, float* out, int pos, int n);
 
+/* qwattn_attend_prefill on the raw projection output: the kernel applies the query half of the
+ * reference's qk_norm_rope dispatch (RMSNorm with weights (1 + qn), rotate-half RoPE from `rope`, the
+ * fp16 operand pre-multiplied by log2(e)/sqrt(D)) to the query half of qg as it loads each query row,
+ * so no query buffer is written or read. The n tokens' key and value rows must already be in the caches
+ * (qwattn_qk_norm_rope_append with q_out = NULL). Needs rope_dim in {0, 32, 64, 128, 256} and
+ * rope_dim <= head_dim (QWATTN_EINVAL otherwise; qwattn_prefill then takes the two-buffer path). */
+int qwattn_attend_prefill_qg(qwattn_ctx* ctx, void* stream, const void* qg, int in_dtype, const float* qn,
+                             const float* rope, const void* kcache, const void* vcache, int kv_cap,
+                             float* out, int pos, int n);
+
 /* The reference's prefill dispatches of one chunk (src/qwen4_vk.cpp:968-992) in two launches:
- * qwattn_qk_norm_rope_append into the context's fp16 query buffer (pre-scaled), then
- * qwattn_attend_prefill on it. n <= max_tokens. */
+ * qwattn_qk_norm_rope_append of the key and value rows, then qwattn_attend_prefill_qg, which normalizes
+ * and rotates the query rows in the attention kernel; with a rope_dim that kernel does not take, the
+ * query rows go through the context's fp16 query buffer (qwattn_qk_norm_rope_append, then
+ * qwattn_attend_prefill). n <= max_tokens. */
 int qwattn_prefill(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
                    int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
                    void* vcache, int kv_cap, float* out, int pos, int n);

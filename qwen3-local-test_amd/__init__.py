@@ -64,6 +64,7 @@ def load_library():
         "qwattn_decode": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, ctypes.POINTER(_I)],
         "qwattn_combine": [_P, _P, _P, _I, _P, _I, _I],
         "qwattn_attend_prefill": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I],
+        "qwattn_attend_prefill_qg": [_P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I],
         "qwattn_prefill": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
         "qwattn_sync_status": [_P, _P],
@@ -191,9 +192,11 @@ class Attention:
 
     # ---- kernels -------------------------------------------------------------------------------------
     def qk_norm_rope_append(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, q_out, pos, n, stream=None):
+        """q_out None: the key and value rows only (for attend_prefill_qg)."""
         self._check(self.lib.qwattn_qk_norm_rope_append(
             self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
-            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(q_out), _DT[q_out.dtype], pos, n))
+            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(q_out) if q_out is not None else None,
+            _DT[q_out.dtype] if q_out is not None else 0, pos, n))
 
     def attend_partial(self, q, kcache, vcache, kv_cap, pos, n, n_split=0, stream=None):
         used = ctypes.c_int()
@@ -225,9 +228,17 @@ class Attention:
         self._check(self.lib.qwattn_attend_prefill(self.h, _stream(stream), _ptr(q), _DT[q.dtype], _ptr(kcache),
                                                    _ptr(vcache), kv_cap, _ptr(qg), _DT[qg.dtype], _ptr(out), pos, n))
 
+    def attend_prefill_qg(self, qg, qn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
+        """The MFMA prefill normalizing and rotating the query half of qg itself (the chunk's K/V rows
+        already appended)."""
+        self._check(self.lib.qwattn_attend_prefill_qg(self.h, _stream(stream), _ptr(qg), _DT[qg.dtype], _ptr(qn),
+                                                      _ptr(rope), _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out),
+                                                      pos, n))
+
     def prefill(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
-        """Norm + rope + append of the chunk (queries into the context's fp16 buffer, pre-scaled), then the
-        MFMA prefill on that buffer: two launches."""
+        """Norm + rope + append of the chunk's K/V rows, then the MFMA prefill normalizing the query rows
+        itself (rope_dim 0, 32, 64, 128 or 256; other widths go through the context's fp16 query buffer):
+        two launches."""
         self._check(self.lib.qwattn_prefill(
             self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
             _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n))

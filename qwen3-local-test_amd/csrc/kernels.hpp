@@ -17,7 +17,7 @@ struct NormRopeArgs {
     const float* rope;   // [>= pos+n][R/2][2]
     uint16_t* kcache;    // blocked fp16
     uint16_t* vcache;    // blocked fp16
-    void* q_out;         // [n][NH][D] fp32, or fp16 pre-scaled by log2(e)/sqrt(D)
+    void* q_out;         // [n][NH][D] fp32, or fp16 pre-scaled by log2(e)/sqrt(D); NULL: K/V rows only
     int pos, n, NH, NKV, R;
     float eps, q_scale;
     int cap;             // capacity (positions) of the caches
@@ -79,7 +79,7 @@ struct CombineArgs {
 hipError_t launch_combine(const CombineArgs& a, int D, int in_dtype, hipStream_t s);
 
 struct PrefillArgs {
-    const void* q;        // [n][NH][D]: fp16 pre-scaled, or fp32 unscaled
+    const void* q;        // [n][NH][D]: fp16 pre-scaled; NULL: the kernel normalizes the query half of qg
     const uint16_t* kc;
     const uint16_t* vc;
     const void* qg;       // gate source
@@ -91,7 +91,18 @@ struct PrefillArgs {
     int* cnt;             // [NKV][slots][4 waves] arrival counters, zero between launches
     int slots;            // split tiles per KV head: pf_split_slots(n_qt, split_all)
     int split_all;        // 0: short and long tiles paired; 1: every tile's keys split over two workgroups
+    // queries normalized in the kernel (q == NULL): RMSNorm weights, rope table [>= pos+n][R/2][2], R
+    // a multiple of 32 with R/32 in {1, 2, 4, 8} and R <= D (pf_fused_rope_ok), or 0
+    const float* qn;
+    const float* rope;
+    int R;
+    float eps;
 };
+// Rope widths the prefill kernel's in-kernel query normalization handles: the rotate-half partner of a
+// lane's dim is then in the same lane.
+__host__ __device__ constexpr bool pf_fused_rope_ok(int R, int D) {
+    return R == 0 || ((R == 32 || R == 64 || R == 128 || R == 256) && R <= D);
+}
 // Split slots per KV head of a launch with n_qt query tiles per KV head.
 __host__ __device__ constexpr int pf_split_slots(int n_qt, int split_all) { return split_all ? n_qt : n_qt / 2; }
 // Floats of one wave's prefill partial: 64 lanes x (D/2 accumulator values + max and sum).

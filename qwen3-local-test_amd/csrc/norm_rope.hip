@@ -72,7 +72,9 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
     constexpr int NR = kNormRows;
     const int hl = threadIdx.x & 31;
     const int item0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * NR;
-    const int heads = a.NH + a.NKV;
+    // without q_out only the key heads are rows of this launch (head index hh = NH + key head)
+    const int q_heads = a.q_out ? a.NH : 0;
+    const int heads = q_heads + a.NKV;
     const int n_items = a.n * heads;
     const int norm_blocks = (n_items + 8 * NR - 1) / (8 * NR);
     if ((int)blockIdx.x >= norm_blocks) {
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         const int item = min(item0 + r, n_items - 1);  // past the end: the last row again, not stored
-        const int t = item / heads, hh = item % heads;
+        const int t = item / heads, hh = item % heads + a.NH - q_heads;
         const bool is_q = hh < a.NH;
         const int h = is_q ? hh : hh - a.NH;
         const size_t src = is_q ? ((size_t)t * a.NH + h) * 2 * D : ((size_t)t * a.NKV + h) * D;
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
     for (int r = 0; r < NR; r++) {
         const int item = item0 + r;
         if (item >= n_items) break;  // uniform over the half-wave
-        const int t = item / heads, hh = item % heads;
+        const int t = item / heads, hh = item % heads + a.NH - q_heads;
         const bool is_q = hh < a.NH;
         const int h = is_q ? hh : hh - a.NH;
         const int p = a.pos + t;
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
 
 template <int D>
 static hipError_t launch_d(const NormRopeArgs& a, int in_dtype, int q_dtype, hipStream_t s) {
-    const int items = a.n * (a.NH + a.NKV);
+    const int items = a.n * ((a.q_out ? a.NH : 0) + a.NKV);
     const int v_lanes = a.NKV * v_groups(a.pos, a.n) * (D / 8);
     const dim3 grid((items + 8 * kNormRows - 1) / (8 * kNormRows) + (v_lanes + 255) / 256), block(256);
     if (in_dtype == 0 && q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 0>), grid, block, 0, s, a);

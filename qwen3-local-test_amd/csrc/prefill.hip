@@ -72,6 +72,121 @@ constexpr int slot_nth(int n, bool pv, int u) {
 
 }  // namespace
 
+// The raw query values of a lane (8 per k-step: one 16-byte load of bf16, two of fp32) and, for R <= 64,
+// its rope (cos, sin) pairs, loaded first and used only in pf_query_fused: every vector load of the
+// prologue is then issued before the first K tiles' copies, so none of them waits behind the copies
+// (vector loads complete in issue order), and the math runs while the copies fly.
+constexpr int kPfRopeEarly = 2;  // k-steps of (cos, sin) loaded with the query (R <= 64)
+template <int D, int IN_DT>
+struct PfQRaw {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typename std::conditional<IN_DT == 0, f32x4, u32x4>::type v[D / 16][IN_DT == 0 ? 2 : 1];
+    f32x4 cs[kPfRopeEarly][4];
+    __device__ __forceinline__ void load(const PrefillArgs& a, int t, int h, int half) {
+        if (a.R > 0 && a.R <= 32 * kPfRopeEarly) {
+            const float* cs_row = a.rope + (size_t)(a.pos + t) * a.R + 16 * half;
+#pragma unroll
+            for (int ks = 0; ks < kPfRopeEarly; ks++)
+                if (32 * ks < a.R)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) cs[ks][k] = *reinterpret_cast<const f32x4*>(cs_row + 32 * ks + 4 * k);
+        }
+        const size_t off = ((size_t)t * a.NH + h) * 2 * D + 8 * half;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ks++) {
+            if constexpr (IN_DT == 0) {
+                const float* p = static_cast<const float*>(a.qg) + off + 16 * ks;
+                v[ks][0] = *reinterpret_cast<const f32x4*>(p);
+                v[ks][1] = *reinterpret_cast<const f32x4*>(p + 4);
+            } else {
+                v[ks][0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qg) + off + 16 * ks);
+            }
+        }
+    }
+    __device__ __forceinline__ float at(int ks, int j) const {
+        if constexpr (IN_DT == 0) return v[ks][j >> 2][j & 3];
+        else return __uint_as_float((j & 1) ? v[ks][0][j >> 1] & 0xffff0000u : v[ks][0][j >> 1] << 16);
+    }
+};
+
+// The Q^T operand of query row (t, h) from the raw projection output: the query half of qg normalized,
+// rotated and scaled in registers — the steps of the norm kernel (norm_rope.hip) for a query row, so a
+// layer's prefill needs no query buffer: y = x * rsqrt(mean(x^2) + eps) * (1 + qn), rotate-half RoPE
+// on dims [0, R) with the (cos, sin) of position pos + t, then fp16(y * q_scale). Lane (col, half) holds
+// dims 16 ks + 8 half + j of the row and its partner lane (col, 1 - half) the other half of every k-step,
+// so the mean of squares is one lane swap, and the rotate-half partner of dim d < R/2 is dim d + R/2 =
+// k-step ks + OFF of the same lane, OFF = R/32 (a template argument, so both operands are static
+// registers). Each k-step (or rotate-half pair) goes from the raw registers to the operand directly;
+// rs = rsqrt term * q_scale folds the score scale into the row factor (0 for a row past the chunk).
+template <int D, int IN_DT, int OFF>
+__device__ __forceinline__ void pf_query_finish(const PrefillArgs& a, const PfQRaw<D, IN_DT>& raw, const float* sW,
+                                                float rs, int t, int half, f16x8 (&qop)[D / 16]) {
+    constexpr int NKS = D / 16;
+    const float* cs_row = a.rope + (size_t)(a.pos + t) * a.R + 16 * half;
+    auto y = [&](int ks, float (&o)[8]) __attribute__((always_inline)) {  // normalized, weighted
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(sW + 16 * ks + 8 * half);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(sW + 16 * ks + 8 * half + 4);
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = raw.at(ks, j) * rs * (j < 4 ? w0[j] : w1[j - 4]);
+    };
+    auto put = [&](int ks, const float (&o)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) qop[ks][j] = (f16)o[j];
+    };
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+        if (ks < OFF) {  // dims d < R/2 and their partners d + R/2
+            float lo[8], hi[8], cs[16];  // (cos, sin) of i = 16 ks + 8 half + j
+            y(ks, lo);
+            y(ks + OFF, hi);
+            if constexpr (OFF <= kPfRopeEarly) {
+#pragma unroll
+                for (int k = 0; k < 16; k++) cs[k] = raw.cs[ks < kPfRopeEarly ? ks : 0][k >> 2][k & 3];
+            } else {
+                load_vec<0, 16>(cs_row, 32 * ks, cs);
+            }
+            float rl[8], rh[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                rl[j] = lo[j] * cs[2 * j] - hi[j] * cs[2 * j + 1];
+                rh[j] = hi[j] * cs[2 * j] + lo[j] * cs[2 * j + 1];
+            }
+            put(ks, rl);
+            put(ks + OFF, rh);
+        } else if (ks >= 2 * OFF) {
+            float o[8];
+            y(ks, o);
+            put(ks, o);
+        }
+    }
+}
+
+template <int D, int IN_DT>
+__device__ __forceinline__ void pf_query_fused(const PrefillArgs& a, const PfQRaw<D, IN_DT>& raw, const float* sW,
+                                               int t, int half, bool row_ok, f16x8 (&qop)[D / 16]) {
+    constexpr int NKS = D / 16;
+    // eight independent partial sums of squares (a single chain would be NKS * 8 instructions long)
+    float s8[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) s8[j] = raw.at(0, j) * raw.at(0, j);
+#pragma unroll
+    for (int ks = 1; ks < NKS; ks++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) s8[j] = __builtin_fmaf(raw.at(ks, j), raw.at(ks, j), s8[j]);
+    float ss = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    // the row factor with the score scale folded in (the rotation is linear, so it commutes); the raw
+    // values of a row past the chunk are those of row 0 (finite), so a zero factor zeroes the row
+    const float rs = row_ok ? 1.0f / sqrtf(ss / (float)D + a.eps) * a.q_scale : 0.f;
+    // the multipliers 1 + qn come from LDS (sW, the same for every row: broadcast reads)
+    if (a.R == 0) pf_query_finish<D, IN_DT, 0>(a, raw, sW, rs, t, half, qop);
+    if constexpr (NKS >= 2) if (a.R == 32) pf_query_finish<D, IN_DT, 1>(a, raw, sW, rs, t, half, qop);
+    if constexpr (NKS >= 4) if (a.R == 64) pf_query_finish<D, IN_DT, 2>(a, raw, sW, rs, t, half, qop);
+    if constexpr (NKS >= 8) if (a.R == 128) pf_query_finish<D, IN_DT, 4>(a, raw, sW, rs, t, half, qop);
+    if constexpr (NKS >= 16) if (a.R == 256) pf_query_finish<D, IN_DT, 8>(a, raw, sW, rs, t, half, qop);
+}
+
 // Key tiles of query tile qt: keys [0, pos + last token of the tile + 1) in 64-key tiles.
 __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, int qt) {
     return (a.pos + min(a.n - 1, (qt + 1) * tok_per_blk - 1) + 1 + PF_KT - 1) / PF_KT;
@@ -83,7 +198,7 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, i
 // (accumulator, reference max, sum) in its half's region of the pair's slot and counts its arrival,
 // unless the partner wave has already arrived; the wave that arrives second merges the two (in a fixed
 // order) and writes the rows, then clears the counter for the next launch.
-template <int D, int IN_DT>
+template <int D, int IN_DT, bool QF>
 __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot) {
     using C = PfCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, BLKE = C::BLKE, TILEE = C::TILEE, LOADS = C::LOADS;
@@ -115,20 +230,22 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     const int maxlen = a.pos + a.n;
 
     // ---- Q^T operand in registers: lane holds row `col`, dims 16*ks + 8*half .. +8 ----------------
+    // the loads are issued here, the operand finished once the first K tiles' copies are in flight.
+    // In-kernel normalization: the norm multipliers 1 + qn go to LDS (after the four tile buffers), loaded
+    // by wave 0 ahead of every other load of the segment
     f16x8 qop[NKS];
-    {
+    PfQRaw<D, IN_DT> qraw;
+    float* sW = reinterpret_cast<float*>(smem + (size_t)4 * C::TILEE * 2);
+    f32x4 wq{};
+    if constexpr (QF) {
+        if (wave == 0 && lane < D / 4) wq = *reinterpret_cast<const f32x4*>(a.qn + 4 * lane);
+        qraw.load(a, row_ok ? t : 0, h, half);
+    } else {
         const size_t qoff = ((size_t)(row_ok ? t : 0) * a.NH + h) * D + 8 * half;
-        // every load issued before the first use, so the row's fetches overlap
 #pragma unroll
-        for (int ks = 0; ks < NKS; ks++) {
-            const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qoff + 16 * ks);
-            qop[ks] = row_ok ? v : f16x8{};
-        }
-        // the Q fragments are only ever matrix-instruction operands: keep them in accumulation registers,
-        // leaving the vector registers to the softmax and the operand staging
-#pragma unroll
-        for (int ks = 0; ks < NKS; ks++) asm volatile("" : "+a"(qop[ks]));
+        for (int ks = 0; ks < NKS; ks++) qop[ks] = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qoff + 16 * ks);
     }
+    asm volatile("" ::: "memory");  // the query loads stay ahead of the copies
 
     f32x16 acc[NDT];
 #pragma unroll
@@ -284,7 +401,10 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
 #pragma unroll
                 for (int e = (i - E0) * 16 / NE; e < (i - E0 + 1) * 16 / NE; e++) {
                     const int sb = e >> 3, j = 2 * (e & 7);
-                    const f16x2 pp = {(f16)exp2_fast(sc[sb][j] - m_use), (f16)exp2_fast(sc[sb][j + 1] - m_use)};
+                    f16x2 pp = {(f16)exp2_fast(sc[sb][j] - m_use), (f16)exp2_fast(sc[sb][j + 1] - m_use)};
+                    // consumed here: otherwise the exponentials are sunk below the rescale branch that
+                    // follows the step and issue after the last matrix instruction instead of beside them
+                    asm volatile("" : "+v"(pp));
                     pcur[sb][j >> 3][j & 7] = pp[0];
                     pcur[sb][j >> 3][(j & 7) + 1] = pp[1];
                     // the row sum adds the same half-precision weights the P.V product uses
@@ -305,6 +425,27 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     // is only overwritten after the first barrier of the loop below.
     copy_tile(rk, sK(lo & 1), lo);
     if (lo + 1 < hi) copy_tile(rk, sK((lo + 1) & 1), lo + 1);
+    {
+        // the Q^T operand, while the copies fly (the query loads were issued before them). sW is free:
+        // every wave finished the previous segment's reads of it many barriers ago
+        if constexpr (QF) {
+            if (wave == 0 && lane < D / 4)
+                *reinterpret_cast<f32x4*>(sW + 4 * lane) = f32x4{1.0f + wq[0], 1.0f + wq[1], 1.0f + wq[2], 1.0f + wq[3]};
+            // a barrier for the LDS write alone (__syncthreads would also wait for the copies in flight)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            pf_query_fused<D, IN_DT>(a, qraw, sW, row_ok ? t : 0, half, row_ok, qop);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ks++) qop[ks] = row_ok ? qop[ks] : f16x8{};
+        }
+        // the Q fragments are only ever matrix-instruction operands: keep them in accumulation registers,
+        // leaving the vector registers to the softmax and the operand staging
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) asm volatile("" : "+a"(qop[ks]));
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     qk_only(sK(lo & 1) + koff_lane);
@@ -356,6 +497,30 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         zero_tail(sV((hi - 1) & 1), hi - 1);
         __syncthreads();
     }
+    // the gates of this wave's rows, kept as loaded (bf16 pairs or fp32). Bf16 gates of a whole tile are
+    // in flight during the last P.V (fp32 ones would need twice the registers and are loaded after it);
+    // a split tile's merging wave loads them after the merge. Accumulator registers 4*q4 .. 4*q4+3 of
+    // lane (col, half) hold dims 32*dt + 8*q4 + 4*half + 0..3.
+    using graw_t = typename std::conditional<IN_DT == 0, f32x4, u32x2_t>::type;
+    graw_t graw[NDT][4];
+    const size_t gb = ((size_t)(row_ok ? t : 0) * a.NH + h) * 2 * D + D + 4 * half;
+    auto load_gates = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                if constexpr (IN_DT == 0)
+                    graw[dt][q4] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.qg) + gb + dt * 32 + 8 * q4);
+                else
+                    graw[dt][q4] = *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(a.qg) + gb + dt * 32 + 8 * q4);
+            }
+    };
+    auto gate = [&](int dt, int q4, int i) __attribute__((always_inline)) -> float {
+        if constexpr (IN_DT == 0) return graw[dt][q4][i];
+        else return __uint_as_float((i & 1) ? graw[dt][q4][i >> 1] & 0xffff0000u : graw[dt][q4][i >> 1] << 16);
+    };
+    constexpr bool kGateEarly = IN_DT == 1;
+    if (kGateEarly && slot < 0) load_gates();
     pv_only(sV((hi - 1) & 1) + voff_lane);
 
     // ---- epilogue: l across the two lane halves, merge of a split tile, normalize, gate, store ----
@@ -430,24 +595,17 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             __builtin_amdgcn_sched_barrier(0);
         });
     }
+    if (!kGateEarly || slot >= 0) load_gates();
     if (row_ok) {
         const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
         const size_t ob = ((size_t)t * a.NH + h) * D;
-        const size_t gb = ((size_t)t * a.NH + h) * 2 * D + D;
-        // accumulator registers 4*q4 .. 4*q4+3 of lane (col, half): dims 32*dt + 8*q4 + 4*half + 0..3.
-        // All gate loads first (the output stores could alias them as far as the compiler knows).
-        float g[NDT][4][4];
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) load_vec<IN_DT, 4>(a.qg, gb + dt * 32 + 8 * q4 + 4 * half, g[dt][q4]);
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
             for (int q4 = 0; q4 < 4; q4++) {
                 f32x4 o;
 #pragma unroll
-                for (int i = 0; i < 4; i++) o[i] = acc[dt][4 * q4 + i] * inv * sigmoid(g[dt][q4][i]);
+                for (int i = 0; i < 4; i++) o[i] = acc[dt][4 * q4 + i] * inv * sigmoid(gate(dt, q4, i));
                 *reinterpret_cast<f32x4*>(a.out + ob + dt * 32 + 8 * q4 + 4 * half) = o;
             }
     }
@@ -457,7 +615,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
 // n_qt-1-p (long) with T = nl + ns key tiles: j = 2p runs the long tile over [x, nl), j = 2p+1 its
 // first x tiles, then the short tile, x = max(0, nl - ceil(T/2)). With n_qt odd the last workgroup
 // runs the middle tile alone.
-template <int D, int IN_DT>
+template <int D, int IN_DT, bool QF>
 __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     const int G = a.NH / a.NKV;
     const int tok_per_blk = PF_ROWS / G;
@@ -488,7 +646,7 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     }
     // one call site, so the segment body exists once in the code object
     for (int s = 0; s < nseg; s++)
-        pf_segment<D, IN_DT>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0);
+        pf_segment<D, IN_DT, QF>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0);
 }
 
 template <int D>
@@ -501,16 +659,22 @@ static hipError_t launch_pf_d(const PrefillArgs& a, int q_dtype, int in_dtype, h
     if (a.n < 1 || a.slots != pf_split_slots(n_qt, a.split_all) || (a.slots > 0 && (!a.part || !a.cnt)))
         return hipErrorInvalidValue;
     const dim3 grid((a.split_all ? 2 : 1) * n_qt * a.NKV), block(256);
-    const size_t shm = 2 * 2 * (size_t)C::TILEE * 2;  // two buffers of a K and a V tile
+    // two buffers of a K and a V tile; with in-kernel query normalization, the D norm multipliers after them
+    const size_t shm = 2 * 2 * (size_t)C::TILEE * 2 + (a.q ? 0 : D * sizeof(float));
     auto go = [&](auto kern) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(kern, grid, block, shm, s, a);
         return hipGetLastError();
     };
-    // fp32 queries reach this kernel converted to the fp16 operand (launch_q_f16)
+    // fp32 queries reach this kernel converted to the fp16 operand (launch_q_f16); without q the kernel
+    // normalizes the query half of qg itself
     if (q_dtype != 2) return hipErrorInvalidValue;
-    return in_dtype == 0 ? go(k_prefill<D, 0>) : go(k_prefill<D, 1>);
+    if (!a.q) {
+        if (!a.qn || (a.R && !a.rope) || !pf_fused_rope_ok(a.R, D)) return hipErrorInvalidValue;
+        return in_dtype == 0 ? go(k_prefill<D, 0, true>) : go(k_prefill<D, 1, true>);
+    }
+    return in_dtype == 0 ? go(k_prefill<D, 0, false>) : go(k_prefill<D, 1, false>);
 }
 
 // fp16(q * scale): the prefill operand from fp32 queries; n4 groups of 4 values

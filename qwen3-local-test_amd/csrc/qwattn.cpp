@@ -384,10 +384,10 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* c, void* stream, const void* qg, cons
                                int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
                                void* vcache, int kv_cap, void* q_out, int q_dtype, int pos, int n) {
     if (!c) return QWATTN_EINVAL;
-    if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || !q_out || (!rope && c->cfg.rope_dim))
+    if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || (!rope && c->cfg.rope_dim))
         return fail(c, QWATTN_EINVAL, "qwattn_qk_norm_rope_append: null pointer");
     if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
-    if (q_dtype != QWATTN_F32 && q_dtype != QWATTN_F16) return fail(c, QWATTN_EINVAL, "q_dtype %d", q_dtype);
+    if (q_out && q_dtype != QWATTN_F32 && q_dtype != QWATTN_F16) return fail(c, QWATTN_EINVAL, "q_dtype %d", q_dtype);
     int rc = check_call(c, pos, n, kv_cap);
     if (rc) return rc;
     DeviceGuard dg(c->device);
@@ -499,6 +499,22 @@ int qwattn_combine(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, fl
     return QWATTN_OK;
 }
 
+// the launch arguments shared by both prefill entry points (split layout sized for n)
+static int prefill_args(qwattn_ctx* c, const void* q, const void* kcache, const void* vcache, int kv_cap,
+                        const void* qg, float* out, int pos, int n, qw::PrefillArgs* a) {
+    const qwattn_config& g = c->cfg;
+    // Few query tiles (two workgroups per tile still fit the CUs): every tile's keys are split over two
+    // workgroups; otherwise short and long tiles are paired. Either way the split tiles fit the slots
+    // sized at creation (n <= max_tokens by check_call; split_all only when 2 * n_qt * NKV <= n_cu).
+    const int n_qt = qw::pf_query_tiles(n, g.n_heads / g.n_kv_heads);
+    const int split_all = 2 * n_qt * g.n_kv_heads <= c->n_cu ? 1 : 0;
+    *a = qw::PrefillArgs{q, (const uint16_t*)kcache, (const uint16_t*)vcache, qg, out, pos, n, g.n_heads,
+                         g.n_kv_heads, qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap, c->pf_part, c->pf_cnt,
+                         qw::pf_split_slots(n_qt, split_all), split_all, nullptr, nullptr, 0, g.rms_eps};
+    if (a->slots > c->pf_slots_per_head) return fail(c, QWATTN_EINVAL, "prefill: %d split slots > %d", a->slots, c->pf_slots_per_head);
+    return QWATTN_OK;
+}
+
 int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtype, const void* kcache,
                           const void* vcache, int kv_cap, const void* qg, int in_dtype, float* out, int pos, int n) {
     if (!c) return QWATTN_EINVAL;
@@ -509,15 +525,8 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     if (rc) return rc;
     const qwattn_config& g = c->cfg;
     DeviceGuard dg(c->device);
-    // Few query tiles (two workgroups per tile still fit the CUs): every tile's keys are split over two
-    // workgroups; otherwise short and long tiles are paired. Either way the split tiles fit the slots
-    // sized at creation (n <= max_tokens by check_call; split_all only when 2 * n_qt * NKV <= n_cu).
-    const int n_qt = qw::pf_query_tiles(n, g.n_heads / g.n_kv_heads);
-    const int split_all = 2 * n_qt * g.n_kv_heads <= c->n_cu ? 1 : 0;
-    qw::PrefillArgs a{q, (const uint16_t*)kcache, (const uint16_t*)vcache, qg, out, pos, n, g.n_heads, g.n_kv_heads,
-                      qw::kLog2eHost / std::sqrt((float)g.head_dim), kv_cap, c->pf_part, c->pf_cnt,
-                      qw::pf_split_slots(n_qt, split_all), split_all};
-    if (a.slots > c->pf_slots_per_head) return fail(c, QWATTN_EINVAL, "prefill: %d split slots > %d", a.slots, c->pf_slots_per_head);
+    qw::PrefillArgs a;
+    if ((rc = prefill_args(c, q, kcache, vcache, kv_cap, qg, out, pos, n, &a))) return rc;
     if (q_dtype == QWATTN_F32) {  // the kernel's operand: fp16(q * log2(e)/sqrt(D)) in the context's query buffer
         HIP_TRY(c, qw::launch_q_f16(static_cast<const float*>(q), c->q16, a.q_scale, (size_t)n * g.n_heads * g.head_dim,
                                     (hipStream_t)stream));
@@ -527,11 +536,42 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     return QWATTN_OK;
 }
 
+int qwattn_attend_prefill_qg(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, const float* qn,
+                             const float* rope, const void* kcache, const void* vcache, int kv_cap, float* out,
+                             int pos, int n) {
+    if (!c) return QWATTN_EINVAL;
+    const qwattn_config& g = c->cfg;
+    if (!qg || !qn || !kcache || !vcache || !out || (!rope && g.rope_dim))
+        return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill_qg: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    if (!qw::pf_fused_rope_ok(g.rope_dim, g.head_dim))
+        return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill_qg: rope_dim %d (needs 0, 32, 64, 128 or 256, <= head_dim %d)",
+                    g.rope_dim, g.head_dim);
+    int rc = check_call(c, pos, n, kv_cap);
+    if (rc) return rc;
+    DeviceGuard dg(c->device);
+    qw::PrefillArgs a;
+    if ((rc = prefill_args(c, nullptr, kcache, vcache, kv_cap, qg, out, pos, n, &a))) return rc;
+    a.qn = qn;
+    a.rope = rope;
+    a.R = g.rope_dim;
+    HIP_TRY(c, qw::launch_prefill(a, g.head_dim, 2, in_dtype, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
 int qwattn_prefill(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
                    const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
                    float* out, int pos, int n) {
     if (!c) return QWATTN_EINVAL;
     if (!out) return fail(c, QWATTN_EINVAL, "qwattn_prefill: null pointer");
+    if (qw::pf_fused_rope_ok(c->cfg.rope_dim, c->cfg.head_dim)) {
+        // the key and value rows appended, then the MFMA prefill normalizing the query rows itself
+        int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap,
+                                            nullptr, QWATTN_F16, pos, n);
+        if (rc) return rc;
+        return qwattn_attend_prefill_qg(c, stream, qg, in_dtype, qn, rope ? rope : c->rope, kcache, vcache, kv_cap,
+                                        out, pos, n);
+    }
     // norm + rope + append into the context's fp16 query buffer, then the MFMA prefill on it
     int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, c->q16,
                                         QWATTN_F16, pos, n);
