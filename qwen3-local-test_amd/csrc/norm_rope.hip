@@ -23,7 +23,11 @@
 
 namespace qw {
 
-constexpr int kNormRows = 4;  // rows per half-wave: every load of the four is issued before any is used
+// rows per half-wave: every load of the rows is issued before any is used. Four when the query rows are
+// in the launch (NH + NKV rows per token); one for a K/V-only launch, whose few rows then spread over
+// four times the workgroups
+constexpr int kNormRows = 4;
+constexpr int kNormRowsKv = 1;
 
 // V groups of a call: 8-position groups overlapping [pos, pos + n)
 __host__ __device__ inline int v_groups(int pos, int n) { return (pos + n - 1) / 8 - pos / 8 + 1; }
@@ -64,12 +68,11 @@ __device__ __forceinline__ void v_copy(const NormRopeArgs& a, int vi) {
     }
 }
 
-template <int D, int IN_DT, int Q_DT>
+template <int D, int IN_DT, int Q_DT, int NR>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(NormRopeArgs a) {
-    // kNormRows rows per half-wave (32 lanes x DPL consecutive dims each): 16-byte loads of the rows and
-    // 16-byte stores of the query rows and of the key rows' blocked-layout pieces
+    // NR rows per half-wave (32 lanes x DPL consecutive dims each): 16-byte loads of the rows and 16-byte
+    // stores of the query rows and of the key rows' blocked-layout pieces
     constexpr int DPL = D / 32;
-    constexpr int NR = kNormRows;
     const int hl = threadIdx.x & 31;
     const int item0 = (blockIdx.x * 8 + (threadIdx.x >> 5)) * NR;
     // without q_out only the key heads are rows of this launch (head index hh = NH + key head)
@@ -159,11 +162,15 @@ template <int D>
 static hipError_t launch_d(const NormRopeArgs& a, int in_dtype, int q_dtype, hipStream_t s) {
     const int items = a.n * ((a.q_out ? a.NH : 0) + a.NKV);
     const int v_lanes = a.NKV * v_groups(a.pos, a.n) * (D / 8);
-    const dim3 grid((items + 8 * kNormRows - 1) / (8 * kNormRows) + (v_lanes + 255) / 256), block(256);
-    if (in_dtype == 0 && q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 0>), grid, block, 0, s, a);
-    else if (in_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 1>), grid, block, 0, s, a);
-    else if (q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 0>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 1>), grid, block, 0, s, a);
+    const int nr = a.q_out ? kNormRows : kNormRowsKv;
+    const dim3 grid((items + 8 * nr - 1) / (8 * nr) + (v_lanes + 255) / 256), block(256);
+    if (!a.q_out) {  // K/V rows only: the query dtype is unused
+        if (in_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 1, kNormRowsKv>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 1, kNormRowsKv>), grid, block, 0, s, a);
+    } else if (in_dtype == 0 && q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 0, kNormRows>), grid, block, 0, s, a);
+    else if (in_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 0, 1, kNormRows>), grid, block, 0, s, a);
+    else if (q_dtype == 0) hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 0, kNormRows>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_qk_norm_rope<D, 1, 1, kNormRows>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
