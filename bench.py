@@ -90,7 +90,10 @@ class Workload:
         self.qn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.kn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.split = n * (NH // NKV) <= 32 and n <= 8
-        self.one_launch = n * (NH // NKV) <= 8  # decode: the combine runs inside the attend launch
+        # decode (up to 8 query rows per KV head): the combine runs inside the attend launch (its combining
+        # workgroups, one per output row, on at most half the CUs)
+        self.one_launch = (self.split and n * (NH // NKV) <= 8
+                           and 2 * n * NH <= torch.cuda.get_device_properties(0).multi_processor_count)
         # prefill: the kernel normalizes the query rows itself (the layer entry point's path for this
         # rope width), so no query buffer
         self.q = None

@@ -86,6 +86,18 @@ __device__ __forceinline__ unsigned long long rec_tag(unsigned long long epoch, 
     return (epoch << 5) | (unsigned)kvh;  // NKV <= 32 (host-checked)
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// The launch's tag from the head's counter as a streaming workgroup read it at its start, computed where
+// the records are stored. The empty asm marks the value as lane-varying, so the compiler keeps it in the
+// vector registers it was loaded into; treated as uniform, it is moved to scalar registers right at the
+// load, which waits for that load before anything else of the workgroup is issued.
+__device__ __forceinline__ unsigned long long tag_of(u32x2 raw, int kvh) {
+    asm volatile("" : "+v"(raw));
+    const unsigned long long cnt = __builtin_bit_cast(unsigned long long, raw);
+    return rec_tag(cnt / kEpochStep + 1u, kvh);
+}
+
 // A bounded wait gave up: the launch's output is not valid. The code goes to the host-visible error word
 // (the first code stored wins: a later one does not overwrite it).
 __device__ __forceinline__ void report_wait(const DecodeArgs& a, int code) {
@@ -96,6 +108,54 @@ __device__ __forceinline__ void report_wait(const DecodeArgs& a, int code) {
     }
 }
 
+
+// Rows of the fused prologues (query rows, new key rows), one row per 32-lane half-wave and D/32
+// consecutive dims per lane from d0 = (lane & 31) * D/32: y = x * rsqrt(mean(x^2) + eps) * (1 + w), then
+// rotate-half RoPE on d < R with the (cos, sin) pairs cv (as k_qk_norm_rope: the partner dim d +- R/2
+// sits (R/2)/(D/32) lanes away in the same half; `rot`: this lane's dims are rotated). NP rows at once,
+// every step of every row issued before the next step, so the rows' latencies overlap; the mean of
+// squares is a DPP/permlane sum (sum32), the partners one LDS-free-address shuffle each. Rows not `valid`
+// come out as zero.
+template <int D, int NP>
+__device__ __forceinline__ void norm_rope_rows(const DecodeArgs& a, int lane, bool rot, const float (&xr)[NP][D / 32],
+                                               const float (&cv)[NP][D / 16], const bool (&valid)[NP],
+                                               const float (&w)[D / 32], float (&y)[NP][D / 32]) {
+    constexpr int DPL2 = D / 32;
+    const int d0 = (lane & 31) * DPL2, half_r = a.R >> 1;
+    float ss[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        ss[p] = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            y[p][jj] = valid[p] ? xr[p][jj] : 0.f;
+            ss[p] += y[p][jj] * y[p][jj];
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; p++) ss[p] = sum32(ss[p]);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const float r = 1.0f / sqrtf(ss[p] / (float)D + a.eps);
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) y[p][jj] = y[p][jj] * r * (1.0f + w[jj]);
+    }
+    const int offl = half_r / DPL2;
+    const bool lo_half = d0 < half_r;
+    const int src_lane = rot ? (lo_half ? lane + offl : lane - offl) : lane;
+    float partner[NP][DPL2];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) partner[p][jj] = __shfl(y[p][jj], src_lane, 64);  // all issued, then used
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int jj = 0; jj < DPL2; jj++) {
+            const float cs = rot ? cv[p][2 * jj] : 1.f, sn = rot ? cv[p][2 * jj + 1] : 0.f;
+            y[p][jj] = lo_half ? y[p][jj] * cs - partner[p][jj] * sn : y[p][jj] * cs + partner[p][jj] * sn;
+        }
+}
 
 // Merges a batch of split partials (m, l, o) into the running (M, L, O) (attn_combine.comp:17-26: the
 // max over the splits with keys, then each partial weighted by exp2(m - max)), in a fixed order and
@@ -230,9 +290,11 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
     }
     if (tid < D) a.out[((size_t)t * a.NH + h) * D + tid] = O / L * sigmoid(gate);
     if (__ballot(gave_up) != 0 && lane == 0) report_wait(a, kWaitCombineFlags);
-    if (tid == 0)  // this combiner is done: its share of the head's epoch step (see kEpochStep)
-        __hip_atomic_fetch_add(a.ep + kvh, (unsigned long long)(kEpochStep / (a.ncomb / a.NKV)), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {  // this combiner is done: its share of the head's epoch step (see kEpochStep)
+        const unsigned m = (unsigned)(a.ncomb / a.NKV), j = (unsigned)(t * G + h % G);  // j-th of the head's m
+        __hip_atomic_fetch_add(a.ep + kvh, (unsigned long long)((j + 1) * kEpochStep / m - j * kEpochStep / m),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int D, int FUSED, int IN_DT>
@@ -297,7 +359,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     const int half_r = a.R >> 1;
     float wq[DPL2], wk[DPL2];
     float qx[QPASS][DPL2], qcv[QPASS][2 * DPL2];
-    float nx[DPL2], ncv[2 * DPL2], nv[DPL2];
+    float nx[1][DPL2], ncv[1][2 * DPL2], nv[DPL2];
     bool qvalid[QPASS];
     const bool rot = FUSED && d0 < a.R;  // lanes whose DPL2 dims are rotated (R/2 is a multiple of DPL2)
     // one row's DPL2 values and (cos, sin) pairs: raw loads only (an invalid row reads row 0, lanes
@@ -308,34 +370,6 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         if constexpr (FUSED) {
             const int i0 = rot ? (d0 < half_r ? d0 : d0 - half_r) : 0;
             load_vec<0, 2 * DPL2>(a.rope, (size_t)(valid && rot ? p : 0) * a.R + 2 * i0, cv);
-        }
-    };
-    // y = x * rsqrt(mean(x^2) + eps) * (1 + w), then rotate-half on d < R (as k_qk_norm_rope: the row
-    // spread over 32 lanes, the partner dim d +- R/2 (R/2)/DPL2 lanes away in the same half)
-    auto finish_row = [&](const float (&xr)[DPL2], const float (&cv)[2 * DPL2], bool valid, const float (&w)[DPL2],
-                          float (&y)[DPL2]) {
-        float x[DPL2];
-        float ss = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) {
-            x[jj] = valid ? xr[jj] : 0.f;
-            ss += x[jj] * x[jj];
-        }
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) y[jj] = x[jj] * r * (1.0f + w[jj]);
-        const int offl = half_r / DPL2;
-        const bool lo_half = d0 < half_r;
-        const int src_lane = rot ? (lo_half ? lane + offl : lane - offl) : lane;
-        float partner[DPL2];
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) partner[jj] = __shfl(y[jj], src_lane, 64);  // all issued, then used
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) {
-            const float cs = rot ? cv[2 * jj] : 1.f, sn = rot ? cv[2 * jj + 1] : 0.f;
-            y[jj] = lo_half ? y[jj] * cs - partner[jj] * sn : y[jj] * cs + partner[jj] * sn;
         }
     };
 #pragma unroll
@@ -353,7 +387,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         load_vec<0, DPL2>(a.qn, d0, wq);
         load_vec<0, DPL2>(a.kn, d0, wk);
         const size_t src = ((size_t)(has_new ? tn : 0) * a.NKV + kvh) * D;
-        issue_row(nx, ncv, a.knew, src, a.pos + (has_new ? tn : 0), has_new);
+        issue_row(nx[0], ncv[0], a.knew, src, a.pos + (has_new ? tn : 0), has_new);
         load_vec<IN_DT, DPL2>(a.vnew, src + d0, nv);
     }
 
@@ -373,13 +407,17 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
 #pragma unroll
     for (int ps = 0; ps < QPASS; ps++) {
         const int r = ps * 8 + wave * 2 + hw;
-        float y[DPL2];
+        // one row at a time here: the first tile is already held in registers
+        float y1[1][DPL2];
         if constexpr (FUSED) {
-            finish_row(qx[ps], qcv[ps], qvalid[ps], wq, y);
+            const bool v1[1] = {qvalid[ps]};
+            norm_rope_rows<D, 1>(a, lane, rot, reinterpret_cast<const float (&)[1][DPL2]>(qx[ps]),
+                                 reinterpret_cast<const float (&)[1][2 * DPL2]>(qcv[ps]), v1, wq, y1);
         } else {
 #pragma unroll
-            for (int jj = 0; jj < DPL2; jj++) y[jj] = qvalid[ps] ? qx[ps][jj] : 0.f;
+            for (int jj = 0; jj < DPL2; jj++) y1[0][jj] = qvalid[ps] ? qx[ps][jj] : 0.f;
         }
+        const float (&y)[DPL2] = y1[0];
         // the lane's DPL2 dims are consecutive inside one 8-dim group, so its hi and lo parts are one
         // vector store each into the fragment layout
         typedef f16 f16v __attribute__((ext_vector_type(DPL2)));
@@ -397,8 +435,10 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         *reinterpret_cast<f16v*>(&s_q[((NKS + kk) * 64 + L) * 8 + e]) = lv;
     }
     if constexpr (FUSED) {
-        float y[DPL2];
-        finish_row(nx, ncv, has_new, wk, y);  // computed by every half-wave, stored by the owners
+        float yn[1][DPL2];
+        const bool hn[1] = {has_new};
+        norm_rope_rows<D, 1>(a, lane, rot, nx, ncv, hn, wk, yn);  // computed by every half-wave, stored by the owners
+        const float (&y)[DPL2] = yn[0];
         if (has_new) {
             const int p = a.pos + tn;
             const size_t part = kv_part(p, kvh, a.cap, D);
@@ -657,14 +697,14 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     const int G = a.NH / a.NKV;
     const int rows = min(RMAX, a.n * G);
     const int maxlen = a.pos + a.n;
-    // one-launch: this launch's epoch tag (see kEpochStep), read now (device-coherent, unconditionally: a
-    // zero-sized range without the combine reads 0 and touches no memory) so that its latency hides behind
-    // the prologue; it must be read before this workgroup stores its records
-    unsigned long long tag = 0;
+    // one-launch: the head's launch counter for this launch's epoch tag (see kEpochStep), read now
+    // (device-coherent, unconditionally: a zero-sized range without the combine reads 0 and touches no
+    // memory) so that its latency hides behind the prologue; it must be read before this workgroup stores
+    // its records
+    u32x2 ep_raw = {0u, 0u};
     if constexpr (FUSED) {
         const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(one ? a.ep + kvh : a.ep, (short)0, one ? 8 : 0, 0x00020000);
-        const unsigned long long cnt = __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(rep, 0, 0, kScDevice));
-        tag = rec_tag(cnt / kEpochStep + 1u, kvh);
+        ep_raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rep, 0, 0, kScDevice));
     }
     // ---- this split's tiles: blocks z, z + S, z + 2S, ... of the nb blocks of the head that hold keys
     // (strided: at every step the splits of a head read neighbouring blocks, so the cache is swept front to
@@ -723,34 +763,6 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             load_vec<0, 2 * DPL2>(a.rope, (size_t)(valid && rot ? p : 0) * a.R + 2 * i0, cv);
         }
     };
-    // y = x * rsqrt(mean(x^2) + eps) * (1 + w), then rotate-half on d < R (the partner dim d +- R/2 sits
-    // (R/2)/DPL2 lanes away in the same half-wave)
-    auto finish_row = [&](const float (&xr)[DPL2], const float (&cv)[2 * DPL2], bool valid, const float (&w)[DPL2],
-                          float (&y)[DPL2]) {
-        float x[DPL2];
-        float ss = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) {
-            x[jj] = valid ? xr[jj] : 0.f;
-            ss += x[jj] * x[jj];
-        }
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) y[jj] = x[jj] * r * (1.0f + w[jj]);
-        const int offl = half_r / DPL2;
-        const bool lo_half = d0 < half_r;
-        const int src_lane = rot ? (lo_half ? lane + offl : lane - offl) : lane;
-        float partner[DPL2];
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) partner[jj] = __shfl(y[jj], src_lane, 64);
-#pragma unroll
-        for (int jj = 0; jj < DPL2; jj++) {
-            const float cs = rot ? cv[2 * jj] : 1.f, sn = rot ? cv[2 * jj + 1] : 0.f;
-            y[jj] = lo_half ? y[jj] * cs - partner[jj] * sn : y[jj] * cs + partner[jj] * sn;
-        }
-    };
     if (!loader) {
         float wq[DPL2], wk[DPL2];
         float qx[QPASS][DPL2], qcv[QPASS][2 * DPL2];
@@ -783,12 +795,18 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
+        float yq[QPASS][DPL2];
+        bool qv[QPASS];
+#pragma unroll
+        for (int ps = 0; ps < QPASS; ps++) qv[ps] = ps * 2 * NCW + wave * 2 + hw < rows;
+        if constexpr (FUSED) norm_rope_rows<D, QPASS>(a, lane, rot, qx, qcv, qv, wq, yq);
 #pragma unroll
         for (int ps = 0; ps < QPASS; ps++) {
             const int r = ps * 2 * NCW + wave * 2 + hw;
             float y[DPL2];
             if constexpr (FUSED) {
-                finish_row(qx[ps], qcv[ps], r < rows, wq, y);
+#pragma unroll
+                for (int jj = 0; jj < DPL2; jj++) y[jj] = yq[ps][jj];
             } else {
 #pragma unroll
                 for (int jj = 0; jj < DPL2; jj++) y[jj] = r < rows ? qx[ps][jj] : 0.f;
@@ -808,11 +826,15 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             *reinterpret_cast<f16v*>(&s_q[(kk * 64 + L + 8) * 8 + e]) = lv;
         }
         if constexpr (FUSED) {
+            float yn[NPASS][DPL2];
+            bool nvl[NPASS];
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ps++) nvl[ps] = t_lo + ps * 2 * NCW + wave * 2 + hw < t_hi;
+            norm_rope_rows<D, NPASS>(a, lane, rot, nx, ncv, nvl, wk, yn);
 #pragma unroll
             for (int ps = 0; ps < NPASS; ps++) {
                 const int tn = t_lo + ps * 2 * NCW + wave * 2 + hw;
-                float y[DPL2];
-                finish_row(nx[ps], ncv[ps], tn < t_hi, wk, y);
+                const float (&y)[DPL2] = yn[ps];
                 if (tn < t_hi) {
                     const int p = a.pos + tn;
                     const size_t part = kv_part(p, kvh, a.cap, D);
@@ -1039,6 +1061,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
         if (wave == 0 && g == 0 && c < rows) {
+            const unsigned long long tag = tag_of(ep_raw, kvh);
             const int t = c / G, h = kvh * G + c % G;
             const int row = (t * a.NH + h) * S + z;
             const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(a.rec, (short)0, 0x7fffffff, 0x00020000);
@@ -1055,32 +1078,36 @@ constexpr size_t decode_ld_lds() {
     return stream > comb ? stream : comb;
 }
 
+// Launches a kernel with `shm` bytes of dynamic LDS; the limit is a per-device attribute of the
+// function, raised once per device (`raised`: one bit per device).
+template <typename K>
+static hipError_t launch_lds(K kern, std::atomic<uint64_t>& raised, dim3 grid, size_t shm, const DecodeArgs& a, hipStream_t s) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(raised.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+        if (e != hipSuccess) return e;
+        raised.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(256), shm, s, a);
+    return hipGetLastError();
+}
+
 template <int D, int FUSED, int IN_DT>
 static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
-    const dim3 block(256);
     // the in-launch combine: fused (it needs the gate), at most 8 rows (the 16-row kernel has no
     // registers left for it), one combining workgroup per output row
     if (a.out != nullptr && (!FUSED || rows > 8 || a.ncomb != a.n * a.NH || !a.ep || !a.rec))
         return hipErrorInvalidValue;
     if (rows <= 8) {
-        auto kern = k_decode_ld<D, FUSED, IN_DT>;
-        const size_t shm = decode_ld_lds<D>();
-        // the dynamic-LDS limit is a per-device attribute of the function: raise it once per device
         static std::atomic<uint64_t> raised{0};
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
-        if (e != hipSuccess) return e;
-        const uint64_t bit = 1ull << (dev & 63);
-        if (!(raised.load(std::memory_order_acquire) & bit)) {
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-            if (e != hipSuccess) return e;
-            raised.fetch_or(bit, std::memory_order_acq_rel);
-        }
         const int ncomb = a.out != nullptr ? a.ncomb : 0;
-        hipLaunchKernelGGL(kern, dim3(ncomb + a.n_split * a.NKV), block, shm, s, a);
+        return launch_lds(k_decode_ld<D, FUSED, IN_DT>, raised, dim3(ncomb + a.n_split * a.NKV), decode_ld_lds<D>(), a, s);
     }
-    else hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), block, 0, s, a);
+    hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -61,11 +61,12 @@ constexpr int kWaitRingCompute = 4;   // a compute wave: its loader wave never p
 constexpr int kSpinDefault = 1 << 22; // default DecodeArgs::spin_max (seconds of polling)
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 
-// One-launch decode: each combining workgroup adds kEpochStep / (combiners per KV head) to its head's
-// counter when done, so a launch whose combiners have all finished advances the counter by exactly
-// kEpochStep whatever their number (1..8), and floor(counter / kEpochStep) + 1 is the epoch of the next
-// launch — also for a participant that reads the counter after some combiners of its own launch are done.
-constexpr unsigned kEpochStep = 840;  // lcm(1, ..., 8)
+// One-launch decode: combining workgroup j of a KV head's m adds (j+1)K/m - jK/m (integer division,
+// K = kEpochStep) to its head's counter when done. The shares add up to exactly K, so a launch whose
+// combiners have all finished advances the counter by K whatever their number (1..32), any part of them by
+// less, and floor(counter / K) + 1 is the epoch of the next launch — also for a participant that reads the
+// counter after some combiners of its own launch are done.
+constexpr unsigned kEpochStep = 840;
 constexpr int kCombSlots = 128;       // split partials a combining workgroup stages in LDS at once
 constexpr int kCombGroup = 32;        // splits merged together (in a fixed order) once all are staged
 

@@ -139,10 +139,19 @@ struct Split {
     int S, cq, cr;
 };
 
+// One launch (attend + combine) for n tokens: up to 8 query rows per KV head (the loader-wave kernel),
+// and the combining workgroups (one per output row, waiting for the streaming ones) on at most half the
+// CUs, so the others always have room to run.
+bool one_launch(int n_cu, const qwattn_config& g, int n) {
+    return n * (g.n_heads / g.n_kv_heads) <= 8 && 2 * n * g.n_heads <= n_cu;
+}
+
+// reserve: CUs left to the combining workgroups of a one-launch call; more than 8 rows go to the decode
+// kernel's 16-row slices (grid.z)
 Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, int reserve = 0) {
     const int nb = (maxlen + 31) / 32;
     const int rows = n * (g.n_heads / g.n_kv_heads);
-    const int slices = rows <= 8 ? 1 : (rows + 15) / 16;  // the decode kernel's 16-row slices (grid.z)
+    const int slices = rows <= 8 ? 1 : (rows + 15) / 16;
     int S = n_split > 0 ? n_split : std::max(1, (n_cu - reserve) / (g.n_kv_heads * slices));
     S = std::max(1, std::min({S, g.max_splits, nb}));
     return Split{S, nb / S, nb % S};
@@ -461,12 +470,10 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     if (n * G > 32 || n > 8)
         return fail(c, QWATTN_EINVAL, "qwattn_decode: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
                     "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
-    // up to 8 query rows per KV head the combine runs inside the attend launch, in one combining
-    // workgroup per output row (first in the grid); the 16-row-slice kernel (verify) is followed by the
-    // combine kernel. Combining workgroups wait for the streaming ones: at most half the CUs may hold one,
-    // so the others always have room to run
+    // the combine runs inside the attend launch, in one combining workgroup per output row (first in the
+    // grid), unless those would take more than half the CUs: then the combine kernel follows
     const int ncomb = n * g.n_heads;
-    const bool one = n * G <= 8 && 2 * ncomb <= c->n_cu;
+    const bool one = one_launch(c->n_cu, g, n);
     const Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0);
     const int used = sp.S;
     DeviceGuard dg(c->device);
@@ -668,7 +675,7 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
     int n_cu = 0;
     if (int rc = scratch_base(device, &base, &n_cu)) return rc;
     const int ncomb = n * g.n_heads;
-    const bool one = n * G <= 8 && 2 * ncomb <= n_cu;
+    const bool one = one_launch(n_cu, g, n);
     const Split sp = pick_split(n_cu, g, pos + n, n, n_split, one ? ncomb : 0);
     const size_t parts = (size_t)ncomb * sp.S;  // split partial rows
     const size_t rec_b = align256(parts * 16), ml_b = align256(parts * 8), o_b = align256(parts * g.head_dim * 4);

@@ -307,6 +307,13 @@ ONE_LAUNCH = CASES_FUSED + [
     (TINY_GGUF, 61, 4, 0, "f32"),       # automatic splits of one block each: the new rows straddle two chunks
     (TINY, 63, 2, 0, "bf16"),           # the same with one new row in each chunk
     (QWEN3_NEXT, 16383, 1, 64, "f32"),  # 64 splits of 8 blocks, the new row opening the last block
+    # 9 to 32 rows (qwattn_decode's 16-row-slice kernel and combine kernel): partly filled slices, 8 new
+    # rows, one split holding every tile, splits of a single tile that holds new rows
+    (TINY, 500, 3, 0, "f32"),           # 12 rows: the second group half full, two idle waves
+    (TINY_GGUF, 100, 5, 0, "bf16"),     # 10 rows at D = 256, G = 2
+    (D128, 2000, 8, 0, "bf16"),         # 32 rows, 8 new rows across a block boundary
+    (QWEN3_NEXT, 5000, 4, 1, "f32"),    # one split: 157 tiles through one ring
+    (QWEN3_NEXT, 40, 2, 0, "bf16"),     # 16 rows, two splits of one tile each
 ]
 
 
@@ -332,9 +339,10 @@ def test_decode_one_launch_parity(qw, oracle, s, pos, n, n_split, dtype):
 
 def test_decode_one_launch_equals_two_launches(qw):
     """The in-launch combine merges what qwattn_combine merges: over a run of calls on one context with
-    changing token counts (decode n=1 on the loader-wave kernel, verify n=4 on two 16-row slices) and
-    split counts (fewer splits than combine units, one split, many), each output matches
-    decode_partial + combine to fp32 rounding (the two merges visit the splits in different orders).
+    changing token counts (decode n=1 on the loader-wave kernel, verify n=4 on two 16-row slices and the
+    combine kernel) and split counts (fewer splits than combine units, one split, many; the two-launch call
+    is given the first call's count), each output matches decode_partial + combine to fp32 rounding (the
+    two merges visit the splits in different orders).
     The one-launch calls use the context's ready flags with changing split counts: a flag left by one
     call that passed for a later call's epoch would let its combiners merge stale partials."""
     s, pos = QWEN3_NEXT, 3000
@@ -345,7 +353,7 @@ def test_decode_one_launch_equals_two_launches(qw):
         out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
         used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
         out2 = torch.zeros((n, s.NH, s.D), device=DEV)
-        used2 = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, n_split)
+        used2 = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, n_split or used)
         ctx.combine(qg_d, out2, n, used2)
         torch.cuda.synchronize()
         assert used == used2
