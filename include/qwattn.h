@@ -140,11 +140,14 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* ctx, void* stream, const void* qg, co
 
 /* Split-KV causal GQA attention partials (reference: shaders/attention.comp, pipeline
  * attention_kv16, dispatched at src/qwen4_vk.cpp:985-988 with PcAttn). Token t attends to keys
- * [0, pos+t+1); the keys [0, pos+n) are cut into `n_split` chunks of whole 32-key blocks (0 =
- * automatic: one workgroup per CU). A requested count is used as given, capped at max_splits and at
- * ceil((pos+n)/32), so that every chunk holds at least one block; of the nb = ceil((pos+n)/32) blocks the
- * first nb % n_split chunks hold one block more than the others. The reference cuts ceil(len/n_split)
- * keys per chunk (src/qwen4_vk.cpp:974-978); both splits give the same output up to fp32 rounding.
+ * [0, pos+t+1); the nb = ceil((pos+n)/32) 32-key blocks of keys [0, pos+n) are cut into `n_split`
+ * parts (0 = automatic: one workgroup per CU). A requested count is used as given, capped at max_splits
+ * and at nb, so that every part holds at least one block. With up to 8 query rows per KV head
+ * (n * NH/NKV <= 8: decode) part z holds the blocks z, z + n_split, z + 2 n_split, ... (the parts of a KV
+ * head read neighbouring blocks at every step); with more rows (verify) part z is a contiguous chunk, the
+ * first nb % n_split chunks one block longer than the others. The reference cuts ceil(len/n_split)
+ * contiguous keys per chunk (src/qwen4_vk.cpp:974-978); every partition gives the same output up to fp32
+ * rounding.
  * Each workgroup serves all NH/NKV query heads of all n tokens of one KV head for one chunk,
  * so every K/V row is read from HBM once. `q` is the normalized, rotated query [n][NH][D] fp32 (the
  * reference's q_out) and rows [pos, pos+n) must already be in the caches. Requires n * NH/NKV <= 32
@@ -167,14 +170,17 @@ int qwattn_decode_partial(qwattn_ctx* ctx, void* stream, const void* qg, const v
 
 /* All three of the reference's decode dispatches (src/qwen4_vk.cpp:968-992: qk_norm_rope,
  * attention, attn_combine): qwattn_decode_partial followed, inside the same kernel, by the log-sum-exp
- * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. The workgroups of the last
- * splits of each KV head merge the split partials once every split's ready flag (in the context, tagged
- * with a per-launch epoch) is set; nothing needs clearing between launches, so the call allocates and
+ * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. Combining workgroups, one per
+ * output row and first in the grid, merge the split partials as their records (in the context, tagged
+ * with a per-launch epoch) arrive; nothing needs clearing between launches, so the call allocates and
  * clears nothing and can be captured into a graph. Calls on one context must not overlap (one stream,
  * or ordered streams). The merge order is fixed, so the output does not depend on which workgroup
  * finishes first. Same limits as qwattn_decode_partial
  * (n <= 8, n * NH/NKV <= 32: decode and MTP verify); one launch for n * NH/NKV <= 8, above that (verify)
- * the attend launch is followed by the combine launch. */
+ * the attend launch is followed by the combine launch. `n_split` as in qwattn_attend_partial, except that
+ * the one-launch form caps a requested count at the automatic one (one streaming workgroup per CU): its
+ * partials never leave the launch, and more parts would only add workgroup prologues and partials to
+ * merge. *used_splits (may be NULL) returns the count used. */
 int qwattn_decode(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
                   int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
                   void* vcache, int kv_cap, float* out, int pos, int n, int n_split, int* used_splits);

@@ -129,12 +129,17 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
     return take_wait_error(c);
 }
 
-// Split of the key axis [0, maxlen) for the decode kernels into S chunks of whole 32-key blocks: of the
-// nb = ceil(maxlen / 32) blocks that hold keys, chunk z takes [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr))
-// with cq = nb / S, cr = nb % S (the first cr chunks one block longer). A requested count n_split > 0 is
-// used as given (the reference's 64, src/qwen4_vk.cpp:974-978, or BASELINE's 1,024), capped at max_splits
-// and at nb: a chunk holds at least one block. n_split = 0 picks one workgroup per CU: (CUs - `reserve`,
-// the one-launch decode's combining workgroups) / (NKV x the decode kernel's 16-row slices) chunks.
+// Split of the key axis [0, maxlen) for the decode kernels into S parts of whole 32-key blocks, of the
+// nb = ceil(maxlen / 32) blocks that hold keys. Up to 8 query rows per KV head (k_decode_ld) part z takes
+// the blocks z, z + S, z + 2S, ...; more rows (k_decode) take contiguous chunks, chunk z the blocks
+// [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr)) with cq = nb / S, cr = nb % S (the first cr chunks one block
+// longer). A requested count n_split > 0 is used as given (the reference's 64, src/qwen4_vk.cpp:974-978,
+// or 1,024 at 256K), capped at max_splits and at nb: a part holds at least one block. n_split = 0 picks
+// one workgroup per CU: (CUs - `reserve`, the one-launch decode's combining workgroups) / (NKV x the
+// decode kernel's 16-row slices) parts. `fill_cap` (the one-launch decode, whose partials never leave the
+// launch) also caps a requested count at that number: more parts than streaming workgroups that fit
+// the CUs at once only add workgroup prologues and partials to merge, and the output is the same up to
+// fp32 rounding.
 struct Split {
     int S, cq, cr;
 };
@@ -148,17 +153,19 @@ bool one_launch(int n_cu, const qwattn_config& g, int n) {
 
 // reserve: CUs left to the combining workgroups of a one-launch call; more than 8 rows go to the decode
 // kernel's 16-row slices (grid.z)
-Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, int reserve = 0) {
+Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, int reserve = 0,
+                 bool fill_cap = false) {
     const int nb = (maxlen + 31) / 32;
     const int rows = n * (g.n_heads / g.n_kv_heads);
     const int slices = rows <= 8 ? 1 : (rows + 15) / 16;
-    int S = n_split > 0 ? n_split : std::max(1, (n_cu - reserve) / (g.n_kv_heads * slices));
+    const int fill = std::max(1, (n_cu - reserve) / (g.n_kv_heads * slices));
+    int S = n_split > 0 ? (fill_cap ? std::min(n_split, fill) : n_split) : fill;
     S = std::max(1, std::min({S, g.max_splits, nb}));
     return Split{S, nb / S, nb % S};
 }
 
-Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int reserve = 0) {
-    return pick_split(c->n_cu, c->cfg, maxlen, n, n_split, reserve);
+Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int reserve = 0, bool fill_cap = false) {
+    return pick_split(c->n_cu, c->cfg, maxlen, n, n_split, reserve, fill_cap);
 }
 
 // Arguments of the decode kernels: shape and split (partials and wait settings: decode_args below).
@@ -474,7 +481,7 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     // grid), unless those would take more than half the CUs: then the combine kernel follows
     const int ncomb = n * g.n_heads;
     const bool one = one_launch(c->n_cu, g, n);
-    const Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0);
+    const Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0, one);
     const int used = sp.S;
     DeviceGuard dg(c->device);
     qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
@@ -676,7 +683,7 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
     if (int rc = scratch_base(device, &base, &n_cu)) return rc;
     const int ncomb = n * g.n_heads;
     const bool one = one_launch(n_cu, g, n);
-    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, one ? ncomb : 0);
+    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, one ? ncomb : 0, one);
     const size_t parts = (size_t)ncomb * sp.S;  // split partial rows
     const size_t rec_b = align256(parts * 16), ml_b = align256(parts * 8), o_b = align256(parts * g.head_dim * 4);
     if (kScratchData + rec_b + ml_b + o_b > kScratchBytes)

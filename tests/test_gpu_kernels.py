@@ -353,7 +353,7 @@ def test_decode_one_launch_equals_two_launches(qw):
         out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
         used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
         out2 = torch.zeros((n, s.NH, s.D), device=DEV)
-        used2 = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, n_split or used)
+        used2 = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, used)
         ctx.combine(qg_d, out2, n, used2)
         torch.cuda.synchronize()
         assert used == used2
@@ -390,10 +390,12 @@ def test_decode_one_launch_graph_replays(qw):
 
 
 def test_decode_256k_peaked_keys(qw, oracle):
-    """262,144 cached tokens + 1 through the one-launch decode (norm, rope, append,
-    split attend, in-launch combine), with 1% of the cached key rows scaled x8 (softmax-range stress), at
-    the configuration's 1,024 splits (run as requested: 8,193 blocks of keys, 1 chunk of 9 and 1,023 of 8)
-    and at the automatic split count, against the oracle on the same fp16 rows."""
+    """262,144 cached tokens + 1, with 1% of the cached key rows scaled x8
+    (softmax-range stress), against the oracle on the same fp16 rows: through the one-launch decode (norm,
+    rope, append, split attend, in-launch combine) at the automatic split count and with the
+    configuration's 1,024 splits requested (capped at the automatic count: one streaming workgroup per
+    CU, the same launch bit for bit), and with exactly 1,024 split partials (8,193 blocks of keys: part z
+    the blocks z, z + 1,024, ...) through the fused partial entry point and the combine kernel."""
     s = QWEN3_NEXT
     pos, n = 262144, 1
     rows = pos + n
@@ -412,22 +414,30 @@ def test_decode_256k_peaked_keys(qw, oracle):
     qg, k, v, qn, kn = projections(2562, n, s)
     qg_d, k_d, v_d, qn_d, kn_d = dev(qg), dev(k), dev(v), dev(qn), dev(kn)
     ctx = make_ctx(qw, s, max_ctx=cap)
-    outs = {}
-    for n_split in (1024, 0):
-        print(f"decode 256K: splits={n_split or 'auto'}", flush=True)
+    outs, used_by_req = {}, {}
+    for n_split in (0, 1024):
+        print(f"decode 256K: one launch, splits requested {n_split or 'auto'}", flush=True)
         out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
-        used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
+        used_by_req[n_split] = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n,
+                                          n_split)
         ctx.sync_status()
-        if n_split:
-            assert used == n_split
-        outs[used] = host(out)
+        outs[f"one launch, {n_split or 'auto'} requested"] = host(out)
+    assert used_by_req[1024] == used_by_req[0] < 1024, used_by_req
+    assert np.array_equal(outs["one launch, 1024 requested"], outs["one launch, auto requested"])
+    print("decode 256K: 1,024 split partials + combine", flush=True)
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    used = ctx.decode_partial(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, pos, n, 1024)
+    assert used == 1024
+    ctx.combine(qg_d, out, n, used)
+    ctx.sync_status()
+    outs["1024 partials"] = host(out)
     rq, rk, _ = oracle.qk_norm_rope(qg, k, v, 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
     kr = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
     assert np.all(np.abs(kr[pos] - rk[pos]) <= np.abs(rk[pos]) * 2.0 ** -10 + 1e-6)
     ref = oracle.attention(rq, kr, host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows]), pos, qg)
-    for used, o in outs.items():
-        print(f"decode 256K splits={used}: max_abs {np.abs(o - ref).max():.2e}", flush=True)
-        assert_parity(o, ref, f"256K splits={used}")
+    for name, o in outs.items():
+        print(f"decode 256K {name}: max_abs {np.abs(o - ref).max():.2e}", flush=True)
+        assert_parity(o, ref, f"256K {name}")
 
 
 def test_decode_wait_timeout_is_reported(qw):

@@ -50,11 +50,23 @@ def test_decode_noalloc_matches_decode(qw, calls):
 
 
 def test_decode_noalloc_rejects_beyond_scratch(qw):
-    """A split count whose partials exceed the 32 MiB scratch is rejected before any launch."""
+    """A split count whose partials exceed the 32 MiB scratch is rejected before any launch: the 4-token
+    verify path, which runs a requested count exactly (4,096 splits x 64 rows). Every buffer is sized for
+    the call, so nothing could be touched out of bounds even if a launch did happen."""
     s = QWEN3_NEXT
     cfg = qw.Config(s.NH, s.NKV, s.D, s.R, s.theta, s.eps, 262144, 64, 4096)
-    pos, n, cap = 262100, 1, 262144
-    t = torch.zeros(16, device=DEV)
+    pos, n, cap = 262100, 4, 262144
+    qg = torch.zeros((n, s.NH, 2 * s.D), device=DEV)
+    k = torch.zeros((n, s.NKV, s.D), device=DEV)
+    v = torch.zeros((n, s.NKV, s.D), device=DEV)
+    w = torch.zeros(s.D, device=DEV)
+    rope = torch.zeros((cap, s.R // 2, 2), device=DEV)
+    kc = torch.zeros(cap * s.NKV * s.D, dtype=torch.float16, device=DEV)
+    vc = torch.zeros(cap * s.NKV * s.D, dtype=torch.float16, device=DEV)
+    out = torch.zeros((n, s.NH, s.D), device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
     with pytest.raises(qw.QwattnError, match="scratch") as e:
-        qw.decode_noalloc(cfg, t, t, t, t, t, t, t, t, cap, t, pos, n, 4096)
+        qw.decode_noalloc(cfg, qg, k, v, w, w, rope, kc, vc, cap, out, pos, n, 4096, status)
     assert e.value.code == qw.EINVAL
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
