@@ -76,9 +76,14 @@ class Oracle:
         lib.orc_attention_f64.argtypes = [_D, _I, _D, _D, _D, _D, _I, _I, _I, _I, _I]
         lib.orc_qk_norm_rope_f64.argtypes = [_D, _D, _D, _I, _I, _I, ctypes.POINTER(_I), ctypes.c_double,
                                              ctypes.c_double, _I]
+        _U = ctypes.POINTER(ctypes.c_uint32)
+        lib.orc_qsa_pool.argtypes = [_F, _F, _F, _I, _I, _I, _I, _I, ctypes.c_double, ctypes.c_float]
+        lib.orc_qsa_select.argtypes = [_F, _F, _F, _U, _I, _F, _I, _I, _I, _I, _I, _I, _I, _I, ctypes.c_double,
+                                       ctypes.c_float]
+        lib.orc_attention_qsa.argtypes = [_F, _I, _F, _F, _F, _F, _I, _I, _I, _I, _I, _U, _I, _I]
         for f in ("orc_inv_freq", "orc_rope_table", "orc_rms_mul", "orc_rmsnorm_one_plus", "orc_rope",
                   "orc_qk_norm_rope", "orc_attention", "orc_attention_split", "orc_attention_f64",
-                  "orc_qk_norm_rope_f64"):
+                  "orc_qk_norm_rope_f64", "orc_qsa_pool", "orc_qsa_select", "orc_attention_qsa"):
             getattr(lib, f).restype = None
         self.lib = lib
 
@@ -173,6 +178,98 @@ class Oracle:
         self.lib.orc_qk_norm_rope_f64(_dp(x), _dp(np.ascontiguousarray(gamma, np.float64)), _dp(out), rows, D, R,
                                       rp.ctypes.data_as(ctypes.POINTER(_I)), theta, eps, int(fp32_angle))
         return out
+
+
+    # ---- QSA indexer (src/qwen4_qsa.h) and block-sparse attention ----------------------------------
+
+    def qsa_pool(self, raw, gamma, b0, b1, cr, R, theta, eps, pooled=None):
+        """raw [rows, ID] raw indexer keys -> pooled [>= b1, ID] with blocks [b0, b1) (re)computed."""
+        raw = _f32(raw)
+        ID = raw.shape[1]
+        if pooled is None:
+            pooled = np.zeros((b1, ID), np.float32)
+        assert pooled.dtype == np.float32 and pooled.flags.c_contiguous and pooled.shape[0] >= b1
+        assert raw.shape[0] >= b1 * cr
+        self.lib.orc_qsa_pool(_fp(raw), _fp(_f32(gamma)), _fp(pooled), b0, b1, ID, cr, R, theta, eps)
+        return pooled
+
+    def qsa_select(self, iq, gamma, pooled, pos, cr, top, R, theta, eps, mask_words, with_scores=False):
+        """iq [n, IH, ID] raw indexer queries -> mask [n, mask_words] uint32 (and scores [n, nblk_max],
+        NaN where a token does not select)."""
+        iq = _f32(iq)
+        n, IH, ID = iq.shape
+        pooled = _f32(pooled)
+        nmax = (pos + n) // cr
+        assert pooled.shape[0] >= nmax and mask_words * 32 >= nmax
+        mask = np.zeros((n, mask_words), np.uint32)
+        scores = np.full((n, max(nmax, 1)), np.nan, np.float32) if with_scores else None
+        self.lib.orc_qsa_select(_fp(iq), _fp(_f32(gamma)), _fp(pooled),
+                                mask.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), mask_words, _fp(scores),
+                                max(nmax, 1), pos, n, IH, ID, cr, top, R, theta, eps)
+        return (mask, scores) if with_scores else mask
+
+    def attention_qsa(self, q, kcache, vcache, pos, mask, cr, qg=None):
+        """orc_attention with the QSA block mask [n, mask_words] (tail block always visible)."""
+        q = _f32(q)
+        n, NH, QS = q.shape
+        kcache, vcache = _f32(kcache), _f32(vcache)
+        NKV, D = kcache.shape[1], kcache.shape[2]
+        mask = np.ascontiguousarray(mask, np.uint32)
+        out = np.zeros((n, NH, D), np.float32)
+        g = None if qg is None else _f32(qg)
+        self.lib.orc_attention_qsa(_fp(q), QS, _fp(g), _fp(kcache), _fp(vcache), _fp(out), pos, n, NH, NKV, D,
+                                   mask.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), mask.shape[1], cr)
+        return out
+
+
+def qsa_key_bits(mask, pos, n, cr):
+    """The per-key visibility the block-sparse kernels consume: bits [n, ceil((pos + n) / 32)] uint32, bit j
+    of token t set when key j is in a complete block whose mask bit is set or in the tail block (keys from
+    ((pos + t + 1) // cr) * cr on), as shaders/attention.comp:35-43 tests it. Keys past a token's own length
+    follow the tail rule (visible); causality masks them separately."""
+    maxlen = pos + n
+    words = (maxlen + 31) // 32
+    j = np.arange(words * 32)
+    blk = j // cr
+    mask = np.asarray(mask, np.uint32)
+    out = np.zeros((n, words), np.uint32)
+    for t in range(n):
+        tail = (pos + t + 1) // cr * cr
+        wi = np.minimum(blk >> 5, mask.shape[1] - 1)
+        bit = (mask[t][wi] >> (blk & 31).astype(np.uint32)) & 1
+        vis = (j >= tail) | ((bit == 1) & ((blk >> 5) < mask.shape[1]))
+        out[t] = (vis.reshape(words, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)).sum(axis=1)
+    return out
+
+
+class RefQsa:
+    """The reference's own QSA indexer (class QsaIndexer, src/qwen4_qsa.h) compiled in place with the sources
+    it needs (oracle/_ref/libref_qsa.so; see ref_qsa_driver.cpp)."""
+
+    def __init__(self, path=os.path.join(HERE, "_ref", f"libref_qsa{_SUFFIX}.so")):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        lib = ctypes.CDLL(path)
+        _IP = ctypes.POINTER(_I)
+        lib.ref_qsa_run.argtypes = [_I, _I, _I, _I, _I, ctypes.c_float, ctypes.c_float, _F, _F, _I, _I, _I, _IP, _IP,
+                                    _F, _F, ctypes.POINTER(ctypes.c_uint32), _I]
+        lib.ref_qsa_run.restype = _I
+        self.lib = lib
+
+    def run(self, calls, iq, ik, q_gamma, k_gamma, cr, budget, R, theta, eps, max_ctx, mask_words, threads=4):
+        """calls: [(pos, n), ...] in order; iq [sum n, IH, ID], ik [sum n, ID] in call order ->
+        mask [sum n, mask_words] uint32."""
+        iq, ik = _f32(iq), _f32(ik)
+        IH, ID = iq.shape[1], iq.shape[2]
+        cp = np.array([c[0] for c in calls], np.int32)
+        cn = np.array([c[1] for c in calls], np.int32)
+        mask = np.zeros((int(cn.sum()), mask_words), np.uint32)
+        rc = self.lib.ref_qsa_run(IH, ID, cr, budget, R, theta, eps, _fp(_f32(q_gamma)), _fp(_f32(k_gamma)), max_ctx,
+                                  threads, len(calls), cp.ctypes.data_as(ctypes.POINTER(_I)),
+                                  cn.ctypes.data_as(ctypes.POINTER(_I)), _fp(iq), _fp(ik),
+                                  mask.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), mask_words)
+        assert rc == 0, rc
+        return mask
 
 
 class RefPrimitives:

@@ -16,6 +16,9 @@
 //   - parallel_for       src/threadpool.h:25-37 (spinning pool, one contiguous chunk per thread)
 //   - split partials     shaders/attention.comp:26-75 and shaders/attn_combine.comp:13-29 (the
 //                        split-K online softmax and its log-sum-exp merge, on the CPU)
+//   - QSA indexer        src/qwen4_qsa.h:38-54 (pooled block keys), :58-91 (block selection), the
+//                        bitmask of src/qwen4_vk.cpp:952-960, and the masked attention of
+//                        src/qwen4_cpu.cpp:325-344 (runs of visible keys) / shaders/attention.comp:35-43
 // plus an fp64 brute-force attention used to write golden fixtures.
 //
 // Parity pins for every function here live in tests/test_oracle.py (closed forms, invariants,
@@ -290,6 +293,109 @@ void orc_attention_split(const float* q, int q_stride, const float* qg_gate, con
                 if (qg_gate) res[d] *= sigmoid(qg_gate[((size_t)t * NH + h) * 2 * D + D + d]);
             }
         }
+}
+
+// ---- QSA indexer and block-sparse attention ------------------------------------------------------
+
+// Pooled keys of the blocks [b0, b1) of `cr` consecutive positions (src/qwen4_qsa.h:44-53): the mean of
+// the blocks' raw indexer keys raw[pos][ID] accumulated one key at a time (axpy with 1/cr), RMS-normed
+// with the gamma as stored (no 1 + w) and rotated to the block's first position.
+void orc_qsa_pool(const float* raw, const float* gamma, float* pooled, int b0, int b1, int ID, int cr, int R,
+                  double theta, float eps) {
+    std::vector<float> inv(R / 2);
+    for (int i = 0; i < R / 2; i++) inv[i] = (float)(1.0 / std::pow(theta, (2.0 * i) / R));
+    for (int b = b0; b < b1; b++) {
+        float* pk = pooled + (size_t)b * ID;
+        std::fill(pk, pk + ID, 0.f);
+        for (int i = 0; i < cr; i++) axpy(pk, 1.0f / cr, raw + ((size_t)b * cr + i) * ID, ID);
+        rms_mul(pk, gamma, pk, ID, eps);
+        rope(pk, b * cr, inv.data(), R);
+    }
+}
+
+// Block selection for n tokens at positions pos.. (src/qwen4_qsa.h:58-91) written as the per-token
+// bitmask the attention consumes (src/qwen4_vk.cpp:952-960). Token t (position p = pos + t) sees
+// nblk = (p + 1) / cr complete blocks; with nblk <= top it selects nothing and its row is all ones
+// (dense). Otherwise its IH indexer query heads iq[t][h][ID] are RMS-normed (gamma as stored) and rotated
+// to p, block b scores sum_h max(0, q_h . pooled_b), and the `top` best blocks (higher score first, the
+// lower block id on a tie) have their bits set. scores (NULL or [n][stride]) receives the scores of
+// the tokens that select.
+void orc_qsa_select(const float* iq, const float* gamma, const float* pooled, uint32_t* mask, int mask_words,
+                    float* scores, int stride, int pos, int n, int IH, int ID, int cr, int top, int R,
+                    double theta, float eps) {
+    std::vector<float> inv(R / 2);
+    for (int i = 0; i < R / 2; i++) inv[i] = (float)(1.0 / std::pow(theta, (2.0 * i) / R));
+    std::vector<float> q((size_t)IH * ID), sc;
+    std::vector<int> order;
+    for (int t = 0; t < n; t++) {
+        const int p = pos + t, nblk = (p + 1) / cr;
+        uint32_t* m = mask + (size_t)t * mask_words;
+        if (nblk <= top) {
+            std::fill(m, m + mask_words, 0xFFFFFFFFu);
+            continue;
+        }
+        std::fill(m, m + mask_words, 0u);
+        for (int h = 0; h < IH; h++) {
+            rms_mul(iq + ((size_t)t * IH + h) * ID, gamma, &q[(size_t)h * ID], ID, eps);
+            rope(&q[(size_t)h * ID], p, inv.data(), R);
+        }
+        sc.assign(nblk, 0.f);
+        for (int b = 0; b < nblk; b++) {
+            float s = 0;
+            for (int h = 0; h < IH; h++) s += std::max(0.f, dot_f32(&q[(size_t)h * ID], pooled + (size_t)b * ID, ID));
+            sc[b] = s;
+        }
+        if (scores) std::copy(sc.begin(), sc.end(), scores + (size_t)t * stride);
+        order.resize(nblk);
+        for (int b = 0; b < nblk; b++) order[b] = b;
+        std::partial_sort(order.begin(), order.begin() + top, order.end(),
+                          [&](int x, int y) { return sc[x] > sc[y] || (sc[x] == sc[y] && x < y); });
+        for (int i = 0; i < top; i++) m[order[i] >> 5] |= 1u << (order[i] & 31);
+    }
+}
+
+// Causal GQA attention restricted to the keys the QSA mask leaves visible (src/qwen4_cpu.cpp:325-372,
+// shaders/attention.comp:35-43): token t (len = pos + t + 1) attends to the keys of the complete blocks
+// whose bit is set in mask[t][mask_words] and to the incomplete tail block, keys [(len / cr) * cr, len),
+// in key order. Arguments otherwise as orc_attention.
+void orc_attention_qsa(const float* q, int q_stride, const float* qg_gate, const float* kcache,
+                       const float* vcache, float* out, int pos, int n, int NH, int NKV, int D,
+                       const uint32_t* mask, int mask_words, int cr) {
+    const float scale = 1.0f / std::sqrt((float)D);
+    const int group = NH / NKV;
+    pool().parallel_for((int64_t)n * NH, [&](int64_t b, int64_t e) {
+        std::vector<float> sc;
+        std::vector<int> keys;
+        for (int64_t i = b; i < e; i++) {
+            const int t = (int)(i / NH), h = (int)(i % NH), kvh = h / group, len = pos + t + 1;
+            const int tail = len / cr * cr;
+            const uint32_t* m = mask + (size_t)t * mask_words;
+            keys.clear();
+            for (int j = 0; j < len; j++) {
+                const int blk = j / cr;
+                if (j >= tail || (m[blk >> 5] >> (blk & 31)) & 1u) keys.push_back(j);
+            }
+            const float* qh = &q[((size_t)t * NH + h) * q_stride];
+            sc.resize(keys.size());
+            float mx = -1e30f;
+            for (size_t k = 0; k < keys.size(); k++) {
+                sc[k] = dot_f32(qh, &kcache[((size_t)keys[k] * NKV + kvh) * D], D) * scale;
+                mx = std::max(mx, sc[k]);
+            }
+            float sum = 0;
+            for (float& s : sc) {
+                s = std::exp(s - mx);
+                sum += s;
+            }
+            float* o = &out[((size_t)t * NH + h) * D];
+            std::fill(o, o + D, 0.f);
+            for (size_t k = 0; k < keys.size(); k++) axpy(o, sc[k] / sum, &vcache[((size_t)keys[k] * NKV + kvh) * D], D);
+            if (qg_gate) {
+                const float* gate = &qg_gate[((size_t)t * NH + h) * 2 * D + D];
+                for (int d = 0; d < D; d++) o[d] *= sigmoid(gate[d]);
+            }
+        }
+    });
 }
 
 }  // extern "C"

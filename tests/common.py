@@ -60,6 +60,58 @@ QWEN3_NEXT = Shape(16, 2, 256, 64)  # src/model.h:15-20 of the reference
 D128 = Shape(8, 2, 128, 32)        # a head_dim-128 layout: the 128-dim kernel variants
 
 
+class QsaShape:
+    """QSA indexer of a full-attention layer (src/qwen4.h:27, :61): IH indexer heads of ID dims, blocks of
+    CR positions, a budget of `budget` keys (budget / CR blocks), rotated over the layer's rope_dim R."""
+
+    def __init__(self, IH, ID, CR, budget, R, theta=1e7, eps=1e-6):
+        self.IH, self.ID, self.CR, self.budget, self.R, self.theta, self.eps = IH, ID, CR, budget, R, theta, eps
+        self.top = budget // CR
+
+    def mask_words(self, max_ctx):
+        """The mask row width of src/qwen4_vk.cpp:517-519."""
+        return (max_ctx // self.CR + 1 + 31) // 32
+
+    def __repr__(self):
+        return f"qsa{self.IH}x{self.ID}/cr{self.CR}/b{self.budget}/r{self.R}"
+
+
+QSA_TINY = QsaShape(2, 128, 4, 16, 64)     # tests/make_tiny_gguf.py:11 of the reference (rope_dim 64: :10)
+QSA_WIDE = QsaShape(4, 128, 8, 512, 64)    # a production-like budget
+QSA_BLOCK64 = QsaShape(2, 128, 64, 1024, 64)  # blocks longer than a 32-key tile
+QSA_ODD = QsaShape(3, 64, 3, 48, 32)       # a ratio that divides no tile
+
+
+def qsa_inputs(seed, n, qs):
+    """Seeded raw indexer queries iq [n, IH, ID] and keys ik [n, ID] ~ N(0,1), and norm gammas ~ 1 + 0.1 N(0,1)
+    (stored as is: the indexer multiplies by gamma, not 1 + gamma)."""
+    r = np.random.default_rng(seed)
+    iq = r.standard_normal((n, qs.IH, qs.ID)).astype(np.float32)
+    ik = r.standard_normal((n, qs.ID)).astype(np.float32)
+    qg = (1 + 0.1 * r.standard_normal(qs.ID)).astype(np.float32)
+    kg = (1 + 0.1 * r.standard_normal(qs.ID)).astype(np.float32)
+    return iq, ik, qg, kg
+
+
+def qsa_oracle_run(oracle, calls, iq, ik, qg, kg, qs, max_ctx):
+    """The oracle's indexer over a call sequence [(pos, n), ...] with inputs in call order (the reference's
+    update-then-select per call, src/qwen4_cpu.cpp:326-329): masks [sum n, mask_words], and the raw and
+    pooled key arrays after the last call."""
+    mw = qs.mask_words(max_ctx)
+    raw = np.zeros((max_ctx, qs.ID), np.float32)
+    pooled = np.zeros((max_ctx // qs.CR + 1, qs.ID), np.float32)
+    out, row = [], 0
+    for pos, n in calls:
+        raw[pos:pos + n] = ik[row:row + n]
+        oracle.qsa_pool(raw, kg, pos // qs.CR, (pos + n) // qs.CR, qs.CR, qs.R, qs.theta, qs.eps, pooled)
+        if (pos + n) // qs.CR > qs.top:
+            out.append(oracle.qsa_select(iq[row:row + n], qg, pooled, pos, qs.CR, qs.top, qs.R, qs.theta, qs.eps, mw))
+        else:
+            out.append(np.full((n, mw), 0xFFFFFFFF, np.uint32))
+        row += n
+    return np.concatenate(out), raw, pooled
+
+
 def rng(seed):
     return np.random.default_rng(seed)
 

@@ -295,3 +295,141 @@ def test_qk_norm_rope_matches_projection_pipeline(oracle):
             assert np.array_equal(q_out[t, h], exp)
         assert np.array_equal(vc[10 + t], v[t])
     assert not kc[:10].any()
+
+
+# ---- QSA indexer and block-sparse attention (src/qwen4_qsa.h, shaders/attention.comp:35-43) ----------------
+
+from common import QSA_BLOCK64, QSA_ODD, QSA_TINY, QSA_WIDE, qsa_inputs, qsa_oracle_run  # noqa: E402
+
+
+def _ref_qsa():
+    import oracle as orc
+    try:
+        return orc.RefQsa()
+    except (FileNotFoundError, OSError):
+        pytest.skip("oracle/_ref/libref_qsa.so not built (needs /root/reference)")
+
+
+QSA_CALLS = {
+    # a prefill chunk, decode steps, a 4-token verify pass, then a rollback: the pass is redone at the
+    # smaller position (rows and blocks past it are rewritten, src/qwen4_vk.cpp:286-300)
+    "tiny": (QSA_TINY, 256, [(0, 40), (40, 1), (41, 1), (42, 4), (44, 4), (48, 1), (49, 3)]),
+    "wide": (QSA_WIDE, 8192, [(0, 3000), (3000, 1), (3001, 4), (3003, 4), (3007, 1), (3008, 64)]),
+    "block64": (QSA_BLOCK64, 8192, [(0, 2000), (2000, 1), (2001, 100), (2101, 4), (2103, 1)]),
+    "odd": (QSA_ODD, 1024, [(0, 100), (100, 1), (101, 4), (103, 2), (105, 50)]),
+}
+
+
+@pytest.mark.parametrize("name", list(QSA_CALLS))
+def test_qsa_selection_matches_reference(oracle, name):
+    """The oracle's indexer selects exactly the blocks the reference's own QsaIndexer selects (compiled in
+    place: oracle/_ref/libref_qsa.so), over prefill chunks, decode steps, verify passes and a rollback."""
+    ref = _ref_qsa()
+    qs, max_ctx, calls = QSA_CALLS[name]
+    tot = sum(c[1] for c in calls)
+    iq, ik, qg, kg = qsa_inputs(31, tot, qs)
+    mw = qs.mask_words(max_ctx)
+    want = ref.run(calls, iq, ik, qg, kg, qs.CR, qs.budget, qs.R, qs.theta, qs.eps, max_ctx, mw)
+    got, _, _ = qsa_oracle_run(oracle, calls, iq, ik, qg, kg, qs, max_ctx)
+    assert np.array_equal(got, want)
+    # the selecting tokens pick exactly budget / CR blocks
+    row = 0
+    for pos, n in calls:
+        for t in range(n):
+            if (pos + t + 1) // qs.CR > qs.top:
+                assert sum(bin(int(w)).count("1") for w in got[row + t]) == qs.top
+        row += n
+
+
+def test_qsa_pool_closed_forms(oracle):
+    """A block of identical raw keys pools to that key, normed (gamma as stored) and rotated to the block's
+    first position; the first block is not rotated; pooling is the mean (order-free up to rounding)."""
+    qs = QSA_WIDE
+    r = np.random.default_rng(32)
+    g = (1 + 0.1 * r.standard_normal(qs.ID)).astype(np.float32)
+    x = r.standard_normal(qs.ID).astype(np.float32)
+    raw = np.tile(x, (4 * qs.CR, 1))
+    pooled = oracle.qsa_pool(raw, g, 0, 4, qs.CR, qs.R, qs.theta, qs.eps)
+    normed = oracle.rms_mul(x, g, qs.eps)
+    assert np.allclose(pooled[0], normed, rtol=1e-5, atol=1e-6)  # block 0: position 0, no rotation
+    for b in range(1, 4):
+        assert np.allclose(pooled[b], oracle.rope(normed, b * qs.CR, qs.R, qs.theta), rtol=1e-5, atol=1e-5)
+    raw = r.standard_normal((qs.CR, qs.ID)).astype(np.float32)
+    mean = raw.astype(np.float64).mean(axis=0)
+    exp = mean / np.sqrt(np.mean(mean ** 2) + qs.eps) * g
+    p0 = oracle.qsa_pool(raw, g, 0, 1, qs.CR, qs.R, qs.theta, qs.eps)[0]
+    assert np.allclose(p0, exp, rtol=1e-5, atol=1e-6)
+    p1 = oracle.qsa_pool(raw[::-1].copy(), g, 0, 1, qs.CR, qs.R, qs.theta, qs.eps)[0]
+    assert np.allclose(p0, p1, rtol=1e-5, atol=1e-6)
+
+
+def test_qsa_select_brute_force(oracle):
+    """Selection = the budget/CR blocks with the largest fp64 score sum_h relu(q_h . k_b), where the k-th
+    and (k+1)-th scores are apart; all-zero scores fall back to the lowest block ids; tokens that see at
+    most budget/CR complete blocks select nothing (all-ones row)."""
+    qs = QSA_TINY
+    r = np.random.default_rng(33)
+    nblk_max, pos, n = 60, 200, 3
+    pooled = r.standard_normal((nblk_max, qs.ID)).astype(np.float32)
+    iq = r.standard_normal((n, qs.IH, qs.ID)).astype(np.float32)
+    g = np.ones(qs.ID, np.float32)
+    mw = 2
+    mask, scores = oracle.qsa_select(iq, g, pooled, pos, qs.CR, qs.top, qs.R, qs.theta, qs.eps, mw, with_scores=True)
+    for t in range(n):
+        p = pos + t
+        nblk = (p + 1) // qs.CR
+        q = np.stack([oracle.rope(oracle.rms_mul(iq[t, h], g, qs.eps), p, qs.R, qs.theta) for h in range(qs.IH)])
+        s64 = np.maximum(0, q.astype(np.float64) @ pooled[:nblk].astype(np.float64).T).sum(axis=0)
+        assert np.allclose(scores[t, :nblk], s64, rtol=1e-5, atol=1e-5)
+        order = sorted(range(nblk), key=lambda b: (-s64[b], b))
+        sel = {b for b in range(nblk) if (int(mask[t, b >> 5]) >> (b & 31)) & 1}
+        assert len(sel) == qs.top
+        gap = s64[order[qs.top - 1]] - s64[order[qs.top]]
+        if gap > 1e-4:
+            assert sel == set(order[:qs.top])
+    # every score zero (queries opposite to every pooled key): the lowest ids win the ties
+    neg = -np.abs(r.standard_normal((nblk_max, qs.ID))).astype(np.float32)
+    pos_q = np.abs(r.standard_normal((1, qs.IH, qs.ID))).astype(np.float32)
+    m0 = oracle.qsa_select(pos_q, g, neg, 100, qs.CR, qs.top, 0, qs.theta, qs.eps, mw)  # R = 0: no rotation
+    sel = [b for b in range(64) if (int(m0[0, b >> 5]) >> (b & 31)) & 1]
+    assert sel == list(range(qs.top))
+    # not enough complete blocks yet: dense
+    md = oracle.qsa_select(iq[:1], g, pooled, qs.top * qs.CR - 1, qs.CR, qs.top, qs.R, qs.theta, qs.eps, mw)
+    assert np.all(md == 0xFFFFFFFF)
+
+
+@pytest.mark.parametrize("cr", [3, 4, 64])
+def test_attention_qsa_equals_attention_over_visible_keys(oracle, cr):
+    """Masked attention equals plain causal attention over a cache that holds only the visible keys (the
+    selected complete blocks, then the tail block), and with an all-ones mask it equals dense attention."""
+    NH, NKV, D, pos, n = 4, 2, 64, 700, 4
+    q, qg, kc, vc = _rand_attn(34, n, NH, NKV, D, pos + n)
+    r = np.random.default_rng(35)
+    mw = (pos + n) // cr // 32 + 1
+    mask = r.integers(0, 2 ** 32, size=(n, mw), dtype=np.uint64).astype(np.uint32) & np.uint32(0x5A5A33CC)
+    out = oracle.attention_qsa(q, kc, vc, pos, mask, cr, qg)
+    for t in range(n):
+        ln = pos + t + 1
+        tail = ln // cr * cr
+        keys = [j for j in range(ln) if j >= tail or (int(mask[t, (j // cr) >> 5]) >> ((j // cr) & 31)) & 1]
+        exp = oracle.attention(q[t:t + 1], kc[keys], vc[keys], len(keys) - 1, qg[t:t + 1])
+        assert np.abs(out[t] - exp[0]).max() <= 2e-6
+    full = np.full((n, mw), 0xFFFFFFFF, np.uint32)
+    assert np.abs(oracle.attention_qsa(q, kc, vc, pos, full, cr, qg) - oracle.attention(q, kc, vc, pos, qg)).max() <= 1e-6
+
+
+def test_qsa_key_bits():
+    """qsa_key_bits, checked key by key against the rule of shaders/attention.comp:35-43."""
+    import oracle as orc
+    r = np.random.default_rng(36)
+    for cr, pos, n in [(4, 100, 3), (3, 61, 4), (64, 700, 2), (32, 95, 1)]:
+        mw = (pos + n) // cr // 32 + 1
+        mask = r.integers(0, 2 ** 32, size=(n, mw), dtype=np.uint64).astype(np.uint32)
+        bits = orc.qsa_key_bits(mask, pos, n, cr)
+        assert bits.shape == (n, (pos + n + 31) // 32)
+        for t in range(n):
+            tail = (pos + t + 1) // cr * cr
+            for j in range(pos + n):
+                b = j // cr
+                vis = j >= tail or (int(mask[t, b >> 5]) >> (b & 31)) & 1 == 1
+                assert ((int(bits[t, j >> 5]) >> (j & 31)) & 1) == int(vis), (cr, t, j)
