@@ -256,6 +256,41 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
                           void* kcache, void* vcache, int kv_cap, float* out, int pos, int n, int n_split,
                           int* wait_status, int* used_splits);
 
+/* ---- QSA block-sparse attention: the indexer ------------------------------------------------------------
+ * A full-attention layer with a compress ratio `cr` scores blocks of cr consecutive positions with one pooled
+ * key each; past its budget a token attends only to its budget/cr best complete blocks and to the incomplete
+ * tail block (reference: class QsaIndexer, src/qwen4_qsa.h:17-115, run on the CPU there; here on the GPU). */
+
+/* QsaIndexer::update (src/qwen4_qsa.h:38-54): caches the raw indexer keys ik[n][idx_dim] (in_dtype) of
+ * positions pos.. pos+n-1 into raw[cap][idx_dim] fp32 and pools every block the call completes, blocks
+ * [pos/cr, (pos+n)/cr), into pooled[cap/cr + 1][idx_dim] fp32: the mean of the block's raw keys, RMS-normed
+ * with k_gamma as stored (not 1 + gamma) and rotated (rotate-half over the context's rope_dim) to the
+ * block's first position. Positions below pos must have been cached by earlier calls; a pass redone at a
+ * smaller pos (rollback) rewrites what it covers. idx_dim: a multiple of 64, <= 256, >= rope_dim; cr >= 2;
+ * pos + n <= cap <= max_ctx. */
+int qwattn_qsa_pool(qwattn_ctx* ctx, void* stream, const void* ik, int in_dtype, const float* k_gamma,
+                    int idx_dim, int cr, float* raw, float* pooled, int cap, int pos, int n);
+
+/* QsaIndexer::select (src/qwen4_qsa.h:58-91) with the bitmask the Vulkan backend builds from it
+ * (src/qwen4_vk.cpp:952-960). Token t (position p = pos + t) sees nblk = (p + 1) / cr complete blocks. With
+ * nblk <= budget / cr it selects nothing: its mask row is all ones (dense). Otherwise its idx_heads indexer
+ * query heads iq[t][h][idx_dim] (in_dtype) are RMS-normed with q_gamma as stored and rotated to p, block b
+ * scores sum_h max(0, q_h . pooled[b]), and the budget/cr best blocks (higher score first, the lower block id
+ * on a tie) get their bit in mask[t][mask_words] (the other words zero). key_bits[t][kb_words] (either output
+ * may be NULL) receives the per-key form the _qsa attention entry points take: bit j set when key j lies in
+ * a selected block or at or past nblk * cr (the tail block). mask_words * 32 >= (pos+n)/cr; kb_words * 32 >=
+ * pos + n; (pos+n)/cr <= 147,456 blocks; n <= max_tokens; idx_dim as for qwattn_qsa_pool, idx_heads x
+ * idx_dim <= 8192. Calls on one context must not overlap. */
+int qwattn_qsa_select(qwattn_ctx* ctx, void* stream, const void* iq, int in_dtype, const float* q_gamma,
+                      int idx_heads, int idx_dim, int cr, int budget, const float* pooled, int pos, int n,
+                      uint32_t* mask, int mask_words, uint32_t* key_bits, int kb_words);
+
+/* The per-key visibility bits from a block mask in the reference's format (mask[t][mask_words], as the
+ * reference's attention_qsa_kv16 pipeline takes it: shaders/attention.comp:35-43): bit j of key_bits[t] is
+ * set when block j / cr has its bit set or j >= ((pos + t + 1) / cr) * cr. */
+int qwattn_qsa_key_bits(qwattn_ctx* ctx, void* stream, const uint32_t* mask, int mask_words, int cr, int pos,
+                        int n, uint32_t* key_bits, int kb_words);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,9 @@ def load_library():
         "qwattn_prefill": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I],
         "qwattn_layer_attention": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I],
         "qwattn_sync_status": [_P, _P],
+        "qwattn_qsa_pool": [_P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I],
+        "qwattn_qsa_select": [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I],
+        "qwattn_qsa_key_bits": [_P, _P, _P, _I, _I, _I, _I, _P, _I],
         "qwattn_decode_noalloc": [_I, _P, ctypes.POINTER(Config), _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I,
                                   _I, _P, ctypes.POINTER(_I)],
         "qwattn_set_wait_limits": [_P, _I, _I],
@@ -227,6 +230,27 @@ class Attention:
     def attend_prefill(self, q, kcache, vcache, kv_cap, qg, out, pos, n, stream=None):
         self._check(self.lib.qwattn_attend_prefill(self.h, _stream(stream), _ptr(q), _DT[q.dtype], _ptr(kcache),
                                                    _ptr(vcache), kv_cap, _ptr(qg), _DT[qg.dtype], _ptr(out), pos, n))
+
+    # ---- QSA indexer ------------------------------------------------------------------------------------
+
+    def qsa_pool(self, ik, k_gamma, cr, raw, pooled, cap, pos, n, stream=None):
+        """Caches raw indexer keys ik [n, ID] at positions pos.. into raw [cap, ID] and pools the blocks the
+        call completes into pooled [cap // cr + 1, ID] (src/qwen4_qsa.h:38-54)."""
+        self._check(self.lib.qwattn_qsa_pool(self.h, _stream(stream), _ptr(ik), _DT[ik.dtype], _ptr(k_gamma),
+                                             ik.shape[-1], cr, _ptr(raw), _ptr(pooled), cap, pos, n))
+
+    def qsa_select(self, iq, q_gamma, cr, budget, pooled, pos, n, mask=None, key_bits=None, stream=None):
+        """Block selection of iq [n, IH, ID] (src/qwen4_qsa.h:58-91) into mask [n, mask_words] uint32 (as
+        int32 storage) and/or key_bits [n, kb_words]."""
+        self._check(self.lib.qwattn_qsa_select(
+            self.h, _stream(stream), _ptr(iq), _DT[iq.dtype], _ptr(q_gamma), iq.shape[1], iq.shape[2], cr, budget,
+            _ptr(pooled), pos, n, _ptr(mask), 0 if mask is None else mask.shape[-1], _ptr(key_bits),
+            0 if key_bits is None else key_bits.shape[-1]))
+
+    def qsa_key_bits(self, mask, cr, pos, n, key_bits, stream=None):
+        """Per-key visibility bits [n, kb_words] from a block mask [n, mask_words] (shaders/attention.comp:35-43)."""
+        self._check(self.lib.qwattn_qsa_key_bits(self.h, _stream(stream), _ptr(mask), mask.shape[-1], cr, pos, n,
+                                                 _ptr(key_bits), key_bits.shape[-1]))
 
     def attend_prefill_qg(self, qg, qn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
         """The MFMA prefill normalizing and rotating the query half of qg itself (the chunk's K/V rows

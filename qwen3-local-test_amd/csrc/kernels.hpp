@@ -116,4 +116,40 @@ hipError_t launch_q_f16(const float* q, void* out, float scale, size_t n, hipStr
 
 hipError_t launch_rope_table(float* rope, const float* inv_freq, int n_pos, int R, hipStream_t s);
 
+// ---- QSA indexer (qsa.hip) ----
+struct QsaPoolArgs {
+    const void* ik;       // [n][ID] raw indexer keys of positions pos.. (in_dtype)
+    const float* gamma;   // [ID] the indexer key norm's gamma (applied as is)
+    const float* rope;    // rope table [>= pos+n][R/2][2]
+    float* raw;           // [cap][ID] raw keys of every cached position
+    float* pooled;        // [cap / CR + 1][ID] pooled block keys
+    int pos, n, ID, CR, R;
+    float eps;
+};
+hipError_t launch_qsa_pool(const QsaPoolArgs& a, int in_dtype, hipStream_t s);
+
+struct QsaSelectArgs {
+    const void* iq;       // [n][IH][ID] raw indexer queries (in_dtype)
+    const float* gamma;   // [ID] the indexer query norm's gamma (applied as is)
+    const float* rope;
+    const float* pooled;  // [>= (pos+n)/CR][ID]
+    float* scores;        // workspace [n][stride], stride >= (pos+n)/CR
+    int* cnt;             // [n] arrival counters, zero between launches
+    unsigned* mask;       // [n][mask_words] block bitmask, or NULL
+    unsigned* kbits;      // [n][kb_words] key visibility bits, or NULL
+    int mask_words, kb_words, stride;
+    int pos, n, IH, ID, CR, top, R;
+    float eps;
+};
+hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s);
+size_t qsa_select_lds(int IH, int ID);
+int qsa_mask_lds_words();  // complete blocks a select launch can hold: 32 x this
+
+struct QsaKeyBitsArgs {
+    const unsigned* mask;  // [n][mask_words]
+    unsigned* kbits;       // [n][kb_words]
+    int mask_words, kb_words, pos, n, CR;
+};
+hipError_t launch_qsa_key_bits(const QsaKeyBitsArgs& a, hipStream_t s);
+
 }  // namespace qw

@@ -1,0 +1,355 @@
+// QSA block-sparse attention, the indexer side, for gfx950: pooled block keys, block selection, and the
+// per-key visibility bits the attention kernels consume.
+//
+// Replaces the reference's CPU indexer (class QsaIndexer, src/qwen4_qsa.h:17-115) and the bitmask the
+// Vulkan backend builds from its selection (src/qwen4_vk.cpp:952-960). Semantics:
+//  - pooling (QsaIndexer::update, :38-54): block b of CR consecutive positions gets the mean of its raw
+//    indexer keys (accumulated key by key, 1/CR times each), RMS-normed with the gamma as stored (not
+//    1 + gamma) and rotated (rotate-half over the layer's rope_dim) to the block's first position b*CR;
+//  - selection (QsaIndexer::select, :58-91): token t at position p sees nblk = (p + 1) / CR complete
+//    blocks; with nblk <= top = budget / CR it selects nothing (attention stays dense: mask row all
+//    ones). Otherwise its IH indexer query heads are normed and rotated to p, block b scores
+//    sum_h max(0, q_h . pooled_b), and the top blocks by (score, then the lower block id) are selected;
+//  - visibility (shaders/attention.comp:35-43): key j of token t is visible when it lies in a selected
+//    complete block or in the incomplete tail block, j >= nblk * CR.
+//
+// MI355X design (not the reference's): the indexer runs on the GPU, so a QSA layer needs no GPU -> CPU
+// round trip (the reference waits for the GPU and copies the block input out for every QSA layer past
+// the budget). Scoring is spread over (token, 256-block chunk) workgroups, 16 lanes per pooled key
+// (coalesced 512-byte rows); the scores go to a workspace with device-coherent stores, and the last
+// workgroup of a token to arrive (an arrival counter, no waiting anywhere) runs an exact radix select on
+// the scores' bit patterns (scores are >= +0, so their bits order like the values) and writes the mask.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace qw {
+
+namespace {
+
+constexpr int kQsaThreads = 256;
+constexpr int kQsaChunk = 256;        // blocks scored per workgroup
+constexpr int kQsaKeysLds = 12288;    // scores staged in LDS for the select (more: read from memory)
+constexpr int kQsaMaskLds = 4608;     // mask words staged in LDS (>= (262144 / 2 + 1 + 31) / 32)
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// Rotate-half RoPE of one row held in LDS (src/qwen4_qsa.h:99-107): pairs (i, i + R/2), i < R/2, with the
+// (cos, sin) of position p from the rope table [p][R/2][2]; `x` is the normed row, `y` receives the result
+// (dims past R copied). Threads [0, nthr) cooperate.
+__device__ __forceinline__ void rope_row(const float* x, float* y, const float* rope, int p, int R, int ID, int tid,
+                                         int nthr) {
+    const int half = R >> 1;
+    for (int d = tid; d < ID; d += nthr) {
+        if (d < R) {
+            const int i = d < half ? d : d - half;
+            const float cs = rope[((size_t)p * half + i) * 2], sn = rope[((size_t)p * half + i) * 2 + 1];
+            y[d] = d < half ? x[d] * cs - x[d + half] * sn : x[d] * cs + x[d - half] * sn;
+        } else {
+            y[d] = x[d];
+        }
+    }
+}
+
+}  // namespace
+
+// ---- pooling ---------------------------------------------------------------------------------------------
+// Workgroups [0, nbp): one (64 lanes) per block completed by the call, blocks [pos/CR, (pos+n)/CR). The
+// block's rows at positions >= pos come from the call's ik, the earlier ones from the raw cache. Workgroups
+// [nbp, nbp + n): one per new row, appended to the raw cache (the pooling workgroups never read those).
+template <int IN_DT>
+__global__ __launch_bounds__(64) void k_qsa_pool(QsaPoolArgs a) {
+    __shared__ float s_x[512], s_y[512];
+    const int lane = threadIdx.x, ID = a.ID, KD = ID >> 6;
+    const int b0 = a.pos / a.CR, nbp = (a.pos + a.n) / a.CR - b0;
+    if ((int)blockIdx.x >= nbp) {
+        const int t = blockIdx.x - nbp;
+        for (int k = 0; k < KD; k++) {
+            const int d = lane + 64 * k;
+            a.raw[(size_t)(a.pos + t) * ID + d] = load_in<IN_DT>(a.ik, (size_t)t * ID + d);
+        }
+        return;
+    }
+    const int b = b0 + blockIdx.x;
+    const float inv_cr = 1.0f / (float)a.CR;
+    float pk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) pk[k] = 0.f;
+    for (int i = 0; i < a.CR; i++) {
+        const int q = b * a.CR + i;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (k < KD) {
+                const int d = lane + 64 * k;
+                const float x = q >= a.pos ? load_in<IN_DT>(a.ik, (size_t)(q - a.pos) * ID + d) : a.raw[(size_t)q * ID + d];
+                pk[k] = __builtin_fmaf(inv_cr, x, pk[k]);  // ck::axpy with 1/CR, one key at a time
+            }
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        if (k < KD) ss += pk[k] * pk[k];
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)ID + a.eps);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        if (k < KD) {
+            const int d = lane + 64 * k;
+            s_x[d] = pk[k] * r * a.gamma[d];
+        }
+    __syncthreads();
+    rope_row(s_x, s_y, a.rope, b * a.CR, a.R, ID, lane, 64);
+    __syncthreads();
+    for (int d = lane; d < ID; d += 64) a.pooled[(size_t)b * ID + d] = s_y[d];
+}
+
+// ---- selection -------------------------------------------------------------------------------------------
+// Grid (chunks, n): workgroup (c, t) scores blocks [256 c, 256 c + 256) of token t; the last of the token's
+// workgroups to arrive selects. A token that selects nothing has its rows written by workgroup (0, t).
+template <int IN_DT>
+__global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    float* s_q = reinterpret_cast<float*>(smem);          // [IH][ID] normed, rotated query heads
+    float* s_t = s_q + a.IH * a.ID;                         // [IH][ID] the normed heads before rotation
+    unsigned* s_key = reinterpret_cast<unsigned*>(s_t + a.IH * a.ID);  // [kQsaKeysLds] staged score bits
+    unsigned* s_mask = s_key + kQsaKeysLds;                 // [kQsaMaskLds] the token's selection
+    int* s_hist = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [256]
+    int* s_misc = s_hist + 256;                             // [8]
+    int* s_scan = s_misc + 8;                               // [kQsaThreads]
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c = blockIdx.x, t = blockIdx.y;
+    const int p = a.pos + t, nblk = (p + 1) / a.CR, ID = a.ID;
+    const int kb_words = a.kb_words;
+    if (nblk <= a.top) {  // dense: every key visible
+        if (c == 0) {
+            if (a.mask)
+                for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = 0xFFFFFFFFu;
+            if (a.kbits)
+                for (int w = tid; w < kb_words; w += kQsaThreads) a.kbits[(size_t)t * kb_words + w] = 0xFFFFFFFFu;
+        }
+        return;
+    }
+    const int ct = (nblk + kQsaChunk - 1) / kQsaChunk;  // this token's workgroups
+    if (c >= ct) return;
+
+    // the query heads: RMS-normed (gamma as stored), rotated to p; wave w takes heads w, w + 4, ...
+    for (int h = wave; h < a.IH; h += 4) {
+        float ss = 0.f;
+        for (int d = lane; d < ID; d += 64) {
+            const float x = load_in<IN_DT>(a.iq, ((size_t)t * a.IH + h) * ID + d);
+            s_t[h * ID + d] = x;
+            ss += x * x;
+        }
+        ss = wave_sum(ss);
+        const float r = 1.0f / sqrtf(ss / (float)ID + a.eps);
+        for (int d = lane; d < ID; d += 64) s_t[h * ID + d] = s_t[h * ID + d] * r * a.gamma[d];
+    }
+    __syncthreads();
+    for (int h = 0; h < a.IH; h++) rope_row(s_t + h * ID, s_q + h * ID, a.rope, p, a.R, ID, tid, kQsaThreads);
+    __syncthreads();
+
+    // scores of this chunk: 16 lanes per pooled key, DL = ID / 16 consecutive dims a lane
+    const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
+    const int bc0 = c * kQsaChunk, bc1 = min(nblk, bc0 + kQsaChunk);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
+                                                                        a.stride * 4, 0x00020000);
+    for (int b = bc0 + grp; b < bc1; b += kQsaThreads / 16) {
+        const float* pk = a.pooled + (size_t)b * ID + sub * DL;
+        float kv[16];  // DL <= 16: the host keeps ID <= 256
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+            if (i < DL) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
+                kv[i] = v[0], kv[i + 1] = v[1], kv[i + 2] = v[2], kv[i + 3] = v[3];
+            }
+        float s = 0.f;
+        for (int h = 0; h < a.IH; h++) {
+            const float* qh = s_q + h * ID + sub * DL;
+            float dp = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (i < DL) dp = __builtin_fmaf(qh[i], kv[i], dp);
+#pragma unroll
+            for (int o = 8; o >= 1; o >>= 1) dp += __shfl_xor(dp, o, 16);
+            s += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
+        }
+        if (sub == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rs, b * 4, 0, kScDevice);
+    }
+    // arrive: the stores are acknowledged (device-coherent) before the counter moves
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(a.cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_misc[0] = old;
+        if (old == ct - 1) __hip_atomic_store(a.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (s_misc[0] != ct - 1) return;
+
+    // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
+    const bool staged = nblk <= kQsaKeysLds;
+    if (staged)
+        for (int b = tid; b < nblk; b += kQsaThreads) s_key[b] = __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
+    __syncthreads();
+    auto key = [&](int b) -> unsigned { return staged ? s_key[b] : __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice); };
+    unsigned prefix = 0u, pmask = 0u;
+    int need = a.top;  // keys still to take at or below the current prefix
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        s_hist[tid] = 0;
+        __syncthreads();
+        for (int b = tid; b < nblk; b += kQsaThreads) {
+            const unsigned k = key(b);
+            if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255], 1);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // lane l holds digits 255 - 4l .. 252 - 4l; inclusive scan from the top digit down
+            int hv[4], tot = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) tot += (hv[i] = s_hist[255 - 4 * lane - i]);
+            int inc = tot;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int u = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += u;
+            }
+            // the first lane whose digits reach `need` (one always does: the keys matching the prefix number
+            // at least `need`, so lane 63's total reaches it)
+            const unsigned long long hit = __ballot(inc >= need);
+            const int l0 = hit ? __builtin_ctzll(hit) : 63;
+            if (lane == l0) {
+                int above = inc - tot, d = 255 - 4 * lane;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (above + hv[i] >= need) {
+                        d = 255 - 4 * lane - i;
+                        break;
+                    }
+                    above += hv[i];
+                }
+                s_misc[1] = d;
+                s_misc[2] = above;
+            }
+        }
+        __syncthreads();
+        prefix |= (unsigned)s_misc[1] << shift;
+        pmask |= 255u << shift;
+        need -= s_misc[2];
+        __syncthreads();
+    }
+    // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
+    // block order). Thread tid owns the blocks [tid * per, tid * per + per), per a multiple of 32.
+    const int per = ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
+    const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
+    int eq = 0;
+    for (int b = lo; b < hi; b++) eq += key(b) == prefix;
+    s_scan[tid] = eq;
+    __syncthreads();
+    if (tid < 64) {  // exclusive scan of the 256 per-thread counts, 4 a lane
+        int v[4], tot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) tot += (v[i] = s_scan[4 * tid + i]);
+        int inc = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(inc, o, 64);
+            if (tid >= o) inc += u;
+        }
+        int run = inc - tot;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s_scan[4 * tid + i] = run;
+            run += v[i];
+        }
+    }
+    __syncthreads();
+    int taken = s_scan[tid];
+    const int nmw = (nblk + 31) >> 5;  // mask words holding complete blocks
+    // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
+    for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
+        unsigned bits = 0u;
+        for (int i = 0; i < 32; i++) {
+            const int b = 32 * w + i;
+            if (b < hi) {
+                const unsigned k = key(b);
+                bool sel = k > prefix;
+                if (k == prefix) sel = taken++ < need;
+                bits |= (unsigned)sel << i;
+            }
+        }
+        s_mask[w] = bits;
+    }
+    __syncthreads();
+    if (a.mask)
+        for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = w < nmw ? s_mask[w] : 0u;
+    if (a.kbits) {
+        for (int w = tid; w < kb_words; w += kQsaThreads) {
+            unsigned bits = 0u;
+            for (int i = 0; i < 32; i++) {
+                const int blk = (32 * w + i) / a.CR;
+                const bool vis = blk >= nblk || ((s_mask[blk >> 5] >> (blk & 31)) & 1u);
+                bits |= (unsigned)vis << i;
+            }
+            a.kbits[(size_t)t * kb_words + w] = bits;
+        }
+    }
+}
+
+// ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
+__global__ __launch_bounds__(256) void k_qsa_key_bits(QsaKeyBitsArgs a) {
+    const int w = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (w >= a.kb_words) return;
+    const int nblk = (a.pos + t + 1) / a.CR;
+    const unsigned* m = a.mask + (size_t)t * a.mask_words;
+    unsigned bits = 0u;
+    for (int i = 0; i < 32; i++) {
+        const int blk = (32 * w + i) / a.CR;
+        const bool vis = blk >= nblk || ((m[blk >> 5] >> (blk & 31)) & 1u);
+        bits |= (unsigned)vis << i;
+    }
+    a.kbits[(size_t)t * a.kb_words + w] = bits;
+}
+
+size_t qsa_select_lds(int IH, int ID) {
+    return (size_t)2 * IH * ID * 4 + (size_t)(kQsaKeysLds + kQsaMaskLds) * 4 + (256 + 8 + kQsaThreads) * 4;
+}
+
+int qsa_mask_lds_words() { return kQsaMaskLds; }
+
+hipError_t launch_qsa_pool(const QsaPoolArgs& a, int in_dtype, hipStream_t s) {
+    const int nbp = (a.pos + a.n) / a.CR - a.pos / a.CR;
+    const dim3 grid(nbp + a.n);
+    if (in_dtype == 0) hipLaunchKernelGGL(k_qsa_pool<0>, grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_qsa_pool<1>, grid, dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s) {
+    static unsigned raised[2] = {0u, 0u};  // per device: dynamic LDS limit raised (bit per device)
+    const size_t shm = qsa_select_lds(a.IH, a.ID);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+    auto kern = in_dtype == 0 ? k_qsa_select<0> : k_qsa_select<1>;
+    const unsigned bit = 1u << (dev & 31);
+    if (!(raised[in_dtype] & bit)) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+        if (e != hipSuccess) return e;
+        raised[in_dtype] |= bit;
+    }
+    const int nmax = (a.pos + a.n) / a.CR;
+    const dim3 grid((nmax + kQsaChunk - 1) / kQsaChunk > 0 ? (nmax + kQsaChunk - 1) / kQsaChunk : 1, a.n);
+    hipLaunchKernelGGL(kern, grid, dim3(kQsaThreads), shm, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_qsa_key_bits(const QsaKeyBitsArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_qsa_key_bits, dim3((a.kb_words + 255) / 256, a.n), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace qw

@@ -33,6 +33,8 @@ struct qwattn_ctx {
     float* pf_part = nullptr;    // prefill: partials of split query tiles (qw::PrefillArgs::part)
     int* pf_cnt = nullptr;       // prefill: their arrival counters, zero between launches
     int pf_slots_per_head = 0;   // prefill: split slots per KV head in pf_part / pf_cnt
+    float* qsa_scores = nullptr; // QSA select: block scores of the tokens of one launch (kQsaScoreBytes)
+    int* qsa_cnt = nullptr;      // QSA select: per-token arrival counters [max_tokens], zero between launches
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
     int last_splits = 0;         // split count of the last qwattn_attend_partial / qwattn_decode_partial
     int last_n = 0;
@@ -48,6 +50,9 @@ struct qwattn_ctx {
 namespace {
 
 thread_local std::string g_create_err;
+// QSA select workspace per context: the block scores of the tokens one select launch handles (a call's
+// tokens go in as many launches as the scores need: 512 tokens at 8,192 blocks)
+constexpr size_t kQsaScoreBytes = (size_t)16 << 20;
 
 int fail(qwattn_ctx* c, int code, const char* fmt, ...) {
     char buf[512];
@@ -247,6 +252,8 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->ep, sizeof(unsigned long long) * NKV) == hipSuccess &&
               hipMalloc(&c->rec, sizeof(float) * 4 * part) == hipSuccess &&
               hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess &&
+              hipMalloc(&c->qsa_scores, kQsaScoreBytes) == hipSuccess &&
+              hipMalloc(&c->qsa_cnt, sizeof(int) * cfg->max_tokens) == hipSuccess &&
               hipHostMalloc(&c->wait_err_host, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
               hipHostGetDevicePointer((void**)&c->wait_err_dev, c->wait_err_host, 0) == hipSuccess;
     if (!ok) {
@@ -260,6 +267,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
         (R > 0 && qw::launch_rope_table(c->rope, c->inv_freq, cfg->max_ctx, R, nullptr) != hipSuccess) ||
         hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
         hipMemset(c->pf_cnt, 0, sizeof(int) * pf_slots) != hipSuccess ||
+        hipMemset(c->qsa_cnt, 0, sizeof(int) * cfg->max_tokens) != hipSuccess ||
         hipMemset(c->ep, 0, sizeof(unsigned long long) * NKV) != hipSuccess ||
         hipMemset(c->rec, 0, sizeof(float) * 4 * part) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
@@ -275,7 +283,7 @@ int qwattn_destroy(qwattn_ctx* c) {
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
     for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ep, (void*)c->rec,
-                    (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt})
+                    (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt, (void*)c->qsa_scores, (void*)c->qsa_cnt})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
@@ -704,6 +712,85 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
     }
     if (e != hipSuccess) return fail(nullptr, QWATTN_EHIP, "qwattn_decode_noalloc: launch failed: %s", hipGetErrorString(e));
     if (used_splits) *used_splits = sp.S;
+    return QWATTN_OK;
+}
+
+// ---- QSA indexer ----------------------------------------------------------------------------------------
+
+int qwattn_qsa_pool(qwattn_ctx* c, void* stream, const void* ik, int in_dtype, const float* k_gamma, int idx_dim,
+                    int cr, float* raw, float* pooled, int cap, int pos, int n) {
+    if (!c) return QWATTN_EINVAL;
+    if (!ik || !k_gamma || !raw || !pooled) return fail(c, QWATTN_EINVAL, "qwattn_qsa_pool: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    const qwattn_config& g = c->cfg;
+    if (idx_dim <= 0 || idx_dim % 64 || idx_dim > 256 || idx_dim < g.rope_dim)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_pool: idx_dim %d (a multiple of 64, <= 256, >= rope_dim %d)", idx_dim,
+                    g.rope_dim);
+    if (cr < 2) return fail(c, QWATTN_EINVAL, "qwattn_qsa_pool: compress ratio %d (>= 2)", cr);
+    if (n <= 0 || pos < 0 || pos + n > cap || cap > g.max_ctx)
+        return fail(c, QWATTN_ERANGE, "qwattn_qsa_pool: positions [%d, %d) beyond the capacity %d (max_ctx %d)", pos,
+                    pos + n, cap, g.max_ctx);
+    if (int rc = take_wait_error(c)) return rc;
+    DeviceGuard dg(c->device);
+    qw::QsaPoolArgs a{ik, k_gamma, c->rope, raw, pooled, pos, n, idx_dim, cr, g.rope_dim, g.rms_eps};
+    HIP_TRY(c, qw::launch_qsa_pool(a, in_dtype, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+int qwattn_qsa_select(qwattn_ctx* c, void* stream, const void* iq, int in_dtype, const float* q_gamma, int idx_heads,
+                      int idx_dim, int cr, int budget, const float* pooled, int pos, int n, uint32_t* mask,
+                      int mask_words, uint32_t* key_bits, int kb_words) {
+    if (!c) return QWATTN_EINVAL;
+    if (!iq || !q_gamma || !pooled || (!mask && !key_bits))
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    const qwattn_config& g = c->cfg;
+    if (idx_dim <= 0 || idx_dim % 64 || idx_dim > 256 || idx_dim < g.rope_dim || idx_heads <= 0 ||
+        idx_heads * idx_dim > 8192)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: %d heads of %d dims (idx_dim a multiple of 64, <= 256, >= "
+                    "rope_dim %d; heads x dims <= 8192)", idx_heads, idx_dim, g.rope_dim);
+    if (cr < 2 || budget <= 0 || budget % cr)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: budget %d with compress ratio %d (a positive multiple)",
+                    budget, cr);
+    if (n <= 0 || pos < 0 || pos + n > g.max_ctx || n > g.max_tokens)
+        return fail(c, QWATTN_ERANGE, "qwattn_qsa_select: tokens [%d, %d) (max_ctx %d, max_tokens %d)", pos, pos + n,
+                    g.max_ctx, g.max_tokens);
+    const int nmax = (pos + n) / cr;  // complete blocks of the last token
+    if ((nmax + 31) / 32 > qw::qsa_mask_lds_words())
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: %d complete blocks exceed the %d a launch holds", nmax,
+                    32 * qw::qsa_mask_lds_words());
+    if (mask && mask_words * 32 < nmax)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: mask_words %d < %d blocks / 32", mask_words, nmax);
+    if (key_bits && kb_words * 32 < pos + n)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: kb_words %d < %d keys / 32", kb_words, pos + n);
+    if (int rc = take_wait_error(c)) return rc;
+    DeviceGuard dg(c->device);
+    const int stride = std::max(1, nmax);
+    const int per = (int)std::max<size_t>(1, kQsaScoreBytes / ((size_t)stride * sizeof(float)));
+    for (int t0 = 0; t0 < n; t0 += per) {
+        const int nt = std::min(per, n - t0);
+        qw::QsaSelectArgs a{(const char*)iq + (size_t)t0 * idx_heads * idx_dim * (in_dtype == QWATTN_F32 ? 4 : 2),
+                            q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt,
+                            mask ? mask + (size_t)t0 * mask_words : nullptr,
+                            key_bits ? key_bits + (size_t)t0 * kb_words : nullptr, mask_words, kb_words, stride,
+                            pos + t0, nt, idx_heads, idx_dim, cr, budget / cr, g.rope_dim, g.rms_eps};
+        HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
+    }
+    return QWATTN_OK;
+}
+
+int qwattn_qsa_key_bits(qwattn_ctx* c, void* stream, const uint32_t* mask, int mask_words, int cr, int pos, int n,
+                        uint32_t* key_bits, int kb_words) {
+    if (!c) return QWATTN_EINVAL;
+    if (!mask || !key_bits) return fail(c, QWATTN_EINVAL, "qwattn_qsa_key_bits: null pointer");
+    if (cr < 2) return fail(c, QWATTN_EINVAL, "qwattn_qsa_key_bits: compress ratio %d (>= 2)", cr);
+    if (n <= 0 || pos < 0) return fail(c, QWATTN_ERANGE, "qwattn_qsa_key_bits: tokens [%d, %d)", pos, pos + n);
+    if (mask_words * 32 < (pos + n) / cr || kb_words * 32 < pos + n)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_key_bits: mask_words %d / kb_words %d too small for %d keys",
+                    mask_words, kb_words, pos + n);
+    DeviceGuard dg(c->device);
+    qw::QsaKeyBitsArgs a{mask, key_bits, mask_words, kb_words, pos, n, cr};
+    HIP_TRY(c, qw::launch_qsa_key_bits(a, (hipStream_t)stream));
     return QWATTN_OK;
 }
 

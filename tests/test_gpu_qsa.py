@@ -1,0 +1,146 @@
+"""QSA block-sparse attention on the GPU against the CPU oracle (oracle/, pinned to the reference's own
+QsaIndexer in tests/test_oracle.py).
+
+Indexer: the pooled block keys agree with the oracle's to fp32 rounding (rtol 1e-5); the selection is the
+oracle's exactly, except where the oracle's own scores put the budget boundary within float rounding of a
+tie (|score - threshold| <= 1e-5 * (1 + threshold)): there a block may swap with its near-equal neighbour,
+and the test checks that only such blocks differ. Zero scores (all heads' dots negative) tie exactly on
+both sides and fall back to the lower block ids, which the comparison covers.
+"""
+import numpy as np
+import pytest
+import torch
+
+from common import QSA_BLOCK64, QSA_ODD, QSA_TINY, QSA_WIDE, QWEN3_NEXT, QsaShape, qsa_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def _ctx(qw, max_ctx, max_tokens=4096, R=64):
+    s = QWEN3_NEXT
+    return qw.Attention(s.NH, s.NKV, s.D, R, s.theta, s.eps, max_ctx=max_ctx, max_tokens=max_tokens, max_splits=256)
+
+
+def _bits(m, b):
+    return (int(m[b >> 5]) >> (b & 31)) & 1
+
+
+def assert_selection(got, want, scores, qs, pos, n, what):
+    """got/want [n, mask_words] uint32; scores [n, nblk] from the oracle (NaN for dense tokens)."""
+    for t in range(n):
+        nblk = (pos + t + 1) // qs.CR
+        if nblk <= qs.top:
+            assert np.all(got[t] == 0xFFFFFFFF), f"{what}: token {t} should be dense"
+            continue
+        if np.array_equal(got[t], want[t]):
+            continue
+        s = scores[t, :nblk].astype(np.float64)
+        thr = np.sort(s)[::-1][qs.top - 1]
+        tol = 1e-5 * (1 + thr)
+        g = {b for b in range(nblk) if _bits(got[t], b)}
+        w = {b for b in range(nblk) if _bits(want[t], b)}
+        assert len(g) == qs.top, f"{what}: token {t} selected {len(g)} blocks"
+        for b in g ^ w:
+            assert abs(s[b] - thr) <= tol, f"{what}: token {t} block {b} score {s[b]} vs threshold {thr}"
+        assert not np.any(got[t, (nblk + 31) // 32:]), f"{what}: token {t} bits past its complete blocks"
+
+
+# (pos, n, select): indexer calls in order (select False: keys cached and pooled only, as for a long prompt
+# whose selection is not under test)
+CASES = {
+    "tiny": (QSA_TINY, 256, [(0, 40, 1), (40, 1, 1), (41, 1, 1), (42, 4, 1), (44, 4, 1), (48, 1, 1), (49, 3, 1)], "f32"),
+    "wide": (QSA_WIDE, 8192, [(0, 3000, 1), (3000, 1, 1), (3001, 4, 1), (3003, 4, 1), (3007, 1, 1), (3008, 64, 1)],
+             "f32"),
+    "block64": (QSA_BLOCK64, 8192, [(0, 2000, 1), (2000, 1, 1), (2001, 100, 1), (2101, 4, 1), (2103, 1, 1)], "bf16"),
+    "odd": (QSA_ODD, 1024, [(0, 100, 1), (100, 1, 1), (101, 4, 1), (103, 2, 1), (105, 50, 1)], "f32"),
+    # 131,000+ blocks: the scores no longer fit the select's LDS, and 40 tokens take two select launches
+    "long_cr2": (QsaShape(1, 64, 2, 64, 64), 262144, [(0, 262000, 0), (262000, 40, 1)], "f32"),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_qsa_indexer_matches_oracle(qw, oracle, name):
+    import oracle as orc
+    qs, max_ctx, calls, dt = CASES[name]
+    tot = sum(c[1] for c in calls)
+    iq, ik, qg, kg = qsa_inputs(41, tot, qs)
+    if dt == "bf16":  # the oracle reads the same bf16-rounded values
+        iq = torch.from_numpy(iq).bfloat16().float().numpy()
+        ik = torch.from_numpy(ik).bfloat16().float().numpy()
+    tdt = torch.float32 if dt == "f32" else torch.bfloat16
+    ctx = _ctx(qw, max_ctx, R=qs.R)
+    mw = qs.mask_words(max_ctx)
+    raw = torch.zeros((max_ctx, qs.ID), device=DEV)
+    pooled = torch.full((max_ctx // qs.CR + 1, qs.ID), float("nan"), device=DEV)
+    raw_ref = np.zeros((max_ctx, qs.ID), np.float32)
+    pooled_ref = np.zeros((max_ctx // qs.CR + 1, qs.ID), np.float32)
+    qg_d, kg_d = dev(qg), dev(kg)
+    row = 0
+    for pos, n, sel in calls:
+        print(f"qsa {name}: pos={pos} n={n} select={sel}", flush=True)
+        ik_d = dev(ik[row:row + n]).to(tdt)
+        ctx.qsa_pool(ik_d, kg_d, qs.CR, raw, pooled, max_ctx, pos, n)
+        raw_ref[pos:pos + n] = ik[row:row + n]
+        oracle.qsa_pool(raw_ref, kg, pos // qs.CR, (pos + n) // qs.CR, qs.CR, qs.R, qs.theta, qs.eps, pooled_ref)
+        nb = (pos + n) // qs.CR
+        torch.cuda.synchronize()
+        assert np.allclose(host(pooled[:nb]), pooled_ref[:nb], rtol=1e-5, atol=1e-5)
+        if sel:
+            iq_d = dev(iq[row:row + n]).to(tdt)
+            mask = torch.full((n, mw), -1, dtype=torch.int32, device=DEV)
+            kw = (pos + n + 31) // 32
+            kbits = torch.full((n, kw), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+            ctx.qsa_select(iq_d, qg_d, qs.CR, qs.budget, pooled, pos, n, mask, kbits)
+            ctx.sync_status()
+            got = host(mask).view(np.uint32)
+            want, scores = oracle.qsa_select(iq[row:row + n], qg, pooled_ref, pos, qs.CR, qs.top, qs.R, qs.theta,
+                                             qs.eps, mw, with_scores=True)
+            assert_selection(got, want, scores, qs, pos, n, f"{name} pos={pos}")
+            # the key bits follow the GPU's own selection by the reference's visibility rule
+            assert np.array_equal(host(kbits).view(np.uint32), orc.qsa_key_bits(got, pos, n, qs.CR))
+        row += n
+    # the raw cache holds each position's last written key (passes redone at a smaller pos rewrite it)
+    exp = raw_ref
+    assert np.array_equal(host(raw), exp)
+    ctx.close()
+
+
+def test_qsa_key_bits_from_mask(qw):
+    import oracle as orc
+    r = np.random.default_rng(42)
+    ctx = _ctx(qw, 4096)
+    for cr, pos, n in [(4, 1000, 3), (3, 611, 4), (64, 3000, 2), (32, 95, 1), (2, 4000, 8)]:
+        mw = (pos + n) // cr // 32 + 1
+        mask = r.integers(0, 2 ** 32, size=(n, mw), dtype=np.uint64).astype(np.uint32)
+        kw = (pos + n + 31) // 32
+        out = torch.zeros((n, kw), dtype=torch.int32, device=DEV)
+        ctx.qsa_key_bits(dev(mask.view(np.int32)), cr, pos, n, out)
+        ctx.sync_status()
+        assert np.array_equal(host(out).view(np.uint32), orc.qsa_key_bits(mask, pos, n, cr)), (cr, pos, n)
+    ctx.close()
+
+
+def test_qsa_select_rejects_bad_shapes(qw):
+    ctx = _ctx(qw, 4096)
+    qs = QSA_TINY
+    iq = torch.zeros((1, qs.IH, qs.ID), device=DEV)
+    g = torch.ones(qs.ID, device=DEV)
+    pooled = torch.zeros((4096 // qs.CR + 1, qs.ID), device=DEV)
+    mask = torch.zeros((1, 1), dtype=torch.int32, device=DEV)  # 32 blocks: too few for 1,000 / 4
+    with pytest.raises(qw.QwattnError, match="mask_words"):
+        ctx.qsa_select(iq, g, qs.CR, qs.budget, pooled, 999, 1, mask, None)
+    with pytest.raises(qw.QwattnError, match="budget"):
+        ctx.qsa_select(iq, g, qs.CR, 18, pooled, 10, 1, torch.zeros((1, 8), dtype=torch.int32, device=DEV), None)
+    with pytest.raises(qw.QwattnError, match="idx_dim"):
+        ctx.qsa_pool(torch.zeros((1, 96), device=DEV), g, qs.CR, torch.zeros((4096, 96), device=DEV), pooled, 4096, 0, 1)
+    ctx.close()
