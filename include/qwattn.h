@@ -291,6 +291,24 @@ int qwattn_qsa_select(qwattn_ctx* ctx, void* stream, const void* iq, int in_dtyp
 int qwattn_qsa_key_bits(qwattn_ctx* ctx, void* stream, const uint32_t* mask, int mask_words, int cr, int pos,
                         int n, uint32_t* key_bits, int kb_words);
 
+/* qwattn_attend_partial restricted to the keys QSA leaves visible (reference: the attention_qsa_kv16
+ * pipeline, shaders/attention.comp:35-43, dispatched at src/qwen4_vk.cpp:980-984): token t attends to key j
+ * only when bit j of key_bits[t][kb_words] is set (qwattn_qsa_select or qwattn_qsa_key_bits write them;
+ * kb_words * 32 >= pos + n), within its causal range as always. With at most 8 query rows per KV head
+ * (decode) a workgroup reads only the 32-key tiles some token sees, so the bytes streamed fall with the
+ * selection; the split count is raised, if needed, until no workgroup has more than 256 tiles. Partials
+ * and qwattn_combine as for qwattn_attend_partial. */
+int qwattn_attend_partial_qsa(qwattn_ctx* ctx, void* stream, const float* q, const void* kcache,
+                              const void* vcache, int kv_cap, int pos, int n, int n_split,
+                              const uint32_t* key_bits, int kb_words, int* used_splits);
+
+/* qwattn_decode (norm, RoPE and append of the new rows, split attention, combine and gate) with the QSA key
+ * visibility of qwattn_attend_partial_qsa. The new rows are appended whether or not any token sees them. */
+int qwattn_decode_qsa(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
+                      int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
+                      void* vcache, int kv_cap, float* out, int pos, int n, int n_split,
+                      const uint32_t* key_bits, int kb_words, int* used_splits);
+
 #ifdef __cplusplus
 }
 #endif

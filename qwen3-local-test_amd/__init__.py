@@ -71,6 +71,8 @@ def load_library():
         "qwattn_qsa_pool": [_P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I],
         "qwattn_qsa_select": [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I],
         "qwattn_qsa_key_bits": [_P, _P, _P, _I, _I, _I, _I, _P, _I],
+        "qwattn_attend_partial_qsa": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
+        "qwattn_decode_qsa": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P],
         "qwattn_decode_noalloc": [_I, _P, ctypes.POINTER(Config), _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I,
                                   _I, _P, ctypes.POINTER(_I)],
         "qwattn_set_wait_limits": [_P, _I, _I],
@@ -251,6 +253,23 @@ class Attention:
         """Per-key visibility bits [n, kb_words] from a block mask [n, mask_words] (shaders/attention.comp:35-43)."""
         self._check(self.lib.qwattn_qsa_key_bits(self.h, _stream(stream), _ptr(mask), mask.shape[-1], cr, pos, n,
                                                  _ptr(key_bits), key_bits.shape[-1]))
+
+    def attend_partial_qsa(self, q, kcache, vcache, kv_cap, pos, n, n_split, key_bits, stream=None):
+        """attend_partial over the keys whose bit is set in key_bits [n, kb_words]; returns the split count."""
+        used = ctypes.c_int()
+        self._check(self.lib.qwattn_attend_partial_qsa(self.h, _stream(stream), _ptr(q), _ptr(kcache), _ptr(vcache),
+                                                       kv_cap, pos, n, n_split, _ptr(key_bits), key_bits.shape[-1],
+                                                       ctypes.byref(used)))
+        return used.value
+
+    def decode_qsa(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, n_split, key_bits, stream=None):
+        """decode over the keys whose bit is set in key_bits [n, kb_words]; returns the split count."""
+        used = ctypes.c_int()
+        self._check(self.lib.qwattn_decode_qsa(
+            self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
+            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n, n_split, _ptr(key_bits), key_bits.shape[-1],
+            ctypes.byref(used)))
+        return used.value
 
     def attend_prefill_qg(self, qg, qn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
         """The MFMA prefill normalizing and rotating the query half of qg itself (the chunk's K/V rows

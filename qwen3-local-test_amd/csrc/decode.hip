@@ -297,7 +297,7 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
     }
 }
 
-template <int D, int FUSED, int IN_DT>
+template <int D, int FUSED, int IN_DT, int QSA>
 __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     using C = DecCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, RMAX = C::RMAX, BLKE = C::BLKE, NB = C::NB;
@@ -310,6 +310,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     // new positions (fused): images of their cache blocks, [K, V][block], in the cache's blocked layout
     __shared__ __attribute__((aligned(16))) f16 s_img[FUSED ? 2 * NB : 1][FUSED ? BLKE : 8];
     __shared__ float sM[4][RMAX], sL[4][RMAX], sF[4][RMAX];
+    __shared__ unsigned s_qw[QSA ? RMAX : 1][QSA ? kQsaChunkTiles : 1];  // QSA: [slice token][chunk tile] key bits
     f16* s_q = reinterpret_cast<f16*>(s_u);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -323,6 +324,15 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     split_keys(a, z, maxlen, kb, ke);
     const int ntile_wg = (ke - kb + 31) >> 5;
     const int ntile = ntile_wg > wave ? (ntile_wg - wave + 3) >> 2 : 0;  // tiles wave, wave + 4, ...
+    // QSA: the key bits of the slice's tokens over this chunk (one word per 32-key tile) into LDS, first
+    // thing, while few registers are live (the host keeps a chunk at kQsaChunkTiles tiles or fewer)
+    const int tok0 = r0 / G;
+    if constexpr (QSA) {
+        for (int i = tid; i < RMAX * kQsaChunkTiles; i += 256) {
+            const int u = i / kQsaChunkTiles, t = i % kQsaChunkTiles;
+            s_qw[u][t] = tok0 + u < a.n && t < ntile_wg ? a.kbits[(size_t)(tok0 + u) * a.kb_words + (kb >> 5) + t] : 0u;
+        }
+    }
     const int new_lo = FUSED ? a.pos : maxlen;        // first position not read from the cache
 
     // Buffer resources over this chunk's blocks of this KV head. Tiles past the blocks that hold cached
@@ -526,14 +536,16 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
                 vt[dt] = as_h8(v);
             }
         }
+        // QSA: the column's token sees key tb + i when bit i of its word is set
+        const unsigned vis = QSA ? s_qw[min(max((r0 + rcol) / G - tok0, 0), RMAX - 1)][(tb - kb) >> 5] : 0xFFFFFFFFu;
         float sv[8];
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float v = sc[s][i];
-                const int key = tb + 8 * g + 4 * s + i;
-                sv[s * 4 + i] = key < lim ? v : kNegInf;
+                const int kq = 8 * g + 4 * s + i;
+                sv[s * 4 + i] = tb + kq < lim && ((vis >> kq) & 1u) ? v : kNegInf;
             }
         float mx = sv[0];
 #pragma unroll
@@ -660,7 +672,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
 // acknowledged, so it arrives complete (no patching in LDS: LDS stores crawl while the first copies
 // land); V past the last position is zeroed in registers. Spin waits are bounded, so every wave exits
 // even if a counter were never reached; a wait that gives up is reported through DecodeArgs::err.
-template <int D, int FUSED, int IN_DT>
+template <int D, int FUSED, int IN_DT, int QSA>
 __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     constexpr int NKS = D / 32, NDT = D / 16, RMAX = 8, BLKE = kBlk * D;
     constexpr int DPL2 = D / 32;            // dims per lane in the row passes
@@ -676,9 +688,14 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     f16* ring = reinterpret_cast<f16*>(smem);                 // [NCW][2][TILE_E]
     f16* s_q = ring + NCW * 2 * TILE_E;                        // Q fragments (hi rows 0-7, lo rows 8-15)
+    // QSA: the visible tiles (ordinals into the strided sequence) and, per visible tile, each token's
+    // 32 key bits
+    unsigned* s_vl = reinterpret_cast<unsigned*>(s_q + NKS * 64 * 8);  // [kQsaTiles]
+    unsigned* s_vw = s_vl + kQsaTiles;                                  // [kQsaTiles][8]
     // tile counters in a separate LDS object: an access the compiler cannot tell apart from the
     // direct-to-LDS copies' destination makes it wait for every outstanding copy first
     __shared__ int s_cnt[2 * NCW];
+    __shared__ int s_nvis;
     int* ready = s_cnt;        // [NCW] tiles published per pair
     int* freed = s_cnt + NCW;  // [NCW] tiles released per pair
 
@@ -714,7 +731,9 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     const int ntile = z < nb ? (nb - 1 - z) / S + 1 : 0;
     const bool loader = wave >= NCW;
     const int pr = loader ? wave - NCW : 0;                 // loader p streams the tiles p, p + 2, ... of pair p
-    const int ntp = ntile > pr ? (ntile - pr + 1) / 2 : 0;  // its tile count
+    // tiles streamed: all ntile, or (QSA) the nvt that some token sees, known once the list is built
+    int nvt = ntile;
+    int ntp = ntile > pr ? (ntile - pr + 1) / 2 : 0;        // the loader's tile count
     // first new position: the prologue appends the new rows to the caches, and a tile holding any of them
     // is copied only once those stores are complete (after the prologue), so it arrives whole
     const int new_lo = FUSED ? a.pos : maxlen;
@@ -726,7 +745,18 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         const_cast<uint16_t*>(a.kc) + head0, (short)0, nb * bstride, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.vc) + head0, (short)0, nb * bstride, 0x00020000);
-    auto blk_of = [&](int t) { return z + S * t; };
+    // block of streamed tile t (QSA: of the t-th visible tile; the list is read with an inline LDS load, as
+    // the counters are, so a loader wave does not wait for its copies in flight)
+    auto blk_of = [&](int t) -> int {
+        if constexpr (QSA) {
+            int v;
+            const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_vl + t));
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+            return z + S * __builtin_amdgcn_readfirstlane(v);
+        } else {
+            return z + S * t;
+        }
+    };
     // tile t: loader t & 1, its (t >> 1)-th tile, in that loader's slot (t >> 1) & 1
     auto slot_of = [&](int t) { return ring + ((t & 1) * 2 + ((t >> 1) & 1)) * TILE_E; };
     auto has_new = [&](int t) { return FUSED && kBlk * blk_of(t) + kBlk > new_lo; };  // holds new positions
@@ -857,6 +887,34 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): s_q and the counters are in LDS
     } else {
+        if constexpr (QSA) {
+            // the first loader lists the tiles some token sees (a nonzero word of key bits), before any copy
+            // of its own is in flight; the barrier below publishes the list
+            if (wave == NCW) {
+                int nv = 0;
+                for (int base = 0; base < ntile; base += 64) {
+                    const int t = base + lane;
+                    unsigned w[8];
+                    bool any = false;
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        w[u] = 0u;
+                        if (u < a.n && t < ntile) w[u] = a.kbits[(size_t)u * a.kb_words + z + S * t];
+                        any |= w[u] != 0u;
+                    }
+                    const unsigned long long bal = __ballot(any);
+                    const int ord = nv + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
+                    if (any) {
+                        s_vl[ord] = (unsigned)t;
+#pragma unroll
+                        for (int u = 0; u < 8; u++) s_vw[ord * 8 + u] = w[u];
+                    }
+                    nv += __builtin_popcountll(bal);
+                }
+                if (lane == 0) s_nvis = nv;
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the list is in LDS before the barrier
+            }
+        }
         // wait until the compute waves' row loads are issued, then put the first two tiles in flight
         // behind them: issued any earlier, the copies would queue the row loads behind the whole stream
         asm volatile("" ::: "memory");
@@ -864,6 +922,13 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
+        if constexpr (QSA) {
+            int v;
+            const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&s_nvis));
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+            nvt = __builtin_amdgcn_readfirstlane(v);
+            ntp = nvt > pr ? (nvt - pr + 1) / 2 : 0;
+        }
         // a tile holding new positions waits until they are appended (after the prologue); such tiles
         // are the pair's last, so the copies still go out in tile order
         if (ntp > 0 && !has_new(pr)) dma(pr);
@@ -915,10 +980,12 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         // ---- compute wave p takes the pair's tiles p, p + 2, ... from the slots ------------------------
         const int rcol = c & 7;
         const int lim = rcol < rows ? a.pos + rcol / G + 1 : 0;
+        const int utok = min(rcol / G, 7);  // QSA: the column's token
         f16x8 qreg[NKS];
 #pragma unroll
         for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
-        const int ntc = ntile > wave ? (ntile - wave + 1) / 2 : 0;
+        if constexpr (QSA) nvt = s_nvis;
+        const int ntc = nvt > wave ? (nvt - wave + 1) / 2 : 0;
         for (int i = 0; i < ntc; i++) {
             const int t = wave + 2 * i;
             for (int spin = 0; __hip_atomic_load(&ready[wave], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1;
@@ -962,13 +1029,16 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
                 for (int kk = 0; kk < NKS; kk++) x = mfma16(kt[kk][s2], qreg[kk], x);
                 sc[s2] = x;
             }
+            // QSA: the column's token sees key tb + i when bit i of its word is set
+            const unsigned vis = QSA ? s_vw[t * 8 + utok] : 0xFFFFFFFFu;
             float sv[8];
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const float v = sc[s2][e] + xor8(sc[s2][e]);
-                    sv[s2 * 4 + e] = tb + 8 * g + 4 * s2 + e < lim ? v : kNegInf;
+                    const int kq = 8 * g + 4 * s2 + e;
+                    sv[s2 * 4 + e] = tb + kq < lim && ((vis >> kq) & 1u) ? v : kNegInf;
                 }
             float mx = sv[0];
 #pragma unroll
@@ -1071,9 +1141,10 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
     }
 }
 
-template <int D>
+template <int D, int QSA>
 constexpr size_t decode_ld_lds() {
-    const size_t stream = (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2;  // ring + Q fragments
+    // ring + Q fragments (+ QSA: the visible-tile list and its key words)
+    const size_t stream = (size_t)2 * 2 * 2 * kBlk * D * 2 + (size_t)(D / 32) * 64 * 8 * 2 + (QSA ? kQsaTiles * 9 * 4 : 0);
     const size_t comb = (size_t)4 * (D + 2 + kCombGroup) * 4;  // combiner: a window's group sums, maxima, sums, weights
     return stream > comb ? stream : comb;
 }
@@ -1105,9 +1176,16 @@ static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     if (rows <= 8) {
         static std::atomic<uint64_t> raised{0};
         const int ncomb = a.out != nullptr ? a.ncomb : 0;
-        return launch_lds(k_decode_ld<D, FUSED, IN_DT>, raised, dim3(ncomb + a.n_split * a.NKV), decode_ld_lds<D>(), a, s);
+        const dim3 grid(ncomb + a.n_split * a.NKV);
+        if (a.kbits) {
+            static std::atomic<uint64_t> raised_q{0};
+            return launch_lds(k_decode_ld<D, FUSED, IN_DT, 1>, raised_q, grid, decode_ld_lds<D, 1>(), a, s);
+        }
+        return launch_lds(k_decode_ld<D, FUSED, IN_DT, 0>, raised, grid, decode_ld_lds<D, 0>(), a, s);
     }
-    hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT>), dim3(a.n_split, a.NKV, (rows + 15) / 16), dim3(256), 0, s, a);
+    const dim3 grid(a.n_split, a.NKV, (rows + 15) / 16);
+    if (a.kbits) hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT, 1>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_decode<D, FUSED, IN_DT, 0>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

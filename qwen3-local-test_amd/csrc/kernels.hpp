@@ -49,6 +49,8 @@ struct DecodeArgs {
     int ncomb;            // with out: combining workgroups, one per output row (n * NH), first in the grid
     int cap;              // capacity (positions) of the caches kc, vc
     int* err;             // a bounded wait that gives up stores its kWait* code here (nullptr: not reported)
+    const unsigned* kbits;  // QSA: per-token key visibility bits [n][kb_words] (nullptr: dense attention)
+    int kb_words;
     int spin_max;         // polls of the in-launch combine's flag wait before it gives up
     int epoch_skew;       // added to the epoch the combine waits for: 0, or nonzero to force the give-up path
 };
@@ -59,6 +61,8 @@ constexpr int kWaitCombineFlags = 1;  // a combining workgroup: a split's record
 constexpr int kWaitRingLoad = 3;      // a loader wave: its compute wave never released a slot
 constexpr int kWaitRingCompute = 4;   // a compute wave: its loader wave never published a tile
 constexpr int kSpinDefault = 1 << 22; // default DecodeArgs::spin_max (seconds of polling)
+constexpr int kQsaTiles = 256;        // QSA decode (up to 8 rows): tiles per streaming workgroup at most
+constexpr int kQsaChunkTiles = 64;    // QSA verify (16-row slices): tiles per chunk at most
 hipError_t launch_decode(const DecodeArgs& a, int D, bool fused, int in_dtype, hipStream_t s);
 
 // One-launch decode: combining workgroup j of a KV head's m adds (j+1)K/m - jK/m (integer division,

@@ -423,26 +423,63 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* c, void* stream, const void* qg, cons
     return QWATTN_OK;
 }
 
-int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const void* kcache, const void* vcache,
-                          int kv_cap, int pos, int n, int n_split, int* used_splits) {
+// QSA key bits of a call (NULL: dense): checks the row width and raises the split count until no workgroup
+// has more tiles than its kernel holds key words for (kQsaTiles: the loader-wave kernel, at most 8 query rows
+// per KV head; kQsaChunkTiles: the 16-row-slice kernel)
+static int qsa_args(qwattn_ctx* c, const char* fn, const uint32_t* kbits, int kb_words, int pos, int n, Split* sp,
+                    qw::DecodeArgs* a) {
+    if (!kbits) return QWATTN_OK;
+    const qwattn_config& g = c->cfg;
+    if (kb_words * 32 < pos + n)
+        return fail(c, QWATTN_EINVAL, "%s: kb_words %d < %d keys / 32", fn, kb_words, pos + n);
+    const int nb = (pos + n + 31) / 32;
+    const int cap_tiles = n * (g.n_heads / g.n_kv_heads) <= 8 ? qw::kQsaTiles : qw::kQsaChunkTiles;
+    if ((nb + sp->S - 1) / sp->S > cap_tiles) {
+        const int S = (nb + cap_tiles - 1) / cap_tiles;
+        if (S > g.max_splits)
+            return fail(c, QWATTN_EINVAL, "%s: %d keys need %d splits, more than max_splits %d", fn, pos + n, S,
+                        g.max_splits);
+        *sp = Split{S, nb / S, nb % S};
+    }
+    a->kbits = kbits, a->kb_words = kb_words;
+    a->n_split = sp->S, a->cq = sp->cq, a->cr = sp->cr;
+    return QWATTN_OK;
+}
+
+static int attend_partial_impl(qwattn_ctx* c, const char* fn, void* stream, const float* q, const void* kcache,
+                               const void* vcache, int kv_cap, int pos, int n, int n_split, const uint32_t* kbits,
+                               int kb_words, int* used_splits) {
     if (!c) return QWATTN_EINVAL;
-    if (!q || !kcache || !vcache) return fail(c, QWATTN_EINVAL, "qwattn_attend_partial: null pointer");
+    if (!q || !kcache || !vcache) return fail(c, QWATTN_EINVAL, "%s: null pointer", fn);
     int rc = check_call(c, pos, n, kv_cap);
     if (rc) return rc;
     const qwattn_config& g = c->cfg;
     const int G = g.n_heads / g.n_kv_heads;
-    if (n * G > 32)
-        return fail(c, QWATTN_EINVAL, "qwattn_attend_partial: n * NH/NKV = %d > 32 rows (use the prefill kernel)", n * G);
-    const Split sp = pick_split(c, pos + n, n, n_split);
+    if (n * G > 32) return fail(c, QWATTN_EINVAL, "%s: n * NH/NKV = %d > 32 rows (use the prefill kernel)", fn, n * G);
+    Split sp = pick_split(c, pos + n, n, n_split);
+    qw::DecodeArgs a = decode_args(c, q, nullptr, nullptr, nullptr, nullptr, nullptr, kcache, vcache, kv_cap, pos, n, sp);
+    if ((rc = qsa_args(c, fn, kbits, kb_words, pos, n, &sp, &a))) return rc;
     const int used = sp.S;
     DeviceGuard dg(c->device);
-    const qw::DecodeArgs a = decode_args(c, q, nullptr, nullptr, nullptr, nullptr, nullptr, kcache, vcache, kv_cap,
-                                         pos, n, sp);
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, false, QWATTN_F32, (hipStream_t)stream));
     c->last_splits = used;
     c->last_n = n;
     if (used_splits) *used_splits = used;
     return QWATTN_OK;
+}
+
+int qwattn_attend_partial(qwattn_ctx* c, void* stream, const float* q, const void* kcache, const void* vcache,
+                          int kv_cap, int pos, int n, int n_split, int* used_splits) {
+    return attend_partial_impl(c, "qwattn_attend_partial", stream, q, kcache, vcache, kv_cap, pos, n, n_split, nullptr,
+                               0, used_splits);
+}
+
+int qwattn_attend_partial_qsa(qwattn_ctx* c, void* stream, const float* q, const void* kcache, const void* vcache,
+                              int kv_cap, int pos, int n, int n_split, const uint32_t* key_bits, int kb_words,
+                              int* used_splits) {
+    if (c && !key_bits) return fail(c, QWATTN_EINVAL, "qwattn_attend_partial_qsa: null key_bits");
+    return attend_partial_impl(c, "qwattn_attend_partial_qsa", stream, q, kcache, vcache, kv_cap, pos, n, n_split,
+                               key_bits, kb_words, used_splits);
 }
 
 int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
@@ -471,12 +508,13 @@ int qwattn_decode_partial(qwattn_ctx* c, void* stream, const void* qg, const voi
     return QWATTN_OK;
 }
 
-int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
-                  const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
-                  float* out, int pos, int n, int n_split, int* used_splits) {
+static int decode_impl(qwattn_ctx* c, const char* fn, void* stream, const void* qg, const void* k, const void* v,
+                       int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache, void* vcache,
+                       int kv_cap, float* out, int pos, int n, int n_split, const uint32_t* kbits, int kb_words,
+                       int* used_splits) {
     if (!c) return QWATTN_EINVAL;
     if (!qg || !k || !v || !qn || !kn || !kcache || !vcache || !out || (!rope && c->cfg.rope_dim))
-        return fail(c, QWATTN_EINVAL, "qwattn_decode: null pointer");
+        return fail(c, QWATTN_EINVAL, "%s: null pointer", fn);
     if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
     int rc = check_call(c, pos, n, kv_cap);
     if (rc) return rc;
@@ -489,10 +527,11 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     // grid), unless those would take more than half the CUs: then the combine kernel follows
     const int ncomb = n * g.n_heads;
     const bool one = one_launch(c->n_cu, g, n);
-    const Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0, one);
+    Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0, one);
+    qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
+    if ((rc = qsa_args(c, fn, kbits, kb_words, pos, n, &sp, &a))) return rc;
     const int used = sp.S;
     DeviceGuard dg(c->device);
-    qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
     if (one) a.out = out, a.ep = c->ep, a.rec = c->rec, a.ncomb = ncomb;
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     if (!one) {
@@ -503,6 +542,22 @@ int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, co
     c->last_splits = 0;
     if (used_splits) *used_splits = used;
     return QWATTN_OK;
+}
+
+int qwattn_decode(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
+                  const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
+                  float* out, int pos, int n, int n_split, int* used_splits) {
+    return decode_impl(c, "qwattn_decode", stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, out, pos,
+                       n, n_split, nullptr, 0, used_splits);
+}
+
+int qwattn_decode_qsa(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
+                      const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
+                      float* out, int pos, int n, int n_split, const uint32_t* key_bits, int kb_words,
+                      int* used_splits) {
+    if (c && !key_bits) return fail(c, QWATTN_EINVAL, "qwattn_decode_qsa: null key_bits");
+    return decode_impl(c, "qwattn_decode_qsa", stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, out,
+                       pos, n, n_split, key_bits, kb_words, used_splits);
 }
 
 int qwattn_combine(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, float* out, int n, int n_split) {

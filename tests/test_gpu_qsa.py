@@ -23,7 +23,8 @@ def dev(x):
 
 
 def host(t):
-    return t.detach().cpu().numpy()
+    t = t.detach()
+    return (t.float() if t.dtype in (torch.bfloat16, torch.float16) else t).cpu().numpy()
 
 
 def _ctx(qw, max_ctx, max_tokens=4096, R=64):
@@ -144,3 +145,120 @@ def test_qsa_select_rejects_bad_shapes(qw):
     with pytest.raises(qw.QwattnError, match="idx_dim"):
         ctx.qsa_pool(torch.zeros((1, 96), device=DEV), g, qs.CR, torch.zeros((4096, 96), device=DEV), pooled, 4096, 0, 1)
     ctx.close()
+
+
+# ---- block-sparse attention -------------------------------------------------------------------------------
+
+from common import D128, TINY, TINY_GGUF, assert_parity  # noqa: E402
+from test_gpu_kernels import _fused_setup, make_ctx  # noqa: E402
+
+
+def _rand_mask(seed, pos, n, cr, density, mw=None):
+    """A block mask [n, mask_words] with about `density` of each token's complete blocks set."""
+    r = np.random.default_rng(seed)
+    nmax = (pos + n) // cr
+    mw = mw or nmax // 32 + 1
+    bits = r.random((n, mw * 32)) < density
+    bits[:, nmax:] = False
+    return (bits.reshape(n, mw, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
+
+
+# (shape, pos, n, n_split, dtype, cr, density)
+QSA_DEC = [
+    (QWEN3_NEXT, 3000, 1, 0, "f32", 4, 0.1),     # decode: one launch, a few keys per tile
+    (QWEN3_NEXT, 32768, 1, 0, "bf16", 64, 0.05),  # the headline shape, blocks of two tiles: most tiles skipped
+    (QWEN3_NEXT, 20000, 1, 1, "f32", 8, 0.1),    # one split requested: raised until a workgroup lists <= 256 tiles
+    (QWEN3_NEXT, 5000, 4, 0, "f32", 3, 0.2),     # verify: 16-row slices and the combine kernel, blocks across tiles
+    (QWEN3_NEXT, 5000, 4, 1, "bf16", 4, 0.1),    # verify, one split requested: raised to <= 64 tiles a chunk
+    (TINY, 500, 2, 0, "f32", 4, 0.3),            # two tokens on the loader kernel (G = 4): per-token key words
+    (TINY_GGUF, 100, 5, 0, "bf16", 4, 0.25),     # 10 rows at G = 2: 5 tokens in one slice
+    (D128, 2000, 8, 0, "bf16", 8, 0.1),          # 32 rows, 8 tokens in two slices
+    (QWEN3_NEXT, 700, 1, 0, "f32", 4, 0.0),      # nothing selected: only the tail block is visible
+]
+
+
+@pytest.mark.parametrize("s,pos,n,n_split,dtype,cr,density", QSA_DEC, ids=lambda v: repr(v))
+def test_decode_qsa_parity(qw, oracle, s, pos, n, n_split, dtype, cr, density):
+    """qwattn_decode_qsa and qwattn_attend_partial_qsa + qwattn_combine against the oracle's masked attention
+    (src/qwen4_cpu.cpp:325-372 semantics) on the same fp16 rows; the new rows are appended as in the dense
+    path whether or not a token sees them."""
+    import oracle as orc
+    print(f"qsa decode {s} pos={pos} n={n} split={n_split} {dtype} cr={cr} d={density}", flush=True)
+    rows = pos + n
+    cap, k16, v16, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, dtype, 700 + pos + n)
+    mask = _rand_mask(pos + cr, pos, n, cr, density)
+    kbits = dev(orc.qsa_key_bits(mask, pos, n, cr).view(np.int32))
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    used = ctx.decode_qsa(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split, kbits)
+    torch.cuda.synchronize()
+    qg_h, k_h, v_h = host(qg_d), host(k_d), host(v_d)
+    rq, rk, _ = oracle.qk_norm_rope(qg_h, k_h, v_h, 1 + host(qn_d), 1 + host(kn_d), pos, s.R, s.theta, s.eps)
+    krows, vrows = qw.k_rows(kc, cap, s.NKV, s.D), qw.v_rows(vc, cap, s.NKV, s.D)
+    assert np.all(np.abs(host(krows[pos:rows]) - rk[pos:rows]) <= np.abs(rk[pos:rows]) * 2.0 ** -10 + 1e-6)
+    assert np.array_equal(host(vrows[pos:rows]), v_h.astype(np.float16).astype(np.float32))
+    kr, vr = host(krows[:rows]), host(vrows[:rows])
+    ref = oracle.attention_qsa(rq, kr, vr, pos, mask, cr, qg_h)
+    assert_parity(host(out), ref, f"qsa decode {s} pos={pos} n={n} splits={used}")
+    # the per-dispatch form on the same caches (the rows are in place now): normalized query, partials, combine
+    q = dev(rq)
+    out2 = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    used2 = ctx.attend_partial_qsa(q, kc, vc, cap, pos, n, n_split, kbits)
+    ctx.combine(qg_d, out2, n, used2)
+    ctx.sync_status()
+    assert_parity(host(out2), ref, f"qsa attend_partial {s} pos={pos} n={n} splits={used2}")
+
+
+@pytest.mark.parametrize("s,pos,n", [(QWEN3_NEXT, 3000, 1), (QWEN3_NEXT, 3001, 4), (TINY, 301, 2)], ids=repr)
+def test_decode_qsa_all_visible_equals_dense(qw, s, pos, n):
+    """Key bits all set: the masked kernels compute exactly what the dense ones do (same splits, same order)."""
+    cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 800 + pos)
+    kc2, vc2 = kc.clone(), vc.clone()
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    kbits = torch.full((n, (pos + n + 31) // 32), -1, dtype=torch.int32, device=DEV)
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    out2 = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, 0)
+    used2 = ctx.decode_qsa(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc2, vc2, cap, out2, pos, n, 0, kbits)
+    ctx.sync_status()
+    assert used == used2
+    # bit patterns: the caches hold NaN past their end on purpose
+    assert torch.equal(kc.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), vc2.view(torch.int16))
+    assert torch.equal(out, out2)
+
+
+def test_qsa_indexer_then_decode(qw, oracle):
+    """The whole QSA layer step on the GPU: pool the keys of a 3,000-token history and of one new token,
+    select its blocks (budget 512 keys of 3,001), and decode over them; against the oracle's masked attention
+    with the GPU's selection (the selection itself is checked against the oracle above)."""
+    import oracle as orc
+    s, qs = QWEN3_NEXT, QSA_WIDE
+    pos, n = 3000, 1
+    rows = pos + n
+    cap, k16, v16, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 901)
+    iq, ik, qg_i, kg_i = qsa_inputs(902, rows, qs)
+    ctx = make_ctx(qw, s, max_ctx=cap)
+    raw = torch.zeros((cap, qs.ID), device=DEV)
+    pooled = torch.zeros((cap // qs.CR + 1, qs.ID), device=DEV)
+    ctx.qsa_pool(dev(ik[:pos]), dev(kg_i), qs.CR, raw, pooled, cap, 0, pos)
+    ctx.qsa_pool(dev(ik[pos:]), dev(kg_i), qs.CR, raw, pooled, cap, pos, n)
+    mw = qs.mask_words(cap)
+    mask = torch.zeros((n, mw), dtype=torch.int32, device=DEV)
+    kbits = torch.zeros((n, (rows + 31) // 32), dtype=torch.int32, device=DEV)
+    ctx.qsa_select(dev(iq[pos:]), dev(qg_i), qs.CR, qs.budget, pooled, pos, n, mask, kbits)
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    ctx.decode_qsa(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, 0, kbits)
+    ctx.sync_status()
+    m = host(mask).view(np.uint32)
+    assert sum(bin(int(w)).count("1") for w in m[0]) == qs.top
+    assert np.array_equal(host(kbits).view(np.uint32), orc.qsa_key_bits(m, pos, n, qs.CR))
+    qg_h = host(qg_d)
+    rq, _, _ = oracle.qk_norm_rope(qg_h, host(k_d), host(v_d), 1 + host(qn_d), 1 + host(kn_d), pos, s.R, s.theta, s.eps)
+    kr = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
+    vr = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
+    ref = oracle.attention_qsa(rq, kr, vr, pos, m, qs.CR, qg_h)
+    assert_parity(host(out), ref, "qsa layer step")
+    # and it is not the dense result: the selection matters
+    dense = oracle.attention(rq, kr, vr, pos, qg_h)
+    assert np.abs(ref - dense).max() > 1e-2
