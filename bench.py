@@ -146,6 +146,73 @@ class Workload:
         self.att.close()
 
 
+class QsaWorkload(Workload):
+    """A QSA layer step past the budget (the reference's masked path, src/qwen4_vk.cpp:942-984), all on the
+    GPU: pool the new token's indexer key, select its blocks, then the one-launch decode over the keys the
+    selection leaves visible. Indexer: IH heads of ID dims, blocks of CR keys, a budget of BUDGET keys;
+    every layer slot has its own raw and pooled key arrays, built once over the cached history."""
+    IH, ID, CR, BUDGET = 4, 128, 4, 2048
+
+    def __init__(self, qw, name, pos, n, slots, seed=0):
+        import torch
+        super().__init__(qw, name, pos, n, slots, 0, "f32", 0.0, seed)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 1000)
+        self.qsa = True
+        self.raw, self.pooled = [], []
+        self.ik = torch.randn((n, self.ID), device="cuda", generator=g)
+        self.iq = torch.randn((n, self.IH, self.ID), device="cuda", generator=g)
+        self.kg = 1 + 0.1 * torch.randn(self.ID, device="cuda", generator=g)
+        self.qgam = 1 + 0.1 * torch.randn(self.ID, device="cuda", generator=g)
+        for s in range(slots):
+            raw = torch.zeros((self.cap, self.ID), device="cuda")
+            pooled = torch.zeros((self.cap // self.CR + 1, self.ID), device="cuda")
+            hist = torch.randn((pos, self.ID), device="cuda", generator=g)
+            self.att.qsa_pool(hist, self.kg, self.CR, raw, pooled, self.cap, 0, pos)
+            del hist
+            self.raw.append(raw)
+            self.pooled.append(pooled)
+        self.kbits = torch.zeros((n, (pos + n + 31) // 32), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+
+    def select(self, slot):
+        self.att.qsa_pool(self.ik, self.kg, self.CR, self.raw[slot], self.pooled[slot], self.cap, self.pos, self.n)
+        self.att.qsa_select(self.iq, self.qgam, self.CR, self.BUDGET, self.pooled[slot], self.pos, self.n, None,
+                            self.kbits)
+
+    def step(self, slot):
+        self.select(slot)
+        self.att.layer_attention_qsa(slot, self.qg, self.k, self.v, self.qn, self.kn, self.out, self.pos, self.n,
+                                     self.kbits)
+
+    def step_events(self, slot, ev):
+        kc, vc, cap = self.slot_views[slot]
+        ev[0].record()
+        self.select(slot)
+        ev[1].record()
+        self.used = self.att.decode_qsa(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.out,
+                                        self.pos, self.n, 0, self.kbits)
+        ev[2].record()
+
+    def main_only(self, slot):
+        kc, vc, cap = self.slot_views[slot]
+        self.att.decode_qsa(self.qg, self.k, self.v, self.qn, self.kn, self.rope, kc, vc, cap, self.out, self.pos,
+                            self.n, 0, self.kbits)
+
+    def visible(self):
+        """(visible keys, keys of the 32-key tiles that hold one) of the last selection."""
+        import numpy as np
+        w = self.kbits[0].cpu().numpy().view(np.uint32)
+        rows = self.pos + self.n
+        bits = np.unpackbits(w.view(np.uint8), bitorder="little")  # bit j of word i: key 32 i + j
+        bits[rows:] = 0
+        return int(bits.sum()), int(bits.reshape(-1, 32).any(axis=1).sum()) * 32
+
+    def close(self):
+        self.raw, self.pooled = [], []
+        super().close()
+
+
 _SLEEP_PER_MS = None
 KERNEL_BATCHES = 50  # batches of 16 launches timed for the dominant kernel's duration (median reported)
 
@@ -240,7 +307,13 @@ def run_workload(wl, steps, warmup, graph):
     r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all),
          "us_main": statistics.median(per_launch), "us_main_batches": len(per_launch),
          "us_main_min": min(per_launch)}
-    if wl.split:
+    if getattr(wl, "qsa", False):
+        vis, tile_keys = wl.visible()
+        r.update({"kernel": "k_decode_ld<256,1,0,QSA> (one launch, visible tiles only) after k_qsa_pool + k_qsa_select",
+                  "us_indexer": statistics.mean(k_first), "us_main_each_event": statistics.mean(k_second),
+                  "splits": wl.used, "visible_keys": vis, "streamed_tile_keys": tile_keys,
+                  "indexer": f"{wl.IH} heads x {wl.ID} dims, blocks of {wl.CR}, budget {wl.BUDGET}"})
+    elif wl.split:
         if wl.one_launch:
             r.update({"kernel": "k_decode_ld (fused norm+rope+append+split attend+combine, one launch)",
                       "us_main_each_event": statistics.mean(k_first), "splits": wl.used})
@@ -370,6 +443,7 @@ def main():
         ("decode_256k_1024splits", 262144, 1, 2, 1024, "f32", 0.01),
         ("decode_256k", 262144, 1, 2, 0, "f32", 0.01),
         ("prefill_2k_on_2k", 2048, 2048, 8, 0, "bf16", 0.0),
+        ("decode_32k_qsa", 32768, 1, args.slots, 0, "f32", 0.0),
     ]
     results = {}
     for name, pos, n, slots, n_split, dt, heavy in configs:
@@ -377,12 +451,25 @@ def main():
             continue
         print(f"[bench] {name}: pos={pos} n={n} slots={slots} splits={n_split or 'auto'}", file=sys.stderr,
               flush=True)
-        wl = Workload(qw, name, pos, n, slots, n_split, dt, heavy, seed=len(results))
+        if name.endswith("_qsa"):
+            wl = QsaWorkload(qw, name, pos, n, slots, seed=len(results))
+        else:
+            wl = Workload(qw, name, pos, n, slots, n_split, dt, heavy, seed=len(results))
         r = run_workload(wl, args.steps, args.warmup, graph)
         wl.close()
         del wl
         torch.cuda.empty_cache()
-        if n * (NH // NKV) <= 32:
+        if name.endswith("_qsa"):
+            # the K/V bytes of the keys the selection leaves visible (each fp16 row once)
+            byts = 2 * r["visible_keys"] * NKV * D * 2
+            r["value"] = byts / (r["us_per_step"] * 1e-6) / 1e9
+            r["unit"] = "GB/s (visible keys)"
+            r["algorithmic_bytes"] = byts
+            r["frac_hbm_kernel"] = byts / (r["us_main"] * 1e-6) / HBM_PEAK
+            dense = results.get("decode_32k")
+            if dense:
+                r["step_speedup_vs_dense"] = dense["us_per_step"] / r["us_per_step"]
+        elif n * (NH // NKV) <= 32:
             byts = kv_bytes(pos + n)
             r["value"] = byts / (r["us_per_step"] * 1e-6) / 1e9
             r["unit"] = "GB/s"
@@ -396,7 +483,7 @@ def main():
             r["frac_mfma_step"] = fl / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
             r["frac_mfma_kernel"] = fl / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
             r["algorithmic_flops"] = fl
-        if n * (NH // NKV) <= 32:
+        if n * (NH // NKV) <= 32 and not name.endswith("_qsa"):
             r["splits_requested"] = n_split or "auto"
         results[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)

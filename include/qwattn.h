@@ -309,6 +309,26 @@ int qwattn_decode_qsa(qwattn_ctx* ctx, void* stream, const void* qg, const void*
                       void* vcache, int kv_cap, float* out, int pos, int n, int n_split,
                       const uint32_t* key_bits, int kb_words, int* used_splits);
 
+/* The MFMA prefill (qwattn_attend_prefill / qwattn_prefill) with the QSA key visibility of
+ * qwattn_attend_partial_qsa: query row t attends to key j < pos + t + 1 only when bit j of key_bits[t] is
+ * set (the reference runs QSA prefill chunks through the same attention_qsa_kv16 dispatch,
+ * src/qwen4_vk.cpp:980-984). The masked scores are taken out per element; every key tile is still read. */
+int qwattn_attend_prefill_qsa(qwattn_ctx* ctx, void* stream, const void* q, int q_dtype,
+                              const void* kcache, const void* vcache, int kv_cap, const void* qg,
+                              int in_dtype, float* out, int pos, int n, const uint32_t* key_bits,
+                              int kb_words);
+int qwattn_prefill_qsa(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
+                       int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
+                       void* vcache, int kv_cap, float* out, int pos, int n, const uint32_t* key_bits,
+                       int kb_words);
+
+/* qwattn_layer_attention of a QSA layer past its budget (reference: Qwen4Vulkan::attention with `masked`,
+ * src/qwen4_vk.cpp:942-984): the same dispatch (decode, verify, small-group split path, prefill) with the
+ * key visibility bits key_bits[n][kb_words] that qwattn_qsa_select wrote for the pass. */
+int qwattn_layer_attention_qsa(qwattn_ctx* ctx, void* stream, int slot, const void* qg, const void* k,
+                               const void* v, int in_dtype, const float* qn, const float* kn, float* out,
+                               int pos, int n, int n_split, const uint32_t* key_bits, int kb_words);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,9 @@ def load_library():
         "qwattn_qsa_key_bits": [_P, _P, _P, _I, _I, _I, _I, _P, _I],
         "qwattn_attend_partial_qsa": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
         "qwattn_decode_qsa": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P],
+        "qwattn_attend_prefill_qsa": [_P, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _P, _I],
+        "qwattn_prefill_qsa": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I],
+        "qwattn_layer_attention_qsa": [_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _I],
         "qwattn_decode_noalloc": [_I, _P, ctypes.POINTER(Config), _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I,
                                   _I, _P, ctypes.POINTER(_I)],
         "qwattn_set_wait_limits": [_P, _I, _I],
@@ -270,6 +273,23 @@ class Attention:
             _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n, n_split, _ptr(key_bits), key_bits.shape[-1],
             ctypes.byref(used)))
         return used.value
+
+    def attend_prefill_qsa(self, q, kcache, vcache, kv_cap, qg, out, pos, n, key_bits, stream=None):
+        """attend_prefill over the keys whose bit is set in key_bits [n, kb_words]."""
+        self._check(self.lib.qwattn_attend_prefill_qsa(self.h, _stream(stream), _ptr(q), _DT[q.dtype], _ptr(kcache),
+                                                       _ptr(vcache), kv_cap, _ptr(qg), _DT[qg.dtype], _ptr(out), pos,
+                                                       n, _ptr(key_bits), key_bits.shape[-1]))
+
+    def prefill_qsa(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, key_bits, stream=None):
+        """prefill (norm + rope + append, MFMA attention) over the keys whose bit is set in key_bits."""
+        self._check(self.lib.qwattn_prefill_qsa(
+            self.h, _stream(stream), _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(rope),
+            _ptr(kcache), _ptr(vcache), kv_cap, _ptr(out), pos, n, _ptr(key_bits), key_bits.shape[-1]))
+
+    def layer_attention_qsa(self, slot, qg, k, v, qn, kn, out, pos, n, key_bits, n_split=0, stream=None):
+        self._check(self.lib.qwattn_layer_attention_qsa(
+            self.h, _stream(stream), slot, _ptr(qg), _ptr(k), _ptr(v), _DT[qg.dtype], _ptr(qn), _ptr(kn), _ptr(out),
+            pos, n, n_split, _ptr(key_bits), key_bits.shape[-1]))
 
     def attend_prefill_qg(self, qg, qn, rope, kcache, vcache, kv_cap, out, pos, n, stream=None):
         """The MFMA prefill normalizing and rotating the query half of qg itself (the chunk's K/V rows

@@ -288,7 +288,7 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
         }
         __syncthreads();  // s_go is rewritten by the next window
     }
-    if (tid < D) a.out[((size_t)t * a.NH + h) * D + tid] = O / L * sigmoid(gate);
+    if (tid < D) a.out[((size_t)t * a.NH + h) * D + tid] = (L > 0.f ? O / L : 0.f) * sigmoid(gate);
     if (__ballot(gave_up) != 0 && lane == 0) report_wait(a, kWaitCombineFlags);
     if (tid == 0) {  // this combiner is done: its share of the head's epoch step (see kEpochStep)
         const unsigned m = (unsigned)(a.ncomb / a.NKV), j = (unsigned)(t * G + h % G);  // j-th of the head's m
@@ -559,7 +559,7 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         const bool grow = mx > m_run + TAU;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
             const float m_new = fmaxf(m_run, mx);
-            const float corr = exp2_fast(m_run - m_new);
+            const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);  // a column with no key yet: 1
             m_run = m_new;
             l_run *= corr;
 #pragma unroll
@@ -1049,7 +1049,7 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             if (m_run == kNegInf) m_run = mx;
             if (__builtin_amdgcn_ballot_w64(mx > m_run + TAU) != 0) {
                 const float m_new = fmaxf(m_run, mx);
-                const float corr = exp2_fast(m_run - m_new);
+                const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);  // a column with no key yet: 1
                 m_run = m_new;
                 l_run *= corr;
 #pragma unroll
@@ -1265,7 +1265,7 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a, int D) {
                 Os += sOt[k][q] * f;
             }
         }
-        const float inv = 1.0f / Ls;
+        const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;  // a row with no visible key: 0, as the CPU path gives
         f32x4 res;
 #pragma unroll
         for (int i = 0; i < 4; i++) res[i] = Os[i] * inv * sigmoid(gate[i]);

@@ -102,6 +102,8 @@ struct PrefillArgs {
     const float* rope;
     int R;
     float eps;
+    const unsigned* kbits;  // QSA: per-token key visibility bits [n][kb_words] (nullptr: dense)
+    int kb_words;
 };
 // Rope widths the prefill kernel's in-kernel query normalization handles: the rotate-half partner of a
 // lane's dim is then in the same lane.

@@ -198,7 +198,7 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, i
 // (accumulator, reference max, sum) in its half's region of the pair's slot and counts its arrival,
 // unless the partner wave has already arrived; the wave that arrives second merges the two (in a fixed
 // order) and writes the rows, then clears the counter for the next launch.
-template <int D, int IN_DT, bool QF>
+template <int D, int IN_DT, bool QF, bool QSA>
 __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot) {
     using C = PfCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, BLKE = C::BLKE, TILEE = C::TILEE, LOADS = C::LOADS;
@@ -228,6 +228,16 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     const int t_wave_first = t0 + wave * 32 / G;
     const int wave_nomask = a.pos + t_wave_first + 1;  // keys below this are visible to every row of the wave
     const int maxlen = a.pos + a.n;
+    // QSA: the key bits of this lane's token for the current 64-key tile (two words), the next tile's
+    // loaded once these are applied; words past the row's end read as zero
+    const unsigned* qrow = QSA ? a.kbits + (size_t)(row_ok ? t : 0) * a.kb_words : nullptr;
+    unsigned qw0 = 0xFFFFFFFFu, qw1 = 0xFFFFFFFFu;
+    auto qsa_words = [&](int kt) __attribute__((always_inline)) {
+        if constexpr (QSA) {
+            qw0 = 2 * kt < a.kb_words ? qrow[2 * kt] : 0u;
+            qw1 = 2 * kt + 1 < a.kb_words ? qrow[2 * kt + 1] : 0u;
+        }
+    };
 
     // ---- Q^T operand in registers: lane holds row `col`, dims 16*ks + 8*half .. +8 ----------------
     // the loads are issued here, the operand finished once the first K tiles' copies are in flight.
@@ -393,7 +403,9 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
                 m_new = grow ? mx : m_run;
             } else if constexpr (i == M1 + 2) {
                 any_rescale = __builtin_amdgcn_ballot_w64(grow) != 0;
-                corr = exp2_fast(m_run - m_new);  // 0 on a row's first keys, 1 when unchanged
+                // 0 on a row's first keys, 1 when unchanged, and 1 for a row that has seen no key yet (both
+                // maxima -inf: a row a QSA mask hides from this tile while another row of the wave grows)
+                corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
                 m_use = m_new == kNegInf ? 0.f : m_new;
                 m_run = m_new;
             }
@@ -465,6 +477,16 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             __syncthreads();
         }
         const int k0 = kt * PF_KT;
+        if constexpr (QSA) {
+            // register j of lane (col, half) in block sb holds key 32*sb + 16*(j/8) + 8*half + j%8 of the
+            // tile: bit 16*(j/8) + 8*half + j%8 of word sb
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    sc[sb][j] = (((sb ? qw1 : qw0) >> (16 * (j >> 3) + 8 * half + (j & 7))) & 1u) ? sc[sb][j] : kNegInf;
+            qsa_words(kt + 1);
+        }
         if (k0 + PF_KT > wave_nomask) {
             // causal edge: register j of lane (col, half) in block sb holds key
             // k0 + 32*sb + 16*(j/8) + 8*half + j%8, visible to this lane's row when below len
@@ -488,6 +510,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             pprev[sb][1] = pcur[sb][1];
         }
     };
+    qsa_words(lo);
     iter(std::false_type{}, lo);
     for (int kt = lo + 1; kt < hi; kt++) iter(std::true_type{}, kt);
     // ---- P.V of the last tile ----
@@ -615,7 +638,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
 // n_qt-1-p (long) with T = nl + ns key tiles: j = 2p runs the long tile over [x, nl), j = 2p+1 its
 // first x tiles, then the short tile, x = max(0, nl - ceil(T/2)). With n_qt odd the last workgroup
 // runs the middle tile alone.
-template <int D, int IN_DT, bool QF>
+template <int D, int IN_DT, bool QF, bool QSA>
 __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     const int G = a.NH / a.NKV;
     const int tok_per_blk = PF_ROWS / G;
@@ -646,7 +669,7 @@ __global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
     }
     // one call site, so the segment body exists once in the code object
     for (int s = 0; s < nseg; s++)
-        pf_segment<D, IN_DT, QF>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0);
+        pf_segment<D, IN_DT, QF, QSA>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0);
 }
 
 template <int D>
@@ -672,9 +695,11 @@ static hipError_t launch_pf_d(const PrefillArgs& a, int q_dtype, int in_dtype, h
     if (q_dtype != 2) return hipErrorInvalidValue;
     if (!a.q) {
         if (!a.qn || (a.R && !a.rope) || !pf_fused_rope_ok(a.R, D)) return hipErrorInvalidValue;
-        return in_dtype == 0 ? go(k_prefill<D, 0, true>) : go(k_prefill<D, 1, true>);
+        if (a.kbits) return in_dtype == 0 ? go(k_prefill<D, 0, true, true>) : go(k_prefill<D, 1, true, true>);
+        return in_dtype == 0 ? go(k_prefill<D, 0, true, false>) : go(k_prefill<D, 1, true, false>);
     }
-    return in_dtype == 0 ? go(k_prefill<D, 0, false>) : go(k_prefill<D, 1, false>);
+    if (a.kbits) return in_dtype == 0 ? go(k_prefill<D, 0, false, true>) : go(k_prefill<D, 1, false, true>);
+    return in_dtype == 0 ? go(k_prefill<D, 0, false, false>) : go(k_prefill<D, 1, false, false>);
 }
 
 // fp16(q * scale): the prefill operand from fp32 queries; n4 groups of 4 values

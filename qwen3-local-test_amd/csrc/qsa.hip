@@ -26,14 +26,36 @@ namespace qw {
 
 namespace {
 
-constexpr int kQsaThreads = 256;
-constexpr int kQsaChunk = 256;        // blocks scored per workgroup
+constexpr int kQsaThreads = 1024;
+constexpr int kQsaChunk = 512;        // blocks scored per workgroup
 constexpr int kQsaKeysLds = 12288;    // scores staged in LDS for the select (more: read from memory)
 constexpr int kQsaMaskLds = 4608;     // mask words staged in LDS (>= (262144 / 2 + 1 + 31) / 32)
 
+// Sum over each 16-lane row, in every lane of the row (DPP butterfly: quads, eight lanes, sixteen).
+__device__ __forceinline__ float sum16(float x) {
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, false));
+    return x;
+}
+
+// Sum over the wave, in every lane: 32-lane halves (DPP + permlane16), then the halves (permlane32).
 __device__ __forceinline__ float wave_sum(float x) {
+    x = sum32(x);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
+__device__ __forceinline__ unsigned wave_min(unsigned x) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    for (int o = 32; o >= 1; o >>= 1) x = min(x, (unsigned)__shfl_xor((int)x, o, 64));
+    return x;
+}
+
+__device__ __forceinline__ unsigned wave_max(unsigned x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = max(x, (unsigned)__shfl_xor((int)x, o, 64));
     return x;
 }
 
@@ -52,6 +74,20 @@ __device__ __forceinline__ void rope_row(const float* x, float* y, const float* 
             y[d] = x[d];
         }
     }
+}
+
+// Key bits [32 w, 32 w + 32) of a token with nblk complete blocks of `cr` keys and block mask m: key j is
+// visible when block j / cr has its bit set or lies at or past nblk (the tail). One division per word, the
+// block of each following key by counting.
+__device__ __forceinline__ unsigned key_word(const unsigned* m, int w, int cr, int nblk) {
+    int blk = (32 * w) / cr, r = 32 * w - blk * cr;
+    unsigned bits = 0u;
+    for (int i = 0; i < 32; i++) {
+        const bool vis = blk >= nblk || ((m[blk >> 5] >> (blk & 31)) & 1u);
+        bits |= (unsigned)vis << i;
+        if (++r == cr) r = 0, blk++;
+    }
+    return bits;
 }
 
 }  // namespace
@@ -108,18 +144,21 @@ __global__ __launch_bounds__(64) void k_qsa_pool(QsaPoolArgs a) {
 }
 
 // ---- selection -------------------------------------------------------------------------------------------
-// Grid (chunks, n): workgroup (c, t) scores blocks [256 c, 256 c + 256) of token t; the last of the token's
-// workgroups to arrive selects. A token that selects nothing has its rows written by workgroup (0, t).
+// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [512 c, 512 c + 512) of token t; the last of
+// the token's workgroups to arrive selects. A token that selects nothing has its rows written by workgroup
+// (0, t).
 template <int IN_DT>
 __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    float* s_q = reinterpret_cast<float*>(smem);          // [IH][ID] normed, rotated query heads
-    float* s_t = s_q + a.IH * a.ID;                         // [IH][ID] the normed heads before rotation
-    unsigned* s_key = reinterpret_cast<unsigned*>(s_t + a.IH * a.ID);  // [kQsaKeysLds] staged score bits
+    unsigned* s_key = reinterpret_cast<unsigned*>(smem);   // [kQsaKeysLds] staged score bits
     unsigned* s_mask = s_key + kQsaKeysLds;                 // [kQsaMaskLds] the token's selection
-    int* s_hist = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [256]
-    int* s_misc = s_hist + 256;                             // [8]
-    int* s_scan = s_misc + 8;                               // [kQsaThreads]
+    int* s_misc = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [16]
+    int* s_tot = s_misc + 16;                               // [16] digit counts of a pass
+    int* s_scan = s_tot + 16;                               // [kQsaThreads / 64] per-wave sums
+    unsigned char* work = reinterpret_cast<unsigned char*>(s_scan + kQsaThreads / 64);
+    float* s_q = reinterpret_cast<float*>(work);            // scoring: [IH][ID] normed, rotated query heads
+    float* s_t = s_q + a.IH * a.ID;                         // scoring: [IH][ID] the normed heads before rotation
+    unsigned* s_priv = reinterpret_cast<unsigned*>(work);   // select: [16 digits][kQsaThreads] private counts
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x, t = blockIdx.y;
@@ -137,8 +176,8 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     const int ct = (nblk + kQsaChunk - 1) / kQsaChunk;  // this token's workgroups
     if (c >= ct) return;
 
-    // the query heads: RMS-normed (gamma as stored), rotated to p; wave w takes heads w, w + 4, ...
-    for (int h = wave; h < a.IH; h += 4) {
+    // the query heads: RMS-normed (gamma as stored), rotated to p; wave w takes heads w, w + 16, ...
+    for (int h = wave; h < a.IH; h += kQsaThreads / 64) {
         float ss = 0.f;
         for (int d = lane; d < ID; d += 64) {
             const float x = load_in<IN_DT>(a.iq, ((size_t)t * a.IH + h) * ID + d);
@@ -150,35 +189,47 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
         for (int d = lane; d < ID; d += 64) s_t[h * ID + d] = s_t[h * ID + d] * r * a.gamma[d];
     }
     __syncthreads();
-    for (int h = 0; h < a.IH; h++) rope_row(s_t + h * ID, s_q + h * ID, a.rope, p, a.R, ID, tid, kQsaThreads);
+    for (int i = tid; i < a.IH * ID; i += kQsaThreads) {
+        const int h = i / ID;
+        rope_row(s_t + h * ID, s_q + h * ID, a.rope, p, a.R, ID, i - h * ID, ID);
+    }
     __syncthreads();
 
-    // scores of this chunk: 16 lanes per pooled key, DL = ID / 16 consecutive dims a lane
+    // scores of this chunk: 16 lanes per pooled key, DL = ID / 16 consecutive dims a lane, 64 keys a round;
+    // the loads of four rounds are issued before any is used
     const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
     const int bc0 = c * kQsaChunk, bc1 = min(nblk, bc0 + kQsaChunk);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
                                                                         a.stride * 4, 0x00020000);
-    for (int b = bc0 + grp; b < bc1; b += kQsaThreads / 16) {
-        const float* pk = a.pooled + (size_t)b * ID + sub * DL;
-        float kv[16];  // DL <= 16: the host keeps ID <= 256
+    constexpr int RB = 4, GPR = kQsaThreads / 16;  // rounds per batch, keys per round
+    for (int b0 = bc0; b0 < bc1; b0 += RB * GPR) {
+        float kv[RB][16];
 #pragma unroll
-        for (int i = 0; i < 16; i += 4)
-            if (i < DL) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
-                kv[i] = v[0], kv[i + 1] = v[1], kv[i + 2] = v[2], kv[i + 3] = v[3];
-            }
-        float s = 0.f;
-        for (int h = 0; h < a.IH; h++) {
-            const float* qh = s_q + h * ID + sub * DL;
-            float dp = 0.f;
+        for (int rr = 0; rr < RB; rr++) {
+            const int b = min(b0 + rr * GPR + grp, bc1 - 1);  // past the chunk: a valid row, score not stored
+            const float* pk = a.pooled + (size_t)b * ID + sub * DL;
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                if (i < DL) dp = __builtin_fmaf(qh[i], kv[i], dp);
-#pragma unroll
-            for (int o = 8; o >= 1; o >>= 1) dp += __shfl_xor(dp, o, 16);
-            s += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
+            for (int i = 0; i < 16; i += 4)
+                if (i < DL) {  // DL <= 16: the host keeps ID <= 256
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
+                    kv[rr][i] = v[0], kv[rr][i + 1] = v[1], kv[rr][i + 2] = v[2], kv[rr][i + 3] = v[3];
+                }
         }
-        if (sub == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rs, b * 4, 0, kScDevice);
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            const int b = b0 + rr * GPR + grp;
+            float s = 0.f;
+            for (int h = 0; h < a.IH; h++) {
+                const float* qh = s_q + h * ID + sub * DL;
+                float dp = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (i < DL) dp = __builtin_fmaf(qh[i], kv[rr][i], dp);
+                dp = sum16(dp);
+                s += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
+            }
+            if (sub == 0 && b < bc1) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rs, b * 4, 0, kScDevice);
+        }
     }
     // arrive: the stores are acknowledged (device-coherent) before the counter moves
     __builtin_amdgcn_s_waitcnt(0);
@@ -193,54 +244,70 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
 
     // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
     const bool staged = nblk <= kQsaKeysLds;
-    if (staged)
-        for (int b = tid; b < nblk; b += kQsaThreads) s_key[b] = __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
-    __syncthreads();
+    unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
+    for (int b = tid; b < nblk; b += kQsaThreads) {
+        const unsigned k = __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
+        if (staged) s_key[b] = k;
+        kmin = min(kmin, k), kmax = max(kmax, k);
+    }
     auto key = [&](int b) -> unsigned { return staged ? s_key[b] : __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice); };
-    unsigned prefix = 0u, pmask = 0u;
+    kmin = wave_min(kmin), kmax = wave_max(kmax);
+    if (lane == 0) s_scan[wave] = (int)kmin;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned m = 0xFFFFFFFFu;
+        for (int w = 0; w < kQsaThreads / 64; w++) m = min(m, (unsigned)s_scan[w]);
+        s_misc[3] = (int)m;
+    }
+    __syncthreads();
+    if (lane == 0) s_scan[wave] = (int)kmax;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned m = 0u;
+        for (int w = 0; w < kQsaThreads / 64; w++) m = max(m, (unsigned)s_scan[w]);
+        s_misc[4] = (int)m;
+    }
+    __syncthreads();
+    kmin = (unsigned)s_misc[3], kmax = (unsigned)s_misc[4];
+    // the bits above the highest one where the smallest and largest keys differ are every key's: the radix
+    // passes (4 bits each, from the top) start at the digit holding that bit
+    const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
+    const int shift0 = hb < 0 ? -4 : (hb & ~3);
+    unsigned pmask = hb < 0 ? 0xFFFFFFFFu : (shift0 + 4 >= 32 ? 0u : ~0u << (shift0 + 4));
+    unsigned prefix = kmin & pmask;
     int need = a.top;  // keys still to take at or below the current prefix
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        s_hist[tid] = 0;
-        __syncthreads();
+    for (int shift = shift0; shift >= 0; shift -= 4) {
+        // each thread counts into its own 16 bins (one uncontended LDS add a key), one digit summed per wave
+#pragma unroll
+        for (int i = 0; i < 16; i++) s_priv[i * kQsaThreads + tid] = 0u;
         for (int b = tid; b < nblk; b += kQsaThreads) {
             const unsigned k = key(b);
-            if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255], 1);
+            if ((k & pmask) == prefix) s_priv[((k >> shift) & 15u) * kQsaThreads + tid] += 1u;
         }
         __syncthreads();
-        if (wave == 0) {
-            // lane l holds digits 255 - 4l .. 252 - 4l; inclusive scan from the top digit down
-            int hv[4], tot = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) tot += (hv[i] = s_hist[255 - 4 * lane - i]);
-            int inc = tot;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int u = __shfl_up(inc, o, 64);
-                if (lane >= o) inc += u;
-            }
-            // the first lane whose digits reach `need` (one always does: the keys matching the prefix number
-            // at least `need`, so lane 63's total reaches it)
-            const unsigned long long hit = __ballot(inc >= need);
-            const int l0 = hit ? __builtin_ctzll(hit) : 63;
-            if (lane == l0) {
-                int above = inc - tot, d = 255 - 4 * lane;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    if (above + hv[i] >= need) {
-                        d = 255 - 4 * lane - i;
-                        break;
-                    }
-                    above += hv[i];
+        if (wave < 16) {
+            unsigned v = 0u;
+            for (int i = lane; i < kQsaThreads; i += 64) v += s_priv[wave * kQsaThreads + i];
+            v = (unsigned)wave_sum((float)v);  // at most 147,456: exact in fp32
+            if (lane == 0) s_tot[wave] = (int)v;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int above = 0, d = 0;
+            for (int i = 15; i >= 0; i--) {
+                if (above + s_tot[i] >= need) {
+                    d = i;
+                    break;
                 }
-                s_misc[1] = d;
-                s_misc[2] = above;
+                above += s_tot[i];
             }
+            s_misc[1] = d;
+            s_misc[2] = above;
         }
         __syncthreads();
         prefix |= (unsigned)s_misc[1] << shift;
-        pmask |= 255u << shift;
+        pmask |= 15u << shift;
         need -= s_misc[2];
-        __syncthreads();
     }
     // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
     // block order). Thread tid owns the blocks [tid * per, tid * per + per), per a multiple of 32.
@@ -248,27 +315,18 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
     int eq = 0;
     for (int b = lo; b < hi; b++) eq += key(b) == prefix;
-    s_scan[tid] = eq;
-    __syncthreads();
-    if (tid < 64) {  // exclusive scan of the 256 per-thread counts, 4 a lane
-        int v[4], tot = 0;
+    // exclusive prefix of the equal counts over the threads: within the wave (shuffles), then the waves
+    int inc = eq;
 #pragma unroll
-        for (int i = 0; i < 4; i++) tot += (v[i] = s_scan[4 * tid + i]);
-        int inc = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int u = __shfl_up(inc, o, 64);
-            if (tid >= o) inc += u;
-        }
-        int run = inc - tot;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            s_scan[4 * tid + i] = run;
-            run += v[i];
-        }
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += u;
     }
+    if (lane == 63) s_scan[wave] = inc;
     __syncthreads();
-    int taken = s_scan[tid];
+    int base = 0;
+    for (int w = 0; w < wave; w++) base += s_scan[w];
+    int taken = base + inc - eq;
     const int nmw = (nblk + 31) >> 5;  // mask words holding complete blocks
     // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
     for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
@@ -287,36 +345,21 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     __syncthreads();
     if (a.mask)
         for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = w < nmw ? s_mask[w] : 0u;
-    if (a.kbits) {
-        for (int w = tid; w < kb_words; w += kQsaThreads) {
-            unsigned bits = 0u;
-            for (int i = 0; i < 32; i++) {
-                const int blk = (32 * w + i) / a.CR;
-                const bool vis = blk >= nblk || ((s_mask[blk >> 5] >> (blk & 31)) & 1u);
-                bits |= (unsigned)vis << i;
-            }
-            a.kbits[(size_t)t * kb_words + w] = bits;
-        }
-    }
+    if (a.kbits)
+        for (int w = tid; w < kb_words; w += kQsaThreads)
+            a.kbits[(size_t)t * kb_words + w] = key_word(s_mask, w, a.CR, nblk);
 }
 
 // ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
 __global__ __launch_bounds__(256) void k_qsa_key_bits(QsaKeyBitsArgs a) {
     const int w = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
     if (w >= a.kb_words) return;
-    const int nblk = (a.pos + t + 1) / a.CR;
-    const unsigned* m = a.mask + (size_t)t * a.mask_words;
-    unsigned bits = 0u;
-    for (int i = 0; i < 32; i++) {
-        const int blk = (32 * w + i) / a.CR;
-        const bool vis = blk >= nblk || ((m[blk >> 5] >> (blk & 31)) & 1u);
-        bits |= (unsigned)vis << i;
-    }
-    a.kbits[(size_t)t * a.kb_words + w] = bits;
+    a.kbits[(size_t)t * a.kb_words + w] = key_word(a.mask + (size_t)t * a.mask_words, w, a.CR, (a.pos + t + 1) / a.CR);
 }
 
 size_t qsa_select_lds(int IH, int ID) {
-    return (size_t)2 * IH * ID * 4 + (size_t)(kQsaKeysLds + kQsaMaskLds) * 4 + (256 + 8 + kQsaThreads) * 4;
+    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)16 * kQsaThreads * 4);
+    return (size_t)(kQsaKeysLds + kQsaMaskLds + 32 + kQsaThreads / 64) * 4 + work;
 }
 
 int qsa_mask_lds_words() { return kQsaMaskLds; }

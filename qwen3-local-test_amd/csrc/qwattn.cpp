@@ -592,18 +592,26 @@ static int prefill_args(qwattn_ctx* c, const void* q, const void* kcache, const 
     return QWATTN_OK;
 }
 
-int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtype, const void* kcache,
-                          const void* vcache, int kv_cap, const void* qg, int in_dtype, float* out, int pos, int n) {
+static int kbits_ok(qwattn_ctx* c, const char* fn, const uint32_t* kbits, int kb_words, int pos, int n) {
+    if (kbits && kb_words * 32 < pos + n)
+        return fail(c, QWATTN_EINVAL, "%s: kb_words %d < %d keys / 32", fn, kb_words, pos + n);
+    return QWATTN_OK;
+}
+
+static int attend_prefill_impl(qwattn_ctx* c, const char* fn, void* stream, const void* q, int q_dtype,
+                               const void* kcache, const void* vcache, int kv_cap, const void* qg, int in_dtype,
+                               float* out, int pos, int n, const uint32_t* kbits, int kb_words) {
     if (!c) return QWATTN_EINVAL;
-    if (!q || !kcache || !vcache || !qg || !out) return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill: null pointer");
+    if (!q || !kcache || !vcache || !qg || !out) return fail(c, QWATTN_EINVAL, "%s: null pointer", fn);
     if (q_dtype != QWATTN_F32 && q_dtype != QWATTN_F16) return fail(c, QWATTN_EINVAL, "q_dtype %d", q_dtype);
     if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
     int rc = check_call(c, pos, n, kv_cap);
-    if (rc) return rc;
+    if (rc || (rc = kbits_ok(c, fn, kbits, kb_words, pos, n))) return rc;
     const qwattn_config& g = c->cfg;
     DeviceGuard dg(c->device);
     qw::PrefillArgs a;
     if ((rc = prefill_args(c, q, kcache, vcache, kv_cap, qg, out, pos, n, &a))) return rc;
+    a.kbits = kbits, a.kb_words = kb_words;
     if (q_dtype == QWATTN_F32) {  // the kernel's operand: fp16(q * log2(e)/sqrt(D)) in the context's query buffer
         HIP_TRY(c, qw::launch_q_f16(static_cast<const float*>(q), c->q16, a.q_scale, (size_t)n * g.n_heads * g.head_dim,
                                     (hipStream_t)stream));
@@ -613,69 +621,125 @@ int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtyp
     return QWATTN_OK;
 }
 
-int qwattn_attend_prefill_qg(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, const float* qn,
-                             const float* rope, const void* kcache, const void* vcache, int kv_cap, float* out,
-                             int pos, int n) {
+int qwattn_attend_prefill(qwattn_ctx* c, void* stream, const void* q, int q_dtype, const void* kcache,
+                          const void* vcache, int kv_cap, const void* qg, int in_dtype, float* out, int pos, int n) {
+    return attend_prefill_impl(c, "qwattn_attend_prefill", stream, q, q_dtype, kcache, vcache, kv_cap, qg, in_dtype,
+                               out, pos, n, nullptr, 0);
+}
+
+int qwattn_attend_prefill_qsa(qwattn_ctx* c, void* stream, const void* q, int q_dtype, const void* kcache,
+                              const void* vcache, int kv_cap, const void* qg, int in_dtype, float* out, int pos, int n,
+                              const uint32_t* key_bits, int kb_words) {
+    if (c && !key_bits) return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill_qsa: null key_bits");
+    return attend_prefill_impl(c, "qwattn_attend_prefill_qsa", stream, q, q_dtype, kcache, vcache, kv_cap, qg,
+                               in_dtype, out, pos, n, key_bits, kb_words);
+}
+
+static int attend_prefill_qg_impl(qwattn_ctx* c, const char* fn, void* stream, const void* qg, int in_dtype,
+                                  const float* qn, const float* rope, const void* kcache, const void* vcache,
+                                  int kv_cap, float* out, int pos, int n, const uint32_t* kbits, int kb_words) {
     if (!c) return QWATTN_EINVAL;
     const qwattn_config& g = c->cfg;
     if (!qg || !qn || !kcache || !vcache || !out || (!rope && g.rope_dim))
-        return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill_qg: null pointer");
+        return fail(c, QWATTN_EINVAL, "%s: null pointer", fn);
     if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
     if (!qw::pf_fused_rope_ok(g.rope_dim, g.head_dim))
-        return fail(c, QWATTN_EINVAL, "qwattn_attend_prefill_qg: rope_dim %d (needs 0, 32, 64, 128 or 256, <= head_dim %d)",
-                    g.rope_dim, g.head_dim);
+        return fail(c, QWATTN_EINVAL, "%s: rope_dim %d (needs 0, 32, 64, 128 or 256, <= head_dim %d)", fn, g.rope_dim,
+                    g.head_dim);
     int rc = check_call(c, pos, n, kv_cap);
-    if (rc) return rc;
+    if (rc || (rc = kbits_ok(c, fn, kbits, kb_words, pos, n))) return rc;
     DeviceGuard dg(c->device);
     qw::PrefillArgs a;
     if ((rc = prefill_args(c, nullptr, kcache, vcache, kv_cap, qg, out, pos, n, &a))) return rc;
     a.qn = qn;
     a.rope = rope;
     a.R = g.rope_dim;
+    a.kbits = kbits, a.kb_words = kb_words;
     HIP_TRY(c, qw::launch_prefill(a, g.head_dim, 2, in_dtype, (hipStream_t)stream));
     return QWATTN_OK;
+}
+
+int qwattn_attend_prefill_qg(qwattn_ctx* c, void* stream, const void* qg, int in_dtype, const float* qn,
+                             const float* rope, const void* kcache, const void* vcache, int kv_cap, float* out,
+                             int pos, int n) {
+    return attend_prefill_qg_impl(c, "qwattn_attend_prefill_qg", stream, qg, in_dtype, qn, rope, kcache, vcache,
+                                  kv_cap, out, pos, n, nullptr, 0);
+}
+
+static int prefill_impl(qwattn_ctx* c, const char* fn, void* stream, const void* qg, const void* k, const void* v,
+                        int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache, void* vcache,
+                        int kv_cap, float* out, int pos, int n, const uint32_t* kbits, int kb_words) {
+    if (!c) return QWATTN_EINVAL;
+    if (!out) return fail(c, QWATTN_EINVAL, "%s: null pointer", fn);
+    int rc = kbits_ok(c, fn, kbits, kb_words, pos, n);
+    if (rc) return rc;
+    if (qw::pf_fused_rope_ok(c->cfg.rope_dim, c->cfg.head_dim)) {
+        // the key and value rows appended, then the MFMA prefill normalizing the query rows itself
+        rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, nullptr,
+                                        QWATTN_F16, pos, n);
+        if (rc) return rc;
+        return attend_prefill_qg_impl(c, fn, stream, qg, in_dtype, qn, rope ? rope : c->rope, kcache, vcache, kv_cap,
+                                      out, pos, n, kbits, kb_words);
+    }
+    // norm + rope + append into the context's fp16 query buffer, then the MFMA prefill on it
+    rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, c->q16,
+                                    QWATTN_F16, pos, n);
+    if (rc) return rc;
+    return attend_prefill_impl(c, fn, stream, c->q16, QWATTN_F16, kcache, vcache, kv_cap, qg, in_dtype, out, pos, n,
+                               kbits, kb_words);
 }
 
 int qwattn_prefill(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
                    const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
                    float* out, int pos, int n) {
-    if (!c) return QWATTN_EINVAL;
-    if (!out) return fail(c, QWATTN_EINVAL, "qwattn_prefill: null pointer");
-    if (qw::pf_fused_rope_ok(c->cfg.rope_dim, c->cfg.head_dim)) {
-        // the key and value rows appended, then the MFMA prefill normalizing the query rows itself
-        int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap,
-                                            nullptr, QWATTN_F16, pos, n);
-        if (rc) return rc;
-        return qwattn_attend_prefill_qg(c, stream, qg, in_dtype, qn, rope ? rope : c->rope, kcache, vcache, kv_cap,
-                                        out, pos, n);
-    }
-    // norm + rope + append into the context's fp16 query buffer, then the MFMA prefill on it
-    int rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, c->q16,
-                                        QWATTN_F16, pos, n);
-    if (rc) return rc;
-    return qwattn_attend_prefill(c, stream, c->q16, QWATTN_F16, kcache, vcache, kv_cap, qg, in_dtype, out, pos, n);
+    return prefill_impl(c, "qwattn_prefill", stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, out,
+                        pos, n, nullptr, 0);
 }
 
-int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg, const void* k, const void* v,
-                           int in_dtype, const float* qn, const float* kn, float* out, int pos, int n, int n_split) {
+int qwattn_prefill_qsa(qwattn_ctx* c, void* stream, const void* qg, const void* k, const void* v, int in_dtype,
+                       const float* qn, const float* kn, const float* rope, void* kcache, void* vcache, int kv_cap,
+                       float* out, int pos, int n, const uint32_t* key_bits, int kb_words) {
+    if (c && !key_bits) return fail(c, QWATTN_EINVAL, "qwattn_prefill_qsa: null key_bits");
+    return prefill_impl(c, "qwattn_prefill_qsa", stream, qg, k, v, in_dtype, qn, kn, rope, kcache, vcache, kv_cap, out,
+                        pos, n, key_bits, kb_words);
+}
+
+static int layer_impl(qwattn_ctx* c, const char* fn, void* stream, int slot, const void* qg, const void* k,
+                      const void* v, int in_dtype, const float* qn, const float* kn, float* out, int pos, int n,
+                      int n_split, const uint32_t* kbits, int kb_words) {
     if (!c) return QWATTN_EINVAL;
     if (slot < 0 || slot >= (int)c->kc.size())
-        return fail(c, QWATTN_ESTATE, "qwattn_layer_attention: slot %d of %d allocated K/V caches", slot, (int)c->kc.size());
+        return fail(c, QWATTN_ESTATE, "%s: slot %d of %d allocated K/V caches", fn, slot, (int)c->kc.size());
     const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
     int rc, used = 0;
     if (n * G <= 32 && n <= 8)  // decode / verify: one launch (norm + rope + append + split attend + combine)
-        return qwattn_decode(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
-                             pos, n, n_split, &used);
+        return decode_impl(c, fn, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
+                           pos, n, n_split, kbits, kb_words, &used);
     if (n * G <= 32) {  // more than 8 tokens in small groups: norm + rope + append, split attend, combine
         rc = qwattn_qk_norm_rope_append(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot],
                                         c->kv_cap, c->q32, QWATTN_F32, pos, n);
         if (rc) return rc;
-        rc = qwattn_attend_partial(c, stream, c->q32, c->kc[slot], c->vc[slot], c->kv_cap, pos, n, n_split, &used);
+        rc = attend_partial_impl(c, fn, stream, c->q32, c->kc[slot], c->vc[slot], c->kv_cap, pos, n, n_split, kbits,
+                                 kb_words, &used);
         if (rc) return rc;
         return qwattn_combine(c, stream, qg, in_dtype, out, n, used);
     }
-    return qwattn_prefill(c, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
-                          pos, n);
+    return prefill_impl(c, fn, stream, qg, k, v, in_dtype, qn, kn, c->rope, c->kc[slot], c->vc[slot], c->kv_cap, out,
+                        pos, n, kbits, kb_words);
+}
+
+int qwattn_layer_attention(qwattn_ctx* c, void* stream, int slot, const void* qg, const void* k, const void* v,
+                           int in_dtype, const float* qn, const float* kn, float* out, int pos, int n, int n_split) {
+    return layer_impl(c, "qwattn_layer_attention", stream, slot, qg, k, v, in_dtype, qn, kn, out, pos, n, n_split,
+                      nullptr, 0);
+}
+
+int qwattn_layer_attention_qsa(qwattn_ctx* c, void* stream, int slot, const void* qg, const void* k, const void* v,
+                               int in_dtype, const float* qn, const float* kn, float* out, int pos, int n, int n_split,
+                               const uint32_t* key_bits, int kb_words) {
+    if (c && !key_bits) return fail(c, QWATTN_EINVAL, "qwattn_layer_attention_qsa: null key_bits");
+    return layer_impl(c, "qwattn_layer_attention_qsa", stream, slot, qg, k, v, in_dtype, qn, kn, out, pos, n, n_split,
+                      key_bits, kb_words);
 }
 
 // ---- the decode without allocation ------------------------------------------------------------------

@@ -262,3 +262,131 @@ def test_qsa_indexer_then_decode(qw, oracle):
     # and it is not the dense result: the selection matters
     dense = oracle.attention(rq, kr, vr, pos, qg_h)
     assert np.abs(ref - dense).max() > 1e-2
+
+
+# ---- block-sparse prefill ----------------------------------------------------------------------------------
+
+from test_gpu_kernels import capacity, empty_caches, gpu_caches  # noqa: E402
+from common import cache_rows, projections  # noqa: E402
+
+# (shape, pos, n, dtype, cr, density, path): "prefill" = qwattn_prefill_qsa (the in-kernel query norm where
+# the rope width allows, else the fp16 query buffer), "attend_f32" = norm/rope/append to fp32 queries, then
+# qwattn_attend_prefill_qsa
+QSA_PF = [
+    (QWEN3_NEXT, 1000, 600, "bf16", 4, 0.2, "prefill"),     # paired schedule, keys of 4 over 64-key tiles
+    (QWEN3_NEXT, 2048, 2048, "bf16", 64, 0.1, "prefill"),   # the prefill benchmark's shape, whole-tile blocks
+    (QWEN3_NEXT, 300, 257, "f32", 3, 0.3, "attend_f32"),    # split schedule, a ratio dividing no tile
+    (TINY, 500, 100, "f32", 4, 0.25, "prefill"),            # rope_dim 16: the fp16 query-buffer path
+    (D128, 700, 333, "bf16", 8, 0.15, "prefill"),           # D = 128
+    (QWEN3_NEXT, 100, 64, "f32", 4, 0.0, "prefill"),        # nothing selected: tails only
+]
+
+
+@pytest.mark.parametrize("s,pos,n,dt,cr,density,path", QSA_PF, ids=lambda v: repr(v))
+def test_prefill_qsa_parity(qw, oracle, s, pos, n, dt, cr, density, path):
+    import oracle as orc
+    print(f"qsa prefill {s} pos={pos} n={n} {dt} cr={cr} d={density} {path}", flush=True)
+    rows = pos + n
+    cap = capacity(rows)
+    k16, v16 = cache_rows(70 + pos, pos, s) if pos else (np.zeros((0, s.NKV, s.D), np.float16),) * 2
+    qg, k, v, qn, kn = projections(71 + n, n, s)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    qg_d, k_d, v_d = dev(qg).to(tdt), dev(k).to(tdt), dev(v).to(tdt)
+    ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=max(n, 1))
+    kc, vc = gpu_caches(qw, k16, v16, cap) if pos else empty_caches(s, cap)
+    mask = _rand_mask(pos + n + cr, pos, n, cr, density)
+    kbits = dev(orc.qsa_key_bits(mask, pos, n, cr).view(np.int32))
+    rope = ctx.rope_table() if s.R else None
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    if path == "prefill":
+        ctx.prefill_qsa(qg_d, k_d, v_d, dev(qn), dev(kn), rope, kc, vc, cap, out, pos, n, kbits)
+    else:
+        q = torch.zeros((n, s.NH, s.D), device=DEV)
+        ctx.qk_norm_rope_append(qg_d, k_d, v_d, dev(qn), dev(kn), rope, kc, vc, cap, q, pos, n)
+        ctx.attend_prefill_qsa(q, kc, vc, cap, qg_d, out, pos, n, kbits)
+    ctx.sync_status()
+    rq, _, _ = oracle.qk_norm_rope(host(qg_d), host(k_d), host(v_d), 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
+    kcache = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
+    vcache = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
+    qg_h, out = host(qg_d), host(out)
+    toks = np.arange(n) if n <= 120 else np.unique(np.r_[0, 1, np.linspace(0, n - 1, 40).astype(int), n - 1])
+    for t in toks:
+        ref = oracle.attention_qsa(rq[t:t + 1], kcache, vcache, pos + t, mask[t:t + 1], cr, qg_h[t:t + 1])
+        assert_parity(out[t:t + 1], ref, f"qsa prefill {s} pos={pos} n={n} token {t}")
+
+
+def test_prefill_qsa_all_visible_equals_dense(qw):
+    s, pos, n = QWEN3_NEXT, 1500, 700
+    cap = capacity(pos + n)
+    k16, v16 = cache_rows(81, pos, s)
+    qg, k, v, qn, kn = projections(82, n, s)
+    qg_d, k_d, v_d = dev(qg).bfloat16(), dev(k).bfloat16(), dev(v).bfloat16()
+    ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=n)
+    kc, vc = gpu_caches(qw, k16, v16, cap)
+    kc2, vc2 = kc.clone(), vc.clone()
+    kbits = torch.full((n, (pos + n + 31) // 32), -1, dtype=torch.int32, device=DEV)
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    out2 = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    ctx.prefill(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc, vc, cap, out, pos, n)
+    ctx.prefill_qsa(qg_d, k_d, v_d, dev(qn), dev(kn), ctx.rope_table(), kc2, vc2, cap, out2, pos, n, kbits)
+    ctx.sync_status()
+    assert torch.equal(out, out2)
+
+
+def test_layer_attention_qsa(qw, oracle):
+    """qwattn_layer_attention_qsa over a prefill chunk, a 4-token verify pass and a decode step of one layer
+    slot, each with its own key bits, against the oracle's masked attention on the cache it built."""
+    import oracle as orc
+    s, cr = QWEN3_NEXT, 8
+    ctx = make_ctx(qw, s, max_ctx=4096, max_tokens=1024)
+    ctx.kv_alloc(1, 4096)
+    kc, vc, cap = ctx.kv_slot(0)
+    pos = 0
+    for step, n in enumerate([700, 4, 1]):
+        qg, k, v, qn, kn = projections(90 + step, n, s)
+        mask = _rand_mask(91 + step, pos, n, cr, 0.3)
+        kbits = dev(orc.qsa_key_bits(mask, pos, n, cr).view(np.int32))
+        out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+        ctx.layer_attention_qsa(0, dev(qg), dev(k), dev(v), dev(qn), dev(kn), out, pos, n, kbits)
+        ctx.sync_status()
+        rq, _, _ = oracle.qk_norm_rope(qg, k, v, 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
+        kcache = host(qw.k_rows(kc, cap, s.NKV, s.D)[:pos + n])
+        vcache = host(qw.v_rows(vc, cap, s.NKV, s.D)[:pos + n])
+        o = host(out)
+        for t in ([0, 1, 350, n - 1] if n > 4 else range(n)):
+            ref = oracle.attention_qsa(rq[t:t + 1], kcache, vcache, pos + t, mask[t:t + 1], cr, qg[t:t + 1])
+            assert_parity(o[t:t + 1], ref, f"layer qsa step {step} token {t}")
+        pos += n
+
+
+@pytest.mark.parametrize("s,pos,n,cr,kind", [(TINY, 500, 2, 4, "decode"), (QWEN3_NEXT, 3000, 4, 4, "decode"),
+                                              (QWEN3_NEXT, 1000, 300, 8, "prefill")], ids=repr)
+def test_qsa_token_hidden_from_leading_tiles(qw, oracle, s, pos, n, cr, kind):
+    """Token 0 selects only blocks near its end while every other token selects all: in the leading tiles
+    token 0's rows see no key while the others' maxima grow (their rescale must leave token 0's empty
+    accumulator finite). Loader-wave decode (G = 4, two tokens), 16-row-slice verify, and the prefill."""
+    import oracle as orc
+    rows = pos + n
+    nmax = rows // cr
+    mw = nmax // 32 + 1
+    mask = np.full((n, mw), 0xFFFFFFFF, np.uint32)
+    bits = np.zeros(mw * 32, bool)
+    bits[max(0, nmax - 3):nmax] = True
+    mask[0] = (bits.reshape(mw, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)).sum(axis=1).astype(np.uint32)
+    kbits = dev(orc.qsa_key_bits(mask, pos, n, cr).view(np.int32))
+    cap, k16, v16, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 950 + n)
+    ctx = make_ctx(qw, s, max_ctx=cap, max_tokens=max(n, 64))
+    out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
+    if kind == "decode":
+        ctx.decode_qsa(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, 0, kbits)
+    else:
+        ctx.prefill_qsa(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, kbits)
+    ctx.sync_status()
+    qg_h = host(qg_d)
+    rq, _, _ = oracle.qk_norm_rope(qg_h, host(k_d), host(v_d), 1 + host(qn_d), 1 + host(kn_d), pos, s.R, s.theta, s.eps)
+    kr = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
+    vr = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
+    o = host(out)
+    for t in sorted({0, 1, n - 1}):
+        ref = oracle.attention_qsa(rq[t:t + 1], kr, vr, pos + t, mask[t:t + 1], cr, qg_h[t:t + 1])
+        assert_parity(o[t:t + 1], ref, f"{kind} token {t}")
