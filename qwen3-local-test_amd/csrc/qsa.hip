@@ -27,7 +27,7 @@ namespace qw {
 namespace {
 
 constexpr int kQsaThreads = 1024;
-constexpr int kQsaChunk = 512;        // blocks scored per workgroup
+constexpr int kQsaChunk = 128;        // blocks scored per workgroup
 constexpr int kQsaKeysLds = 12288;    // scores staged in LDS for the select (more: read from memory)
 constexpr int kQsaMaskLds = 4608;     // mask words staged in LDS (>= (262144 / 2 + 1 + 31) / 32)
 
@@ -45,6 +45,18 @@ __device__ __forceinline__ float wave_sum(float x) {
     x = sum32(x);
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
+// Integer sum over the wave, in every lane (DPP within 16-lane rows, then permlane16 and permlane32 swaps).
+__device__ __forceinline__ unsigned wave_isum(unsigned x) {
+    x += (unsigned)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);
+    x += (unsigned)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);
+    x += (unsigned)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xF, 0xF, false);
+    x += (unsigned)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xF, 0xF, false);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = s16[0] + s16[1];
+    const auto s32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return s32[0] + s32[1];
 }
 
 __device__ __forceinline__ unsigned wave_min(unsigned x) {
@@ -81,9 +93,15 @@ __device__ __forceinline__ void rope_row(const float* x, float* y, const float* 
 // block of each following key by counting.
 __device__ __forceinline__ unsigned key_word(const unsigned* m, int w, int cr, int nblk) {
     int blk = (32 * w) / cr, r = 32 * w - blk * cr;
+    // the 32 keys lie in at most 32 consecutive blocks: two mask words, read once (only words that hold
+    // complete blocks are read)
+    const int w0 = blk >> 5, nmw = (nblk + 31) >> 5;
+    const unsigned m0 = w0 < nmw ? m[w0] : 0u, m1 = w0 + 1 < nmw ? m[w0 + 1] : 0u;
     unsigned bits = 0u;
+#pragma unroll
     for (int i = 0; i < 32; i++) {
-        const bool vis = blk >= nblk || ((m[blk >> 5] >> (blk & 31)) & 1u);
+        const unsigned mw = (blk >> 5) == w0 ? m0 : m1;
+        const bool vis = blk >= nblk || ((mw >> (blk & 31)) & 1u);
         bits |= (unsigned)vis << i;
         if (++r == cr) r = 0, blk++;
     }
@@ -144,7 +162,218 @@ __global__ __launch_bounds__(64) void k_qsa_pool(QsaPoolArgs a) {
 }
 
 // ---- selection -------------------------------------------------------------------------------------------
-// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [512 c, 512 c + 512) of token t; the last of
+// The exact top-`top` of token t's nblk block scores (by score, then the lower block id: the scores are >= +0,
+// so their bit patterns order like the values), by the last workgroup to arrive; writes the token's mask
+// row and key bits. STAGED: the scores fit kQsaKeysLds and are read once into LDS, else from memory on each
+// use (device-coherent loads).
+template <bool STAGED>
+__device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
+                                              unsigned* s_key, unsigned* s_mask, int* s_misc, int* s_scan,
+                                              unsigned* s_priv) {
+    constexpr int KPT = (kQsaKeysLds + kQsaThreads - 1) / kQsaThreads;  // staged keys a thread, at most
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    auto key = [&](int b) -> unsigned {
+        if constexpr (STAGED) return s_key[b];
+        else return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
+    };
+    unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
+    if constexpr (STAGED) {
+        unsigned kr[KPT];
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {  // every load issued before any is used
+            const int b = tid + i * kQsaThreads;
+            kr[i] = b < nblk ? __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice) : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+            const int b = tid + i * kQsaThreads;
+            if (b < nblk) s_key[b] = kr[i], kmin = min(kmin, kr[i]), kmax = max(kmax, kr[i]);
+        }
+    } else {
+        for (int b = tid; b < nblk; b += kQsaThreads) {
+            const unsigned k = key(b);
+            kmin = min(kmin, k), kmax = max(kmax, k);
+        }
+    }
+    __syncthreads();
+    const int nmw = (nblk + 31) >> 5;  // mask words holding complete blocks
+
+    if (STAGED && nblk <= kQsaThreads) {
+        // one key a thread: its rank among all keys (ahead of it: larger, or equal with a lower id), from
+        // broadcast LDS reads; selected when the rank is below `top`
+        const unsigned k = tid < nblk ? s_key[tid] : 0u;
+        int rank = 0;
+        const int n4 = nblk & ~3;
+        for (int b = 0; b < n4; b += 4) {
+            const uint4 q = *reinterpret_cast<const uint4*>(&s_key[b]);
+            rank += (q.x > k || (q.x == k && b < tid)) + (q.y > k || (q.y == k && b + 1 < tid)) +
+                    (q.z > k || (q.z == k && b + 2 < tid)) + (q.w > k || (q.w == k && b + 3 < tid));
+        }
+        for (int b = n4; b < nblk; b++) rank += s_key[b] > k || (s_key[b] == k && b < tid);
+        const unsigned long long sel = __ballot(tid < nblk && rank < a.top);
+        if (lane == 0) {
+            if (2 * wave < nmw) s_mask[2 * wave] = (unsigned)sel;
+            if (2 * wave + 1 < nmw) s_mask[2 * wave + 1] = (unsigned)(sel >> 32);
+        }
+    } else {
+        kmin = wave_min(kmin), kmax = wave_max(kmax);
+        if (lane == 0) s_scan[wave] = (int)kmin, s_scan[16 + wave] = (int)kmax;
+        __syncthreads();
+        if (wave == 0) {  // over the 16 waves: one read a lane, then the wave reductions
+            const unsigned m0 = lane < 16 ? (unsigned)s_scan[lane] : 0xFFFFFFFFu;
+            const unsigned m1 = lane < 16 ? (unsigned)s_scan[16 + lane] : 0u;
+            const unsigned mn = wave_min(m0), mx = wave_max(m1);
+            if (lane == 0) s_misc[3] = (int)mn, s_misc[4] = (int)mx;
+        }
+        __syncthreads();
+        kmin = (unsigned)s_misc[3], kmax = (unsigned)s_misc[4];
+        // the bits above the highest one where the smallest and largest keys differ are every key's: the
+        // radix passes (4 bits each, from the top) start at the digit holding that bit
+        const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
+        const int shift0 = hb < 0 ? -4 : (hb & ~3);
+        unsigned pmask = hb < 0 ? 0xFFFFFFFFu : (shift0 + 4 >= 32 ? 0u : ~0u << (shift0 + 4));
+        unsigned prefix = kmin & pmask;
+        int need = a.top;  // keys still to take at or below the current prefix
+        for (int shift = shift0; shift >= 0; shift -= 4) {
+            // each thread counts the 16 digits of its matching keys: staged, at most KPT = 12 keys a thread,
+            // in 4-bit counters of one 64-bit register (a key adds 1 << 4 d); else in four registers of 8-bit
+            // counters (a key adds 1 << 8 (d % 4) to word d / 4; at most 144 keys a thread). The counters are
+            // widened to 16-bit pairs and summed over the wave (DPP), then over the waves through LDS
+            unsigned cw[4] = {0u, 0u, 0u, 0u};
+            if constexpr (STAGED) {
+                static_assert(KPT < 16, "4-bit counters");
+                unsigned kr[KPT];
+#pragma unroll
+                for (int i = 0; i < KPT; i++) kr[i] = tid + i * kQsaThreads < nblk ? s_key[tid + i * kQsaThreads] : 0u;
+                unsigned long long c64 = 0ull;
+#pragma unroll
+                for (int i = 0; i < KPT; i++) {
+                    const unsigned k = kr[i];
+                    const bool m = tid + i * kQsaThreads < nblk && (k & pmask) == prefix;
+                    c64 += m ? 1ull << (4 * ((k >> shift) & 15u)) : 0ull;
+                }
+                // nibble d of c64 -> byte d % 4 of word d / 4
+                const unsigned lo = (unsigned)c64, hi = (unsigned)(c64 >> 32);
+                cw[0] = (lo & 0xFu) | ((lo >> 4) & 0xFu) << 8 | ((lo >> 8) & 0xFu) << 16 | ((lo >> 12) & 0xFu) << 24;
+                cw[1] = ((lo >> 16) & 0xFu) | ((lo >> 20) & 0xFu) << 8 | ((lo >> 24) & 0xFu) << 16 | (lo >> 28) << 24;
+                cw[2] = (hi & 0xFu) | ((hi >> 4) & 0xFu) << 8 | ((hi >> 8) & 0xFu) << 16 | ((hi >> 12) & 0xFu) << 24;
+                cw[3] = ((hi >> 16) & 0xFu) | ((hi >> 20) & 0xFu) << 8 | ((hi >> 24) & 0xFu) << 16 | (hi >> 28) << 24;
+            } else {
+                for (int b = tid; b < nblk; b += kQsaThreads) {
+                    const unsigned k = key(b);
+                    const unsigned d = (k >> shift) & 15u;
+                    const unsigned inc = (k & pmask) == prefix ? 1u << (8 * (d & 3u)) : 0u;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) cw[q] += (d >> 2) == (unsigned)q ? inc : 0u;
+                }
+            }
+            // counts of the pass in their own LDS words (this pass's parity): the previous pass's may
+            // still be read by a wave deciding its digit
+            unsigned* sp = s_priv + (shift & 4 ? 128 : 0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                // digits 4q, 4q + 2 in the low and high halves of one word; 4q + 1, 4q + 3 in another
+                const unsigned ev = wave_isum(cw[q] & 0x00FF00FFu), od = wave_isum((cw[q] >> 8) & 0x00FF00FFu);
+                if (lane == 0) sp[wave * 8 + 2 * q] = ev, sp[wave * 8 + 2 * q + 1] = od;
+            }
+            __syncthreads();
+            // every wave decides the digit itself (the same sums in the same order): no second barrier. Lane l
+            // takes digit d = 15 - l % 16 of the waves 4 (l / 16) .. + 3 (four reads), the four row groups are
+            // summed by permlane swaps, so each lane holds the total of its digit; an inclusive scan over each
+            // 16-lane row (DPP row_shr) then counts the keys whose digit is at least 15 - l % 16
+            const int d = 15 - (lane & 15), g4 = 4 * (lane >> 4);
+            const int word = 2 * (d >> 2) + (d & 1), sh = 16 * ((d >> 1) & 1);
+            unsigned cnt = 0u;
+#pragma unroll
+            for (int w = 0; w < 4; w++) cnt += (sp[(g4 + w) * 8 + word] >> sh) & 0xFFFFu;
+            const auto s16 = __builtin_amdgcn_permlane16_swap(cnt, cnt, false, false);
+            cnt = s16[0] + s16[1];
+            const auto s32 = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
+            cnt = s32[0] + s32[1];
+            const int cntd = (int)cnt;
+            int inc = cntd;
+            inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xF, 0xF, false);  // row_shr:1
+            inc += __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xF, 0xF, false);  // row_shr:2
+            inc += __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xF, 0xF, false);  // row_shr:4
+            inc += __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xF, 0xF, false);  // row_shr:8
+            const unsigned long long hit = __ballot(lane < 16 && inc >= need);
+            const int l0 = hit ? __builtin_ctzll(hit) : 15;  // the keys matching the prefix reach `need`
+            const int above = __builtin_amdgcn_readlane(inc - cntd, l0);
+            prefix |= (unsigned)(15 - l0) << shift;
+            pmask |= 15u << shift;
+            need -= above;
+        }
+        // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
+        // block order). Thread tid owns the blocks [tid * per, tid * per + per): 8 (four threads a mask word,
+        // combined by DPP) when they cover nblk, else a multiple of 32.
+        const int per = nblk <= 8 * kQsaThreads ? 8 : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
+        const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
+        int eq = 0;
+        if (per == 8) {
+            unsigned kr[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) kr[i] = lo + i < hi ? key(lo + i) : 0u;
+#pragma unroll
+            for (int i = 0; i < 8; i++) eq += lo + i < hi && kr[i] == prefix;
+        } else {
+            for (int b = lo; b < hi; b++) eq += key(b) == prefix;
+        }
+        // exclusive prefix of the equal counts over the threads: within the wave, then the earlier waves'
+        // totals (one read a lane and a wave sum)
+        int inc = eq;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += u;
+        }
+        if (lane == 63) s_scan[32 + wave] = inc;
+        __syncthreads();
+        const int base = (int)wave_isum(lane < wave ? (unsigned)s_scan[32 + lane] : 0u);
+        int taken = base + inc - eq;
+        if (per == 8) {
+            unsigned bits = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (lo + i < hi) {
+                    const unsigned k = key(lo + i);
+                    bool sel = k > prefix;
+                    if (k == prefix) sel = taken++ < need;
+                    bits |= (unsigned)sel << i;
+                }
+            }
+            // the word of blocks [32 (tid / 4), + 32): the four threads' bytes OR-ed across the quad
+            unsigned wv = bits << (8 * (tid & 3));
+            wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);
+            wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);
+            if ((tid & 3) == 0 && (tid >> 2) < nmw) s_mask[tid >> 2] = wv;
+        } else {
+            // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
+            for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
+                unsigned bits = 0u;
+                for (int i = 0; i < 32; i++) {
+                    const int b = 32 * w + i;
+                    if (b < hi) {
+                        const unsigned k = key(b);
+                        bool sel = k > prefix;
+                        if (k == prefix) sel = taken++ < need;
+                        bits |= (unsigned)sel << i;
+                    }
+                }
+                s_mask[w] = bits;
+            }
+        }
+    }
+    __syncthreads();
+    const int kb_words = a.kb_words;
+    if (a.mask)
+        for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = w < nmw ? s_mask[w] : 0u;
+    if (a.kbits)
+        for (int w = tid; w < kb_words; w += kQsaThreads)
+            a.kbits[(size_t)t * kb_words + w] = key_word(s_mask, w, a.CR, nblk);
+}
+
+
+// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [128 c, 128 c + 128) of token t; the last of
 // the token's workgroups to arrive selects. A token that selects nothing has its rows written by workgroup
 // (0, t).
 template <int IN_DT>
@@ -154,11 +383,11 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     unsigned* s_mask = s_key + kQsaKeysLds;                 // [kQsaMaskLds] the token's selection
     int* s_misc = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [16]
     int* s_tot = s_misc + 16;                               // [16] digit counts of a pass
-    int* s_scan = s_tot + 16;                               // [kQsaThreads / 64] per-wave sums
-    unsigned char* work = reinterpret_cast<unsigned char*>(s_scan + kQsaThreads / 64);
+    int* s_scan = s_tot + 16;                               // [48]: per-wave minima, maxima, sums
+    unsigned char* work = reinterpret_cast<unsigned char*>(s_scan + 48);
     float* s_q = reinterpret_cast<float*>(work);            // scoring: [IH][ID] normed, rotated query heads
     float* s_t = s_q + a.IH * a.ID;                         // scoring: [IH][ID] the normed heads before rotation
-    unsigned* s_priv = reinterpret_cast<unsigned*>(work);   // select: [16 digits][kQsaThreads] private counts
+    unsigned* s_priv = reinterpret_cast<unsigned*>(work);   // select: [2 passes][waves][8] packed digit counts
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x, t = blockIdx.y;
@@ -243,111 +472,8 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     if (s_misc[0] != ct - 1) return;
 
     // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
-    const bool staged = nblk <= kQsaKeysLds;
-    unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
-    for (int b = tid; b < nblk; b += kQsaThreads) {
-        const unsigned k = __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
-        if (staged) s_key[b] = k;
-        kmin = min(kmin, k), kmax = max(kmax, k);
-    }
-    auto key = [&](int b) -> unsigned { return staged ? s_key[b] : __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice); };
-    kmin = wave_min(kmin), kmax = wave_max(kmax);
-    if (lane == 0) s_scan[wave] = (int)kmin;
-    __syncthreads();
-    if (tid == 0) {
-        unsigned m = 0xFFFFFFFFu;
-        for (int w = 0; w < kQsaThreads / 64; w++) m = min(m, (unsigned)s_scan[w]);
-        s_misc[3] = (int)m;
-    }
-    __syncthreads();
-    if (lane == 0) s_scan[wave] = (int)kmax;
-    __syncthreads();
-    if (tid == 0) {
-        unsigned m = 0u;
-        for (int w = 0; w < kQsaThreads / 64; w++) m = max(m, (unsigned)s_scan[w]);
-        s_misc[4] = (int)m;
-    }
-    __syncthreads();
-    kmin = (unsigned)s_misc[3], kmax = (unsigned)s_misc[4];
-    // the bits above the highest one where the smallest and largest keys differ are every key's: the radix
-    // passes (4 bits each, from the top) start at the digit holding that bit
-    const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
-    const int shift0 = hb < 0 ? -4 : (hb & ~3);
-    unsigned pmask = hb < 0 ? 0xFFFFFFFFu : (shift0 + 4 >= 32 ? 0u : ~0u << (shift0 + 4));
-    unsigned prefix = kmin & pmask;
-    int need = a.top;  // keys still to take at or below the current prefix
-    for (int shift = shift0; shift >= 0; shift -= 4) {
-        // each thread counts into its own 16 bins (one uncontended LDS add a key), one digit summed per wave
-#pragma unroll
-        for (int i = 0; i < 16; i++) s_priv[i * kQsaThreads + tid] = 0u;
-        for (int b = tid; b < nblk; b += kQsaThreads) {
-            const unsigned k = key(b);
-            if ((k & pmask) == prefix) s_priv[((k >> shift) & 15u) * kQsaThreads + tid] += 1u;
-        }
-        __syncthreads();
-        if (wave < 16) {
-            unsigned v = 0u;
-            for (int i = lane; i < kQsaThreads; i += 64) v += s_priv[wave * kQsaThreads + i];
-            v = (unsigned)wave_sum((float)v);  // at most 147,456: exact in fp32
-            if (lane == 0) s_tot[wave] = (int)v;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int above = 0, d = 0;
-            for (int i = 15; i >= 0; i--) {
-                if (above + s_tot[i] >= need) {
-                    d = i;
-                    break;
-                }
-                above += s_tot[i];
-            }
-            s_misc[1] = d;
-            s_misc[2] = above;
-        }
-        __syncthreads();
-        prefix |= (unsigned)s_misc[1] << shift;
-        pmask |= 15u << shift;
-        need -= s_misc[2];
-    }
-    // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
-    // block order). Thread tid owns the blocks [tid * per, tid * per + per), per a multiple of 32.
-    const int per = ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
-    const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
-    int eq = 0;
-    for (int b = lo; b < hi; b++) eq += key(b) == prefix;
-    // exclusive prefix of the equal counts over the threads: within the wave (shuffles), then the waves
-    int inc = eq;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += u;
-    }
-    if (lane == 63) s_scan[wave] = inc;
-    __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wave; w++) base += s_scan[w];
-    int taken = base + inc - eq;
-    const int nmw = (nblk + 31) >> 5;  // mask words holding complete blocks
-    // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
-    for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
-        unsigned bits = 0u;
-        for (int i = 0; i < 32; i++) {
-            const int b = 32 * w + i;
-            if (b < hi) {
-                const unsigned k = key(b);
-                bool sel = k > prefix;
-                if (k == prefix) sel = taken++ < need;
-                bits |= (unsigned)sel << i;
-            }
-        }
-        s_mask[w] = bits;
-    }
-    __syncthreads();
-    if (a.mask)
-        for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = w < nmw ? s_mask[w] : 0u;
-    if (a.kbits)
-        for (int w = tid; w < kb_words; w += kQsaThreads)
-            a.kbits[(size_t)t * kb_words + w] = key_word(s_mask, w, a.CR, nblk);
+    if (nblk <= kQsaKeysLds) select_blocks<true>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_priv);
+    else select_blocks<false>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_priv);
 }
 
 // ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
@@ -358,8 +484,8 @@ __global__ __launch_bounds__(256) void k_qsa_key_bits(QsaKeyBitsArgs a) {
 }
 
 size_t qsa_select_lds(int IH, int ID) {
-    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)16 * kQsaThreads * 4);
-    return (size_t)(kQsaKeysLds + kQsaMaskLds + 32 + kQsaThreads / 64) * 4 + work;
+    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)2 * 8 * (kQsaThreads / 64) * 4);
+    return (size_t)(kQsaKeysLds + kQsaMaskLds + 32 + 48) * 4 + work;
 }
 
 int qsa_mask_lds_words() { return kQsaMaskLds; }
