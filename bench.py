@@ -19,6 +19,11 @@ duration from HIP events around batches of 16 back-to-back launches on the strea
 HBM traffic per launch from the committed rocprofv3 PMC summary in profiles/), and the CPU baseline:
 the reference's CPU attention timed on this host's cores over a bounded sample.
 
+Two QSA workloads (the block-sparse path past the indexer's budget, src/qwen4_vk.cpp:942-984) time the whole
+layer step on the GPU at 32K: pool the new indexer key, select the token's blocks (4 indexer heads of 128
+dims, a budget of 2,048 keys, blocks of 4 or 64 keys), and the one-launch decode over the tiles the
+selection leaves visible; their bytes are the K/V bytes of the visible keys.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
@@ -151,10 +156,11 @@ class QsaWorkload(Workload):
     GPU: pool the new token's indexer key, select its blocks, then the one-launch decode over the keys the
     selection leaves visible. Indexer: IH heads of ID dims, blocks of CR keys, a budget of BUDGET keys;
     every layer slot has its own raw and pooled key arrays, built once over the cached history."""
-    IH, ID, CR, BUDGET = 4, 128, 4, 2048
+    IH, ID, BUDGET = 4, 128, 2048
 
-    def __init__(self, qw, name, pos, n, slots, seed=0):
+    def __init__(self, qw, name, pos, n, slots, cr, seed=0):
         import torch
+        self.CR = cr
         super().__init__(qw, name, pos, n, slots, 0, "f32", 0.0, seed)
         g = torch.Generator(device="cuda")
         g.manual_seed(seed + 1000)
@@ -443,7 +449,9 @@ def main():
         ("decode_256k_1024splits", 262144, 1, 2, 1024, "f32", 0.01),
         ("decode_256k", 262144, 1, 2, 0, "f32", 0.01),
         ("prefill_2k_on_2k", 2048, 2048, 8, 0, "bf16", 0.0),
-        ("decode_32k_qsa", 32768, 1, args.slots, 0, "f32", 0.0),
+        # QSA layer steps (indexer + masked decode); the last field is the block size (compress ratio)
+        ("decode_32k_qsa_cr4", 32768, 1, args.slots, 0, "f32", 4),
+        ("decode_32k_qsa_cr64", 32768, 1, args.slots, 0, "f32", 64),
     ]
     results = {}
     for name, pos, n, slots, n_split, dt, heavy in configs:
@@ -451,15 +459,15 @@ def main():
             continue
         print(f"[bench] {name}: pos={pos} n={n} slots={slots} splits={n_split or 'auto'}", file=sys.stderr,
               flush=True)
-        if name.endswith("_qsa"):
-            wl = QsaWorkload(qw, name, pos, n, slots, seed=len(results))
+        if "_qsa" in name:
+            wl = QsaWorkload(qw, name, pos, n, slots, int(heavy), seed=len(results))
         else:
             wl = Workload(qw, name, pos, n, slots, n_split, dt, heavy, seed=len(results))
         r = run_workload(wl, args.steps, args.warmup, graph)
         wl.close()
         del wl
         torch.cuda.empty_cache()
-        if name.endswith("_qsa"):
+        if "_qsa" in name:
             # the K/V bytes of the keys the selection leaves visible (each fp16 row once)
             byts = 2 * r["visible_keys"] * NKV * D * 2
             r["value"] = byts / (r["us_per_step"] * 1e-6) / 1e9
@@ -483,7 +491,7 @@ def main():
             r["frac_mfma_step"] = fl / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
             r["frac_mfma_kernel"] = fl / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
             r["algorithmic_flops"] = fl
-        if n * (NH // NKV) <= 32 and not name.endswith("_qsa"):
+        if n * (NH // NKV) <= 32 and "_qsa" not in name:
             r["splits_requested"] = n_split or "auto"
         results[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)

@@ -425,12 +425,12 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     __syncthreads();
 
     // scores of this chunk: 16 lanes per pooled key, DL = ID / 16 consecutive dims a lane, 64 keys a round;
-    // the loads of four rounds are issued before any is used
+    // the loads of the chunk's rounds are issued before any is used
     const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
     const int bc0 = c * kQsaChunk, bc1 = min(nblk, bc0 + kQsaChunk);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
                                                                         a.stride * 4, 0x00020000);
-    constexpr int RB = 4, GPR = kQsaThreads / 16;  // rounds per batch, keys per round
+    constexpr int RB = kQsaChunk / (kQsaThreads / 16), GPR = kQsaThreads / 16;  // rounds per batch, keys per round
     for (int b0 = bc0; b0 < bc1; b0 += RB * GPR) {
         float kv[RB][16];
 #pragma unroll

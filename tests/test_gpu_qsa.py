@@ -66,6 +66,10 @@ CASES = {
     "odd": (QSA_ODD, 1024, [(0, 100, 1), (100, 1, 1), (101, 4, 1), (103, 2, 1), (105, 50, 1)], "f32"),
     # 131,000+ blocks: the scores no longer fit the select's LDS, and 40 tokens take two select launches
     "long_cr2": (QsaShape(1, 64, 2, 64, 64), 262144, [(0, 262000, 0), (262000, 40, 1)], "f32"),
+    # 8,192 blocks at 32K: the staged radix passes (more blocks than the select's threads)
+    "cr4_32k": (QsaShape(4, 128, 4, 2048, 64), 32776, [(0, 32768, 0), (32768, 1, 1), (32769, 4, 1)], "f32"),
+    # zero indexer queries: every score is 0, the lowest block ids win (staged radix and rank paths)
+    "zeros": (QsaShape(2, 128, 4, 256, 64), 8200, [(0, 8000, 0), (8000, 2, 1), (8002, 1, 1)], "f32"),
 }
 
 
@@ -75,6 +79,8 @@ def test_qsa_indexer_matches_oracle(qw, oracle, name):
     qs, max_ctx, calls, dt = CASES[name]
     tot = sum(c[1] for c in calls)
     iq, ik, qg, kg = qsa_inputs(41, tot, qs)
+    if name == "zeros":
+        iq[:] = 0.0
     if dt == "bf16":  # the oracle reads the same bf16-rounded values
         iq = torch.from_numpy(iq).bfloat16().float().numpy()
         ik = torch.from_numpy(ik).bfloat16().float().numpy()
