@@ -80,6 +80,26 @@ public:
               "qwattn_layer_attention");
     }
 
+    // A QSA layer past its budget (Qwen4Vulkan::attention with `masked`, src/qwen4_vk.cpp:942-984): cache
+    // and pool the pass's projected indexer keys, select each token's blocks into per-key visibility bits,
+    // and run the layer's attention over the visible keys. raw [max_ctx][idx_dim] and pooled
+    // [max_ctx/cr + 1][idx_dim] are the layer's indexer arrays; key_bits [n][kb_words], kb_words >=
+    // ceil((pos + n) / 32).
+    void qsa_layer_attention(void* stream, int slot, const void* qg, const void* k, const void* v, int in_dtype,
+                             const float* qn, const float* kn, const void* iq, const void* ik, int idx_dtype,
+                             const float* iq_gamma, const float* ik_gamma, int idx_heads, int idx_dim, int cr,
+                             int budget, float* raw, float* pooled, int cap, uint32_t* key_bits, int kb_words,
+                             float* out, int pos, int n, int n_split = 0) {
+        check(ctx_, qwattn_qsa_pool(ctx_, stream, ik, idx_dtype, ik_gamma, idx_dim, cr, raw, pooled, cap, pos, n),
+              "qwattn_qsa_pool");
+        check(ctx_, qwattn_qsa_select(ctx_, stream, iq, idx_dtype, iq_gamma, idx_heads, idx_dim, cr, budget, pooled,
+                                      pos, n, nullptr, 0, key_bits, kb_words),
+              "qwattn_qsa_select");
+        check(ctx_, qwattn_layer_attention_qsa(ctx_, stream, slot, qg, k, v, in_dtype, qn, kn, out, pos, n, n_split,
+                                               key_bits, kb_words),
+              "qwattn_layer_attention_qsa");
+    }
+
     // Waits for `stream` and throws if a bounded in-kernel wait of an earlier decode launch gave up.
     void sync(void* stream) { check(ctx_, qwattn_sync_status(ctx_, stream), "qwattn_sync_status"); }
 
