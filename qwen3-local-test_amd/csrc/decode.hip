@@ -222,7 +222,9 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
         const int z = z0 + lane;
         bool pend = lane < nz;                         // lane j: split z0 + j not arrived yet
         float mj = kNegInf, lj = 0.f;
-        fDL ov[GS];
+        fDL ov[GS];  // splits past S stay zero (weight 0 too), so the group sum needs no per-split guard
+#pragma unroll
+        for (int j = 0; j < GS; j++) ov[j] = fDL{};
         while (__ballot(pend) != 0) {
             const f32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(rrec, (pend ? z : 0) * 16, 0, kScDevice);
             const bool last = ++spins > a.spin_max;
@@ -247,14 +249,11 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
         }
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         // the group's max and weights: lane j < nz holds split z0 + j's (m, l)
+        // (DPP/permlane butterflies over the 32 lanes: no LDS round trips)
         const bool use = lane < nz && lj > 0.f;
-        float mg = use ? mj : kNegInf;
-#pragma unroll
-        for (int x = 1; x < 32; x <<= 1) mg = fmaxf(mg, __shfl_xor(mg, x, 64));
+        const float mg = max32(use ? mj : kNegInf);
         const float w = use ? exp2_fast(mj - mg) : 0.f;
-        float lg = lj * w;
-#pragma unroll
-        for (int x = 1; x < 32; x <<= 1) lg += __shfl_xor(lg, x, 64);
+        const float lg = sum32(lj * w);
         // the weights to every lane through LDS (broadcast reads): lane j < 32 holds split z0 + j's
         if (lane < GS) s_w[wave * GS + lane] = w;
         float wv[GS];
@@ -265,8 +264,7 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
         }
         fDL og = {};
 #pragma unroll
-        for (int j = 0; j < GS; j++)
-            if (j < nz) og += ov[j] * wv[j];  // splits past S hold nothing (their registers are never loaded)
+        for (int j = 0; j < GS; j++) og += ov[j] * wv[j];
         *reinterpret_cast<fDL*>(&s_go[wave * D + lane * DL]) = og;
         if (lane == 0) {
             s_gm[wave] = mg;
