@@ -101,6 +101,15 @@ __device__ __forceinline__ float sum32(float x) {
 }
 
 // Maximum over each 32-lane half of the wave, in every lane of the half (the butterfly of sum32).
+// Maximum over the four 16-lane rows of the wave for each lane position (lanes l, l ^ 16, l ^ 32, l ^ 48):
+// a row swap (permlane16_swap) then a half swap (permlane32_swap), no LDS round trip.
+__device__ __forceinline__ float max_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float max32(float x) {
     x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false)));
     x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false)));

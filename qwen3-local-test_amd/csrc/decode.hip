@@ -984,75 +984,8 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         for (int kk = 0; kk < NKS; kk++) qreg[kk] = *reinterpret_cast<const f16x8*>(s_q + (kk * 64 + lane) * 8);
         if constexpr (QSA) nvt = s_nvis;
         const int ntc = nvt > wave ? (nvt - wave + 1) / 2 : 0;
-        for (int i = 0; i < ntc; i++) {
-            const int t = wave + 2 * i;
-            for (int spin = 0; __hip_atomic_load(&ready[wave], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1;
-                 spin++) {
-                if (spin >= SPIN_MAX) {
-                    if (lane == 0) report_wait(a, kWaitRingCompute);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            const f16* sl = slot_of(t);
-            f16x8 kt[NKS][2], vt[NDT];
-#pragma unroll
-            for (int kk = 0; kk < NKS; kk++)
-#pragma unroll
-                for (int s2 = 0; s2 < 2; s2++) kt[kk][s2] = *reinterpret_cast<const f16x8*>(sl + ((kk * 2 + s2) * 64 + lane) * 8);
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) vt[dt] = *reinterpret_cast<const f16x8*>(sl + BLKE + (dt * 64 + lane) * 8);
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile is in registers, the slot is free
-            asm volatile("" ::: "memory");
-            __hip_atomic_store(&freed[wave], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-
-            const int tb = kBlk * blk_of(t);
-            if (tb + 32 > maxlen) {
-                // keys from maxlen on: their scores are masked, but V there is whatever the cache memory
-                // holds (P = 0 there, and 0 * NaN is not 0): zero it. V fragment dt: lane (c, g) holds
-                // keys 8 g .. 8 g + 7 of dim 16 dt + c, two keys per 32-bit word
-                const int nvk = min(max(maxlen - tb - 8 * g, 0), 8);
-                u32x4 keep;
-#pragma unroll
-                for (int w = 0; w < 4; w++) keep[w] = (2 * w < nvk ? 0xFFFFu : 0u) | (2 * w + 1 < nvk ? 0xFFFF0000u : 0u);
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++) vt[dt] = as_h8(as_u4(vt[dt]) & keep);
-            }
-            // scores: sc[s][i] is key tb + 8g + 4s + i of column c (fp16 hi in columns 0-7, lo in 8-15)
-            f32x4 sc[2];
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++) {
-                f32x4 x = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kk = 0; kk < NKS; kk++) x = mfma16(kt[kk][s2], qreg[kk], x);
-                sc[s2] = x;
-            }
-            // QSA: the column's token sees key tb + i when bit i of its word is set
-            const unsigned vis = QSA ? s_vw[t * 8 + utok] : 0xFFFFFFFFu;
-            float sv[8];
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float v = sc[s2][e] + xor8(sc[s2][e]);
-                    const int kq = 8 * g + 4 * s2 + e;
-                    sv[s2 * 4 + e] = tb + kq < lim && ((vis >> kq) & 1u) ? v : kNegInf;
-                }
-            float mx = sv[0];
-#pragma unroll
-            for (int k = 1; k < 8; k++) mx = fmaxf(mx, sv[k]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            // lazy rescale (see k_decode)
-            if (m_run == kNegInf) m_run = mx;
-            if (__builtin_amdgcn_ballot_w64(mx > m_run + TAU) != 0) {
-                const float m_new = fmaxf(m_run, mx);
-                const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);  // a column with no key yet: 1
-                m_run = m_new;
-                l_run *= corr;
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++) acc[dt] *= corr;
-            }
+        // P = exp2(s - m) and P V with the running max m (shared by the tile loop and the rescale path)
+        auto finish = [&](const float (&sv)[8], const f16x8 (&vt)[NDT]) {
             const float m_use = m_run == kNegInf ? 0.f : m_run;
             float psum = 0.f;
             f16x8 pop;
@@ -1066,6 +999,91 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             l_run += psum;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) acc[dt] = mfma16(vt[dt], pop, acc[dt]);
+        };
+        // The tiles run in an inner loop that leaves only when a tile's max passes the running max by more
+        // than TAU; the rescale (rare) happens outside it and the tile is finished there. With the rescale
+        // as a conditional block inside the tile loop, the compiler copies every accumulator register on
+        // every iteration.
+        int i = 0;
+        for (;;) {
+            bool resc = false;
+            float sv[8], mx = kNegInf;
+            f16x8 vt[NDT];
+            for (; i < ntc; i++) {
+                const int t = wave + 2 * i;
+                for (int spin = 0; __hip_atomic_load(&ready[wave], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < i + 1;
+                     spin++) {
+                    if (spin >= SPIN_MAX) {
+                        if (lane == 0) report_wait(a, kWaitRingCompute);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                const f16* sl = slot_of(t);
+                // K first: the scores start once it is in registers, and V is read behind them
+                f16x8 kt[NKS][2];
+#pragma unroll
+                for (int kk = 0; kk < NKS; kk++)
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; s2++) kt[kk][s2] = *reinterpret_cast<const f16x8*>(sl + ((kk * 2 + s2) * 64 + lane) * 8);
+                // scores: sc[s][i] is key tb + 8g + 4s + i of column c (fp16 hi in columns 0-7, lo in 8-15)
+                f32x4 sc[2];
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) {
+                    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < NKS; kk++) x = mfma16(kt[kk][s2], qreg[kk], x);
+                    sc[s2] = x;
+                }
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) vt[dt] = *reinterpret_cast<const f16x8*>(sl + BLKE + (dt * 64 + lane) * 8);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile is in registers, the slot is free
+                asm volatile("" ::: "memory");
+                __hip_atomic_store(&freed[wave], i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+
+                const int tb = kBlk * blk_of(t);
+                if (tb + 32 > maxlen) {
+                    // keys from maxlen on: their scores are masked, but V there is whatever the cache memory
+                    // holds (P = 0 there, and 0 * NaN is not 0): zero it. V fragment dt: lane (c, g) holds
+                    // keys 8 g .. 8 g + 7 of dim 16 dt + c, two keys per 32-bit word
+                    const int nvk = min(max(maxlen - tb - 8 * g, 0), 8);
+                    u32x4 keep;
+#pragma unroll
+                    for (int w = 0; w < 4; w++) keep[w] = (2 * w < nvk ? 0xFFFFu : 0u) | (2 * w + 1 < nvk ? 0xFFFF0000u : 0u);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; dt++) vt[dt] = as_h8(as_u4(vt[dt]) & keep);
+                }
+                // QSA: the column's token sees key tb + i when bit i of its word is set
+                const unsigned vis = QSA ? s_vw[t * 8 + utok] : 0xFFFFFFFFu;
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float v = sc[s2][e] + xor8(sc[s2][e]);
+                        const int kq = 8 * g + 4 * s2 + e;
+                        sv[s2 * 4 + e] = tb + kq < lim && ((vis >> kq) & 1u) ? v : kNegInf;
+                    }
+                mx = sv[0];
+#pragma unroll
+                for (int k = 1; k < 8; k++) mx = fmaxf(mx, sv[k]);
+                mx = max_rows(mx);  // over the column's four lane groups
+                // lazy rescale (see k_decode)
+                if (m_run == kNegInf) m_run = mx;
+                if (__builtin_amdgcn_ballot_w64(mx > m_run + TAU) != 0) {
+                    resc = true;
+                    break;
+                }
+                finish(sv, vt);
+            }
+            if (!resc) break;
+            const float m_new = fmaxf(m_run, mx);
+            const float corr = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);  // a column with no key yet: 1
+            m_run = m_new;
+            l_run *= corr;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) acc[dt] *= corr;
+            finish(sv, vt);
+            i++;
         }
         l_run += __shfl_xor(l_run, 16, 64);  // the column's sum over the lane groups
         l_run += __shfl_xor(l_run, 32, 64);
