@@ -1089,38 +1089,34 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
         l_run += __shfl_xor(l_run, 32, 64);
     }
 
-    // ---- merge the two compute waves: each hands the other the raw accumulators of the other's half of
-    // the dims (and its running max and sum) through LDS (the ring is dead once every wave is here), then
-    // merges its own half in registers, adds each query row's hi and lo columns and stores its half of the
-    // split's partial rows. Device-coherent stores (they reach the point every XCD reads from): the
-    // combining workgroups of the one-launch decode read them from other XCDs without any cache-wide
-    // write-back
-    constexpr int NDH = NDT / NCW;                // 16-dim fragments per compute wave
-    float* sO = reinterpret_cast<float*>(ring);   // [NCW][NDH][64 lanes][4]
-    float* sML = sO + NCW * NDH * 256;             // [NCW][16 columns][2]
+    // ---- merge: the compute waves put their raw accumulators and running (max, sum) in LDS (the ring is
+    // dead once every wave is here); then all four waves merge them, wave q taking fragments q NDQ ..
+    // q NDQ + NDQ - 1 of both, add each query row's hi and lo columns and store those dims of the split's
+    // partial rows (four waves: each does a quarter of the register arithmetic of the merge, which is the
+    // bulk of its time). Device-coherent stores (they reach the point every XCD reads from): the combining
+    // workgroups of the one-launch decode read them from other XCDs without any cache-wide write-back
+    constexpr int NDQ = NDT / 4;                  // 16-dim fragments merged per wave
+    float* sO = reinterpret_cast<float*>(ring);   // [NCW][NDT][64 lanes][4]
+    float* sML = sO + NCW * NDT * 256;             // [NCW][16 columns][2]
     __syncthreads();
-    // W: this compute wave (a compile-time constant, so every register index below is static)
-    auto hand_over = [&](auto W) {
-        constexpr int OT = 1 - decltype(W)::value;
+    if (!loader) {
 #pragma unroll
-        for (int j = 0; j < NDH; j++)  // the other wave's half, in lane order
-            *reinterpret_cast<f32x4*>(&sO[((OT * NDH + j) * 64 + lane) * 4]) = acc[OT * NDH + j];
-        if (g == 0) sML[(decltype(W)::value * 16 + c) * 2] = m_run, sML[(decltype(W)::value * 16 + c) * 2 + 1] = l_run;
-    };
-    if (wave == 0) hand_over(std::integral_constant<int, 0>{});
-    else if (wave == 1) hand_over(std::integral_constant<int, 1>{});
+        for (int dt = 0; dt < NDT; dt++) *reinterpret_cast<f32x4*>(&sO[((wave * NDT + dt) * 64 + lane) * 4]) = acc[dt];
+        if (g == 0) sML[(wave * 16 + c) * 2] = m_run, sML[(wave * 16 + c) * 2 + 1] = l_run;
+    }
     __syncthreads();
-    auto merge_store = [&](auto W) {
-        constexpr int WV = decltype(W)::value;
-        const float m1 = sML[((1 - WV) * 16 + c) * 2], l1 = sML[((1 - WV) * 16 + c) * 2 + 1];
-        const float M = fmaxf(l_run > 0.f ? m_run : kNegInf, l1 > 0.f ? m1 : kNegInf);
-        const float f0 = l_run > 0.f ? exp2_fast(m_run - M) : 0.f, f1 = l1 > 0.f ? exp2_fast(m1 - M) : 0.f;
-        const float L = l_run * f0 + l1 * f1;
-        f32x4 o[NDH];
+    {
+        const float m0 = sML[c * 2], l0 = sML[c * 2 + 1], m1 = sML[(16 + c) * 2], l1 = sML[(16 + c) * 2 + 1];
+        const float M = fmaxf(l0 > 0.f ? m0 : kNegInf, l1 > 0.f ? m1 : kNegInf);
+        const float f0 = l0 > 0.f ? exp2_fast(m0 - M) : 0.f, f1 = l1 > 0.f ? exp2_fast(m1 - M) : 0.f;
+        const float L = l0 * f0 + l1 * f1;
+        f32x4 o[NDQ];
 #pragma unroll
-        for (int j = 0; j < NDH; j++) {
-            const f32x4 o1 = *reinterpret_cast<const f32x4*>(&sO[((WV * NDH + j) * 64 + lane) * 4]);
-            o[j] = acc[WV * NDH + j] * f0 + o1 * f1;  // columns c and c ^ 8 (one query row) share f0, f1
+        for (int j = 0; j < NDQ; j++) {
+            const int dt = wave * NDQ + j;
+            const f32x4 o0 = *reinterpret_cast<const f32x4*>(&sO[(dt * 64 + lane) * 4]);
+            const f32x4 o1 = *reinterpret_cast<const f32x4*>(&sO[((NDT + dt) * 64 + lane) * 4]);
+            o[j] = o0 * f0 + o1 * f1;  // columns c and c ^ 8 (one query row) share f0, f1
 #pragma unroll
             for (int e = 0; e < 4; e++) o[j][e] += xor8(o[j][e]);
         }
@@ -1129,20 +1125,18 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             const int row = (t * a.NH + h) * S + z;  // the host keeps the partial buffer below 2 GiB
             const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o, (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
-            for (int j = 0; j < NDH; j++)
-                __builtin_amdgcn_raw_buffer_store_b128(o[j], rpo, (row * D + (WV * NDH + j) * 16 + g * 4) * 4, 0, kScDevice);
-            if (!one && WV == 0 && g == 0) {
+            for (int j = 0; j < NDQ; j++)
+                __builtin_amdgcn_raw_buffer_store_b128(o[j], rpo, (row * D + (wave * NDQ + j) * 16 + g * 4) * 4, 0, kScDevice);
+            if (!one && wave == 0 && g == 0) {
                 a.part_ml[(size_t)row * 2] = M;
                 a.part_ml[(size_t)row * 2 + 1] = L;
             }
         }
         m_run = M, l_run = L;
-    };
-    if (wave == 0) merge_store(std::integral_constant<int, 0>{});
-    else if (wave == 1) merge_store(std::integral_constant<int, 1>{});
+    }
     if (one) {
         // the records go out once every o store of the workgroup is acknowledged (the wait counts the
-        // wave's memory operations, the barrier joins both compute waves): a record with this launch's tag
+        // wave's memory operations, the barrier joins the four waves): a record with this launch's tag
         // is the combiner's guarantee that its row's o is visible device-wide
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();

@@ -62,9 +62,11 @@ rep("""            __hip_atomic_store(&freed[wave], i + 1, __ATOMIC_RELAXED, __H
 rep("""        l_run += __shfl_xor(l_run, 16, 64);  // the column's sum over the lane groups""", """        { float s0 = acc[0][0]; asm volatile("" :: "v"(s0)); PSTAMP(2); }
         l_run += __shfl_xor(l_run, 16, 64);  // the column's sum over the lane groups""")
 rep("""        m_run = M, l_run = L;
-    };""", """        m_run = M, l_run = L;
+    }
+""", """        m_run = M, l_run = L;
         PSTAMP(3);
-    };""")
+    }
+""")
 rep("""                                                   rr, row * 16, 0, kScDevice);
         }
     }
