@@ -162,23 +162,53 @@ __global__ __launch_bounds__(64) void k_qsa_pool(QsaPoolArgs a) {
 }
 
 // ---- selection -------------------------------------------------------------------------------------------
+// Inclusive sum over the wave's lanes in lane order: within each 16-lane row (DPP row shifts), then the
+// totals of the rows below added (three lane reads).
+__device__ __forceinline__ int wave_scan(int x, int lane) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+    const int r2 = __builtin_amdgcn_readlane(x, 47);
+    return x + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
+}
+
+// Exclusive sum over the workgroup's threads in thread order (wave scans, then the earlier waves' totals
+// through LDS: one barrier). `s_tot` holds 16 words.
+__device__ __forceinline__ int block_excl_scan(int x, int* s_tot) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int inc = wave_scan(x, lane);
+    if (lane == 63) s_tot[wave] = inc;
+    __syncthreads();
+    const int base = (int)wave_isum(lane < wave ? (unsigned)s_tot[lane] : 0u);
+    return base + inc - x;
+}
+
 // The exact top-`top` of token t's nblk block scores (by score, then the lower block id: the scores are >= +0,
 // so their bit patterns order like the values), by the last workgroup to arrive; writes the token's mask
-// row and key bits. STAGED: the scores fit kQsaKeysLds and are read once into LDS, else from memory on each
-// use (device-coherent loads).
+// row and key bits. STAGED: the scores fit kQsaKeysLds and are read once (into registers and LDS), else
+// from memory on each use (device-coherent loads).
+//
+// The threshold key is found most significant digit first, 11 bits a pass (at most three passes, fewer when
+// the smallest and largest keys share their top bits): the keys that match the digits found so far are
+// counted per next digit in an LDS histogram (2,048 bins, LDS atomic adds), and a scan over the bins from the
+// top, two bins a thread, finds the digit where the count of larger keys reaches the number still needed.
 template <bool STAGED>
 __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
                                               unsigned* s_key, unsigned* s_mask, int* s_misc, int* s_scan,
-                                              unsigned* s_priv) {
+                                              unsigned* s_hist) {
     constexpr int KPT = (kQsaKeysLds + kQsaThreads - 1) / kQsaThreads;  // staged keys a thread, at most
+    constexpr int NB = 2048;                                            // bins of a pass
+    static_assert(NB == 2 * kQsaThreads, "two bins a thread");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     auto key = [&](int b) -> unsigned {
         if constexpr (STAGED) return s_key[b];
         else return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
     };
+    unsigned kr[STAGED ? KPT : 1];  // staged: keys tid + 1024 i
     unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
     if constexpr (STAGED) {
-        unsigned kr[KPT];
 #pragma unroll
         for (int i = 0; i < KPT; i++) {  // every load issued before any is used
             const int b = tid + i * kQsaThreads;
@@ -195,172 +225,97 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
             kmin = min(kmin, k), kmax = max(kmax, k);
         }
     }
+    s_hist[2 * tid] = 0u, s_hist[2 * tid + 1] = 0u;  // the first pass's bins
+    kmin = wave_min(kmin), kmax = wave_max(kmax);
+    if (lane == 0) s_scan[wave] = (int)kmin, s_scan[16 + wave] = (int)kmax;
     __syncthreads();
+    {
+        const unsigned m0 = lane < 16 ? (unsigned)s_scan[lane] : 0xFFFFFFFFu;
+        const unsigned m1 = lane < 16 ? (unsigned)s_scan[16 + lane] : 0u;
+        kmin = wave_min(m0), kmax = wave_max(m1);  // every wave, the same reduction
+    }
     const int nmw = (nblk + 31) >> 5;  // mask words holding complete blocks
 
-    if (STAGED && nblk <= kQsaThreads) {
-        // one key a thread: its rank among all keys (ahead of it: larger, or equal with a lower id), from
-        // broadcast LDS reads; selected when the rank is below `top`
-        const unsigned k = tid < nblk ? s_key[tid] : 0u;
-        int rank = 0;
-        const int n4 = nblk & ~3;
-        for (int b = 0; b < n4; b += 4) {
-            const uint4 q = *reinterpret_cast<const uint4*>(&s_key[b]);
-            rank += (q.x > k || (q.x == k && b < tid)) + (q.y > k || (q.y == k && b + 1 < tid)) +
-                    (q.z > k || (q.z == k && b + 2 < tid)) + (q.w > k || (q.w == k && b + 3 < tid));
-        }
-        for (int b = n4; b < nblk; b++) rank += s_key[b] > k || (s_key[b] == k && b < tid);
-        const unsigned long long sel = __ballot(tid < nblk && rank < a.top);
-        if (lane == 0) {
-            if (2 * wave < nmw) s_mask[2 * wave] = (unsigned)sel;
-            if (2 * wave + 1 < nmw) s_mask[2 * wave + 1] = (unsigned)(sel >> 32);
-        }
-    } else {
-        kmin = wave_min(kmin), kmax = wave_max(kmax);
-        if (lane == 0) s_scan[wave] = (int)kmin, s_scan[16 + wave] = (int)kmax;
-        __syncthreads();
-        if (wave == 0) {  // over the 16 waves: one read a lane, then the wave reductions
-            const unsigned m0 = lane < 16 ? (unsigned)s_scan[lane] : 0xFFFFFFFFu;
-            const unsigned m1 = lane < 16 ? (unsigned)s_scan[16 + lane] : 0u;
-            const unsigned mn = wave_min(m0), mx = wave_max(m1);
-            if (lane == 0) s_misc[3] = (int)mn, s_misc[4] = (int)mx;
-        }
-        __syncthreads();
-        kmin = (unsigned)s_misc[3], kmax = (unsigned)s_misc[4];
-        // the bits above the highest one where the smallest and largest keys differ are every key's: the
-        // radix passes (4 bits each, from the top) start at the digit holding that bit
-        const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
-        const int shift0 = hb < 0 ? -4 : (hb & ~3);
-        unsigned pmask = hb < 0 ? 0xFFFFFFFFu : (shift0 + 4 >= 32 ? 0u : ~0u << (shift0 + 4));
-        unsigned prefix = kmin & pmask;
-        int need = a.top;  // keys still to take at or below the current prefix
-        for (int shift = shift0; shift >= 0; shift -= 4) {
-            // each thread counts the 16 digits of its matching keys: staged, at most KPT = 12 keys a thread,
-            // in 4-bit counters of one 64-bit register (a key adds 1 << 4 d); else in four registers of 8-bit
-            // counters (a key adds 1 << 8 (d % 4) to word d / 4; at most 144 keys a thread). The counters are
-            // widened to 16-bit pairs and summed over the wave (DPP), then over the waves through LDS
-            unsigned cw[4] = {0u, 0u, 0u, 0u};
-            if constexpr (STAGED) {
-                static_assert(KPT < 16, "4-bit counters");
-                unsigned kr[KPT];
+    // the bits above the highest one where the smallest and largest keys differ are every key's
+    const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
+    unsigned prefix = hb < 0 ? kmin : (hb == 31 ? 0u : kmin & ~((2u << hb) - 1u));
+    int need = a.top;  // keys still to take among those matching the prefix
+    for (int hi = hb, pass = 0; hi >= 0; pass++) {
+        const int shift = max(hi - 10, 0), width = hi - shift + 1;
+        const unsigned pmask = hi == 31 ? 0u : ~((2u << hi) - 1u);  // the digits found so far
+        const unsigned dmask = (1u << width) - 1u;
+        unsigned* h = s_hist + (pass & 1) * NB;
+        if constexpr (STAGED) {
 #pragma unroll
-                for (int i = 0; i < KPT; i++) kr[i] = tid + i * kQsaThreads < nblk ? s_key[tid + i * kQsaThreads] : 0u;
-                unsigned long long c64 = 0ull;
-#pragma unroll
-                for (int i = 0; i < KPT; i++) {
-                    const unsigned k = kr[i];
-                    const bool m = tid + i * kQsaThreads < nblk && (k & pmask) == prefix;
-                    c64 += m ? 1ull << (4 * ((k >> shift) & 15u)) : 0ull;
-                }
-                // nibble d of c64 -> byte d % 4 of word d / 4
-                const unsigned lo = (unsigned)c64, hi = (unsigned)(c64 >> 32);
-                cw[0] = (lo & 0xFu) | ((lo >> 4) & 0xFu) << 8 | ((lo >> 8) & 0xFu) << 16 | ((lo >> 12) & 0xFu) << 24;
-                cw[1] = ((lo >> 16) & 0xFu) | ((lo >> 20) & 0xFu) << 8 | ((lo >> 24) & 0xFu) << 16 | (lo >> 28) << 24;
-                cw[2] = (hi & 0xFu) | ((hi >> 4) & 0xFu) << 8 | ((hi >> 8) & 0xFu) << 16 | ((hi >> 12) & 0xFu) << 24;
-                cw[3] = ((hi >> 16) & 0xFu) | ((hi >> 20) & 0xFu) << 8 | ((hi >> 24) & 0xFu) << 16 | (hi >> 28) << 24;
-            } else {
-                for (int b = tid; b < nblk; b += kQsaThreads) {
-                    const unsigned k = key(b);
-                    const unsigned d = (k >> shift) & 15u;
-                    const unsigned inc = (k & pmask) == prefix ? 1u << (8 * (d & 3u)) : 0u;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) cw[q] += (d >> 2) == (unsigned)q ? inc : 0u;
-                }
-            }
-            // counts of the pass in their own LDS words (this pass's parity): the previous pass's may
-            // still be read by a wave deciding its digit
-            unsigned* sp = s_priv + (shift & 4 ? 128 : 0);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                // digits 4q, 4q + 2 in the low and high halves of one word; 4q + 1, 4q + 3 in another
-                const unsigned ev = wave_isum(cw[q] & 0x00FF00FFu), od = wave_isum((cw[q] >> 8) & 0x00FF00FFu);
-                if (lane == 0) sp[wave * 8 + 2 * q] = ev, sp[wave * 8 + 2 * q + 1] = od;
-            }
-            __syncthreads();
-            // every wave decides the digit itself (the same sums in the same order): no second barrier. Lane l
-            // takes digit d = 15 - l % 16 of the waves 4 (l / 16) .. + 3 (four reads), the four row groups are
-            // summed by permlane swaps, so each lane holds the total of its digit; an inclusive scan over each
-            // 16-lane row (DPP row_shr) then counts the keys whose digit is at least 15 - l % 16
-            const int d = 15 - (lane & 15), g4 = 4 * (lane >> 4);
-            const int word = 2 * (d >> 2) + (d & 1), sh = 16 * ((d >> 1) & 1);
-            unsigned cnt = 0u;
-#pragma unroll
-            for (int w = 0; w < 4; w++) cnt += (sp[(g4 + w) * 8 + word] >> sh) & 0xFFFFu;
-            const auto s16 = __builtin_amdgcn_permlane16_swap(cnt, cnt, false, false);
-            cnt = s16[0] + s16[1];
-            const auto s32 = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
-            cnt = s32[0] + s32[1];
-            const int cntd = (int)cnt;
-            int inc = cntd;
-            inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xF, 0xF, false);  // row_shr:1
-            inc += __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xF, 0xF, false);  // row_shr:2
-            inc += __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xF, 0xF, false);  // row_shr:4
-            inc += __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xF, 0xF, false);  // row_shr:8
-            const unsigned long long hit = __ballot(lane < 16 && inc >= need);
-            const int l0 = hit ? __builtin_ctzll(hit) : 15;  // the keys matching the prefix reach `need`
-            const int above = __builtin_amdgcn_readlane(inc - cntd, l0);
-            prefix |= (unsigned)(15 - l0) << shift;
-            pmask |= 15u << shift;
-            need -= above;
-        }
-        // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
-        // block order). Thread tid owns the blocks [tid * per, tid * per + per): 8 (four threads a mask word,
-        // combined by DPP) when they cover nblk, else a multiple of 32.
-        const int per = nblk <= 8 * kQsaThreads ? 8 : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
-        const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
-        int eq = 0;
-        if (per == 8) {
-            unsigned kr[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) kr[i] = lo + i < hi ? key(lo + i) : 0u;
-#pragma unroll
-            for (int i = 0; i < 8; i++) eq += lo + i < hi && kr[i] == prefix;
+            for (int i = 0; i < KPT; i++)
+                if (tid + i * kQsaThreads < nblk && (kr[i] & pmask) == prefix)
+                    __hip_atomic_fetch_add(&h[(kr[i] >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         } else {
-            for (int b = lo; b < hi; b++) eq += key(b) == prefix;
+            for (int b = tid; b < nblk; b += kQsaThreads) {
+                const unsigned k = key(b);
+                if ((k & pmask) == prefix)
+                    __hip_atomic_fetch_add(&h[(k >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
         }
-        // exclusive prefix of the equal counts over the threads: within the wave, then the earlier waves'
-        // totals (one read a lane and a wave sum)
-        int inc = eq;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int u = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += u;
-        }
-        if (lane == 63) s_scan[32 + wave] = inc;
         __syncthreads();
-        const int base = (int)wave_isum(lane < wave ? (unsigned)s_scan[32 + lane] : 0u);
-        int taken = base + inc - eq;
-        if (per == 8) {
-            unsigned bits = 0u;
+        // the next pass's bins (last read two passes ago, before this pass's first barrier)
+        s_hist[((pass + 1) & 1) * NB + 2 * tid] = 0u, s_hist[((pass + 1) & 1) * NB + 2 * tid + 1] = 0u;
+        // thread tid: digits d1 = 2^width - 1 - 2 tid and d1 - 1 (from the top); the keys with a larger digit
+        // are the exclusive scan of the pair counts
+        const int d1 = (int)dmask - 2 * tid, d0 = d1 - 1;
+        const int c1 = d1 >= 0 ? (int)h[d1] : 0, c0 = d0 >= 0 ? (int)h[d0] : 0;
+        const int larger = block_excl_scan(c1 + c0, s_scan + 32);
+        if (larger < need && larger + c1 + c0 >= need) {  // exactly one thread
+            const bool in1 = larger + c1 >= need;
+            s_misc[0] = in1 ? d1 : d0;
+            s_misc[1] = in1 ? larger : larger + c1;
+        }
+        __syncthreads();
+        prefix |= (unsigned)s_misc[0] << shift;
+        need -= s_misc[1];
+        hi = shift - 1;
+    }
+    // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
+    // block order). Thread tid owns the blocks [tid * per, tid * per + per): 8 (four threads a mask word,
+    // combined by DPP) when they cover nblk, else a multiple of 32.
+    const int per = nblk <= 8 * kQsaThreads ? 8 : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
+    const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
+    int eq = 0;
+    if (per == 8) {
+        unsigned kq[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (lo + i < hi) {
-                    const unsigned k = key(lo + i);
+        for (int i = 0; i < 8; i++) kq[i] = lo + i < hi ? key(lo + i) : 0u;
+#pragma unroll
+        for (int i = 0; i < 8; i++) eq += lo + i < hi && kq[i] == prefix;
+        int taken = block_excl_scan(eq, s_scan + 32);  // equal keys in earlier blocks
+        unsigned bits = 0u;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            bool sel = lo + i < hi && kq[i] > prefix;
+            if (lo + i < hi && kq[i] == prefix) sel = taken++ < need;
+            bits |= (unsigned)sel << i;
+        }
+        // the word of blocks [32 (tid / 4), + 32): the four threads' bytes OR-ed across the quad
+        unsigned wv = bits << (8 * (tid & 3));
+        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);
+        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);
+        if ((tid & 3) == 0 && (tid >> 2) < nmw) s_mask[tid >> 2] = wv;
+    } else {
+        for (int b = lo; b < hi; b++) eq += key(b) == prefix;
+        int taken = block_excl_scan(eq, s_scan + 32);
+        // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
+        for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
+            unsigned bits = 0u;
+            for (int i = 0; i < 32; i++) {
+                const int b = 32 * w + i;
+                if (b < hi) {
+                    const unsigned k = key(b);
                     bool sel = k > prefix;
                     if (k == prefix) sel = taken++ < need;
                     bits |= (unsigned)sel << i;
                 }
             }
-            // the word of blocks [32 (tid / 4), + 32): the four threads' bytes OR-ed across the quad
-            unsigned wv = bits << (8 * (tid & 3));
-            wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);
-            wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);
-            if ((tid & 3) == 0 && (tid >> 2) < nmw) s_mask[tid >> 2] = wv;
-        } else {
-            // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
-            for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
-                unsigned bits = 0u;
-                for (int i = 0; i < 32; i++) {
-                    const int b = 32 * w + i;
-                    if (b < hi) {
-                        const unsigned k = key(b);
-                        bool sel = k > prefix;
-                        if (k == prefix) sel = taken++ < need;
-                        bits |= (unsigned)sel << i;
-                    }
-                }
-                s_mask[w] = bits;
-            }
+            s_mask[w] = bits;
         }
     }
     __syncthreads();
@@ -382,12 +337,12 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     unsigned* s_key = reinterpret_cast<unsigned*>(smem);   // [kQsaKeysLds] staged score bits
     unsigned* s_mask = s_key + kQsaKeysLds;                 // [kQsaMaskLds] the token's selection
     int* s_misc = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [16]
-    int* s_tot = s_misc + 16;                               // [16] digit counts of a pass
+    int* s_tot = s_misc + 16;                               // [16] spare
     int* s_scan = s_tot + 16;                               // [48]: per-wave minima, maxima, sums
     unsigned char* work = reinterpret_cast<unsigned char*>(s_scan + 48);
     float* s_q = reinterpret_cast<float*>(work);            // scoring: [IH][ID] normed, rotated query heads
     float* s_t = s_q + a.IH * a.ID;                         // scoring: [IH][ID] the normed heads before rotation
-    unsigned* s_priv = reinterpret_cast<unsigned*>(work);   // select: [2 passes][waves][8] packed digit counts
+    unsigned* s_hist = reinterpret_cast<unsigned*>(work);   // select: [2 passes][2,048] digit counts
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x, t = blockIdx.y;
@@ -472,8 +427,8 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     if (s_misc[0] != ct - 1) return;
 
     // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
-    if (nblk <= kQsaKeysLds) select_blocks<true>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_priv);
-    else select_blocks<false>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_priv);
+    if (nblk <= kQsaKeysLds) select_blocks<true>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_hist);
+    else select_blocks<false>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_hist);
 }
 
 // ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
@@ -484,7 +439,7 @@ __global__ __launch_bounds__(256) void k_qsa_key_bits(QsaKeyBitsArgs a) {
 }
 
 size_t qsa_select_lds(int IH, int ID) {
-    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)2 * 8 * (kQsaThreads / 64) * 4);
+    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)2 * 2048 * 4);
     return (size_t)(kQsaKeysLds + kQsaMaskLds + 32 + 48) * 4 + work;
 }
 
