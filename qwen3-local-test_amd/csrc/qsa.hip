@@ -27,7 +27,7 @@ namespace qw {
 namespace {
 
 constexpr int kQsaThreads = 1024;
-constexpr int kQsaChunk = 128;        // blocks scored per workgroup
+constexpr int kQsaChunk = 64;         // blocks scored per workgroup (one key per 16-lane group)
 constexpr int kQsaKeysLds = 12288;    // scores staged in LDS for the select (more: read from memory)
 constexpr int kQsaMaskLds = 4608;     // mask words staged in LDS (>= (262144 / 2 + 1 + 31) / 32)
 
@@ -92,6 +92,26 @@ __device__ __forceinline__ void rope_row(const float* x, float* y, const float* 
 // visible when block j / cr has its bit set or lies at or past nblk (the tail). One division per word, the
 // block of each following key by counting.
 __device__ __forceinline__ unsigned key_word(const unsigned* m, int w, int cr, int nblk) {
+    const int nmwc = (nblk + 31) >> 5;
+    if ((cr & (cr - 1)) == 0) {
+        // a power of two: the word lies in one block (cr >= 32) or holds 32 / cr whole blocks of one mask word
+        const int lc = __builtin_ctz((unsigned)cr);
+        if (cr >= 32) {
+            const int blk = (32 * w) >> lc;
+            const unsigned mw = (blk >> 5) < nmwc ? m[blk >> 5] : 0u;
+            return blk >= nblk || ((mw >> (blk & 31)) & 1u) ? 0xFFFFFFFFu : 0u;
+        }
+        const int nb = 32 >> lc, blk0 = w * nb;
+        const unsigned mw = (blk0 >> 5) < nmwc ? m[blk0 >> 5] : 0u, ones = (1u << cr) - 1u;
+        unsigned bits = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (i < nb) {
+                const int blk = blk0 + i;
+                bits |= blk >= nblk || ((mw >> (blk & 31)) & 1u) ? ones << (i * cr) : 0u;
+            }
+        return bits;
+    }
     int blk = (32 * w) / cr, r = 32 * w - blk * cr;
     // the 32 keys lie in at most 32 consecutive blocks: two mask words, read once (only words that hold
     // complete blocks are read)
@@ -239,6 +259,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     // the bits above the highest one where the smallest and largest keys differ are every key's
     const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
     unsigned prefix = hb < 0 ? kmin : (hb == 31 ? 0u : kmin & ~((2u << hb) - 1u));
+    unsigned fmask = 0xFFFFFFFFu;  // the bits of a key the final comparison looks at
     int need = a.top;  // keys still to take among those matching the prefix
     for (int hi = hb, pass = 0; hi >= 0; pass++) {
         const int shift = max(hi - 10, 0), width = hi - shift + 1;
@@ -269,11 +290,17 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
             const bool in1 = larger + c1 >= need;
             s_misc[0] = in1 ? d1 : d0;
             s_misc[1] = in1 ? larger : larger + c1;
+            s_misc[2] = in1 ? c1 : c0;
         }
         __syncthreads();
         prefix |= (unsigned)s_misc[0] << shift;
         need -= s_misc[1];
         hi = shift - 1;
+        if (s_misc[2] == need && hi >= 0) {
+            // every key matching the digits so far is taken: the lower bits need not be resolved
+            fmask = ~((2u << hi) - 1u);
+            break;
+        }
     }
     // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
     // block order). Thread tid owns the blocks [tid * per, tid * per + per): 8 (four threads a mask word,
@@ -284,7 +311,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     if (per == 8) {
         unsigned kq[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) kq[i] = lo + i < hi ? key(lo + i) : 0u;
+        for (int i = 0; i < 8; i++) kq[i] = lo + i < hi ? key(lo + i) & fmask : 0u;
 #pragma unroll
         for (int i = 0; i < 8; i++) eq += lo + i < hi && kq[i] == prefix;
         int taken = block_excl_scan(eq, s_scan + 32);  // equal keys in earlier blocks
@@ -301,7 +328,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
         wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);
         if ((tid & 3) == 0 && (tid >> 2) < nmw) s_mask[tid >> 2] = wv;
     } else {
-        for (int b = lo; b < hi; b++) eq += key(b) == prefix;
+        for (int b = lo; b < hi; b++) eq += (key(b) & fmask) == prefix;
         int taken = block_excl_scan(eq, s_scan + 32);
         // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
         for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
@@ -309,7 +336,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
             for (int i = 0; i < 32; i++) {
                 const int b = 32 * w + i;
                 if (b < hi) {
-                    const unsigned k = key(b);
+                    const unsigned k = key(b) & fmask;
                     bool sel = k > prefix;
                     if (k == prefix) sel = taken++ < need;
                     bits |= (unsigned)sel << i;
@@ -328,7 +355,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
 }
 
 
-// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [128 c, 128 c + 128) of token t; the last of
+// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [64 c, 64 c + 64) of token t; the last of
 // the token's workgroups to arrive selects. A token that selects nothing has its rows written by workgroup
 // (0, t).
 template <int IN_DT>
@@ -360,6 +387,22 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     const int ct = (nblk + kQsaChunk - 1) / kQsaChunk;  // this token's workgroups
     if (c >= ct) return;
 
+    // this chunk's pooled keys, 16 lanes a key, DL = ID / 16 consecutive dims a lane: loaded first, so that
+    // their latency hides behind the query heads' prologue
+    static_assert(kQsaChunk == kQsaThreads / 16, "one key per 16-lane group");
+    const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
+    const int bc0 = c * kQsaChunk, bc1 = min(nblk, bc0 + kQsaChunk);
+    const int b = bc0 + grp;
+    float kv[16];
+    {
+        const float* pk = a.pooled + (size_t)min(b, bc1 - 1) * ID + sub * DL;  // past the chunk: a valid row
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+            if (i < DL) {  // DL <= 16: the host keeps ID <= 256
+                const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
+                kv[i] = v[0], kv[i + 1] = v[1], kv[i + 2] = v[2], kv[i + 3] = v[3];
+            }
+    }
     // the query heads: RMS-normed (gamma as stored), rotated to p; wave w takes heads w, w + 16, ...
     for (int h = wave; h < a.IH; h += kQsaThreads / 64) {
         float ss = 0.f;
@@ -379,41 +422,21 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     }
     __syncthreads();
 
-    // scores of this chunk: 16 lanes per pooled key, DL = ID / 16 consecutive dims a lane, 64 keys a round;
-    // the loads of the chunk's rounds are issued before any is used
-    const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
-    const int bc0 = c * kQsaChunk, bc1 = min(nblk, bc0 + kQsaChunk);
+    // the chunk's scores: sum over the heads of relu(q_h . key), the dot products summed over each 16-lane row
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
                                                                         a.stride * 4, 0x00020000);
-    constexpr int RB = kQsaChunk / (kQsaThreads / 16), GPR = kQsaThreads / 16;  // rounds per batch, keys per round
-    for (int b0 = bc0; b0 < bc1; b0 += RB * GPR) {
-        float kv[RB][16];
+    {
+        float sc = 0.f;
+        for (int h = 0; h < a.IH; h++) {
+            const float* qh = s_q + h * ID + sub * DL;
+            float dp = 0.f;
 #pragma unroll
-        for (int rr = 0; rr < RB; rr++) {
-            const int b = min(b0 + rr * GPR + grp, bc1 - 1);  // past the chunk: a valid row, score not stored
-            const float* pk = a.pooled + (size_t)b * ID + sub * DL;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4)
-                if (i < DL) {  // DL <= 16: the host keeps ID <= 256
-                    const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
-                    kv[rr][i] = v[0], kv[rr][i + 1] = v[1], kv[rr][i + 2] = v[2], kv[rr][i + 3] = v[3];
-                }
+            for (int i = 0; i < 16; i++)
+                if (i < DL) dp = __builtin_fmaf(qh[i], kv[i], dp);
+            dp = sum16(dp);
+            sc += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
         }
-#pragma unroll
-        for (int rr = 0; rr < RB; rr++) {
-            const int b = b0 + rr * GPR + grp;
-            float s = 0.f;
-            for (int h = 0; h < a.IH; h++) {
-                const float* qh = s_q + h * ID + sub * DL;
-                float dp = 0.f;
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    if (i < DL) dp = __builtin_fmaf(qh[i], kv[rr][i], dp);
-                dp = sum16(dp);
-                s += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
-            }
-            if (sub == 0 && b < bc1) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rs, b * 4, 0, kScDevice);
-        }
+        if (sub == 0 && b < bc1) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc), rs, b * 4, 0, kScDevice);
     }
     // arrive: the stores are acknowledged (device-coherent) before the counter moves
     __builtin_amdgcn_s_waitcnt(0);
