@@ -452,6 +452,8 @@ def main():
         # QSA layer steps (indexer + masked decode); the last field is the block size (compress ratio)
         ("decode_32k_qsa_cr4", 32768, 1, args.slots, 0, "f32", 4),
         ("decode_32k_qsa_cr64", 32768, 1, args.slots, 0, "f32", 64),
+        ("decode_256k_qsa_cr4", 262144, 1, 2, 0, "f32", 4),
+        ("decode_256k_qsa_cr64", 262144, 1, 2, 0, "f32", 64),
     ]
     results = {}
     for name, pos, n, slots, n_split, dt, heavy in configs:
@@ -474,7 +476,7 @@ def main():
             r["unit"] = "GB/s (visible keys)"
             r["algorithmic_bytes"] = byts
             r["frac_hbm_kernel"] = byts / (r["us_main"] * 1e-6) / HBM_PEAK
-            dense = results.get("decode_32k")
+            dense = results.get("decode_256k" if pos == 262144 else "decode_32k")  # the dense step at this length
             if dense:
                 r["step_speedup_vs_dense"] = dense["us_per_step"] / r["us_per_step"]
         elif n * (NH // NKV) <= 32:

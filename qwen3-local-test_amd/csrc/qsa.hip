@@ -19,6 +19,8 @@
 // (coalesced 512-byte rows); the scores go to a workspace with device-coherent stores, and the last
 // workgroup of a token to arrive (an arrival counter, no waiting anywhere) runs an exact radix select on
 // the scores' bit patterns (scores are >= +0, so their bits order like the values) and writes the mask.
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -28,7 +30,6 @@ namespace {
 
 constexpr int kQsaThreads = 1024;
 constexpr int kQsaChunk = 64;         // blocks scored per workgroup (one key per 16-lane group)
-constexpr int kQsaKeysLds = 12288;    // scores staged in LDS for the select (more: read from memory)
 constexpr int kQsaMaskLds = 4608;     // mask words staged in LDS (>= (262144 / 2 + 1 + 31) / 32)
 
 // Sum over each 16-lane row, in every lane of the row (DPP butterfly: quads, eight lanes, sixteen).
@@ -207,41 +208,43 @@ __device__ __forceinline__ int block_excl_scan(int x, int* s_tot) {
 
 // The exact top-`top` of token t's nblk block scores (by score, then the lower block id: the scores are >= +0,
 // so their bit patterns order like the values), by the last workgroup to arrive; writes the token's mask
-// row and key bits. STAGED: the scores fit kQsaKeysLds and are read once (into registers and LDS), else
-// from memory on each use (device-coherent loads).
+// row and key bits. Thread tid owns the blocks [per tid, per tid + per). KR > 0: per = KR and the thread
+// holds their keys in registers (nblk <= KR * 1,024; one load per four keys); KR == 0: per is a multiple of
+// 32 and the keys are read from memory at each use (device-coherent loads).
 //
 // The threshold key is found most significant digit first, 11 bits a pass (at most three passes, fewer when
-// the smallest and largest keys share their top bits): the keys that match the digits found so far are
-// counted per next digit in an LDS histogram (2,048 bins, LDS atomic adds), and a scan over the bins from the
-// top, two bins a thread, finds the digit where the count of larger keys reaches the number still needed.
-template <bool STAGED>
+// the smallest and largest keys share their top bits or the digit's bin holds exactly the keys still
+// needed): the keys that match the digits found so far are counted per next digit in an LDS histogram
+// (2,048 bins, LDS atomic adds), and a scan over the bins from the top, two bins a thread, finds the digit
+// where the count of larger keys reaches the number still needed.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int KR>
 __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
-                                              unsigned* s_key, unsigned* s_mask, int* s_misc, int* s_scan,
-                                              unsigned* s_hist) {
-    constexpr int KPT = (kQsaKeysLds + kQsaThreads - 1) / kQsaThreads;  // staged keys a thread, at most
-    constexpr int NB = 2048;                                            // bins of a pass
+                                              unsigned* s_mask, int* s_misc, int* s_scan, unsigned* s_hist) {
+    constexpr int NB = 2048;  // bins of a pass
     static_assert(NB == 2 * kQsaThreads, "two bins a thread");
+    static_assert(KR == 0 || KR == 8 || KR == 16 || KR == 32 || KR == 64, "keys a thread");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    auto key = [&](int b) -> unsigned {
-        if constexpr (STAGED) return s_key[b];
-        else return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice);
-    };
-    unsigned kr[STAGED ? KPT : 1];  // staged: keys tid + 1024 i
+    const int per = KR > 0 ? KR : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
+    const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
+    auto load = [&](int b) -> unsigned { return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice); };
+    unsigned kr[KR > 0 ? KR : 1];
     unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
-    if constexpr (STAGED) {
+    if constexpr (KR > 0) {
+        // every load issued before any is used; keys past nblk are never counted (the buffer reads as 0 past
+        // its end)
 #pragma unroll
-        for (int i = 0; i < KPT; i++) {  // every load issued before any is used
-            const int b = tid + i * kQsaThreads;
-            kr[i] = b < nblk ? __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice) : 0u;
+        for (int i = 0; i < KR; i += 4) {
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (tid * KR + i) * 4, 0, kScDevice));
+            kr[i] = v[0], kr[i + 1] = v[1], kr[i + 2] = v[2], kr[i + 3] = v[3];
         }
 #pragma unroll
-        for (int i = 0; i < KPT; i++) {
-            const int b = tid + i * kQsaThreads;
-            if (b < nblk) s_key[b] = kr[i], kmin = min(kmin, kr[i]), kmax = max(kmax, kr[i]);
-        }
+        for (int i = 0; i < KR; i++)
+            if (lo + i < hi) kmin = min(kmin, kr[i]), kmax = max(kmax, kr[i]);
     } else {
-        for (int b = tid; b < nblk; b += kQsaThreads) {
-            const unsigned k = key(b);
+        for (int b = lo; b < hi; b++) {
+            const unsigned k = load(b);
             kmin = min(kmin, k), kmax = max(kmax, k);
         }
     }
@@ -261,22 +264,21 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     unsigned prefix = hb < 0 ? kmin : (hb == 31 ? 0u : kmin & ~((2u << hb) - 1u));
     unsigned fmask = 0xFFFFFFFFu;  // the bits of a key the final comparison looks at
     int need = a.top;  // keys still to take among those matching the prefix
-    for (int hi = hb, pass = 0; hi >= 0; pass++) {
-        const int shift = max(hi - 10, 0), width = hi - shift + 1;
-        const unsigned pmask = hi == 31 ? 0u : ~((2u << hi) - 1u);  // the digits found so far
+    for (int hb_ = hb, pass = 0; hb_ >= 0; pass++) {
+        const int shift = max(hb_ - 10, 0), width = hb_ - shift + 1;
+        const unsigned pmask = hb_ == 31 ? 0u : ~((2u << hb_) - 1u);  // the digits found so far
         const unsigned dmask = (1u << width) - 1u;
         unsigned* h = s_hist + (pass & 1) * NB;
-        if constexpr (STAGED) {
+        auto count = [&](unsigned k) {
+            if ((k & pmask) == prefix)
+                __hip_atomic_fetch_add(&h[(k >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        if constexpr (KR > 0) {
 #pragma unroll
-            for (int i = 0; i < KPT; i++)
-                if (tid + i * kQsaThreads < nblk && (kr[i] & pmask) == prefix)
-                    __hip_atomic_fetch_add(&h[(kr[i] >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            for (int i = 0; i < KR; i++)
+                if (lo + i < hi) count(kr[i]);
         } else {
-            for (int b = tid; b < nblk; b += kQsaThreads) {
-                const unsigned k = key(b);
-                if ((k & pmask) == prefix)
-                    __hip_atomic_fetch_add(&h[(k >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
+            for (int b = lo; b < hi; b++) count(load(b));
         }
         __syncthreads();
         // the next pass's bins (last read two passes ago, before this pass's first barrier)
@@ -295,52 +297,54 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
         __syncthreads();
         prefix |= (unsigned)s_misc[0] << shift;
         need -= s_misc[1];
-        hi = shift - 1;
-        if (s_misc[2] == need && hi >= 0) {
+        hb_ = shift - 1;
+        if (s_misc[2] == need && hb_ >= 0) {
             // every key matching the digits so far is taken: the lower bits need not be resolved
-            fmask = ~((2u << hi) - 1u);
+            fmask = ~((2u << hb_) - 1u);
             break;
         }
     }
-    // prefix: the top-th largest key; all keys above it are taken, and the first `need` equal to it (in
-    // block order). Thread tid owns the blocks [tid * per, tid * per + per): 8 (four threads a mask word,
-    // combined by DPP) when they cover nblk, else a multiple of 32.
-    const int per = nblk <= 8 * kQsaThreads ? 8 : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
-    const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
+    // prefix (under fmask): the top-th largest key; all keys above it are taken, and the first `need` equal
+    // to it (in block order): the equal keys of the earlier threads' blocks are an exclusive scan
     int eq = 0;
-    if (per == 8) {
-        unsigned kq[8];
+    if constexpr (KR > 0) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) kq[i] = lo + i < hi ? key(lo + i) & fmask : 0u;
-#pragma unroll
-        for (int i = 0; i < 8; i++) eq += lo + i < hi && kq[i] == prefix;
-        int taken = block_excl_scan(eq, s_scan + 32);  // equal keys in earlier blocks
+        for (int i = 0; i < KR; i++) eq += lo + i < hi && (kr[i] & fmask) == prefix;
+    } else {
+        for (int b = lo; b < hi; b++) eq += (load(b) & fmask) == prefix;
+    }
+    int taken = block_excl_scan(eq, s_scan + 32);
+    auto selected = [&](unsigned k) {
+        k &= fmask;
+        bool sel = k > prefix;
+        if (k == prefix) sel = taken++ < need;
+        return sel;
+    };
+    if constexpr (KR == 8 || KR == 16) {
         unsigned bits = 0u;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            bool sel = lo + i < hi && kq[i] > prefix;
-            if (lo + i < hi && kq[i] == prefix) sel = taken++ < need;
-            bits |= (unsigned)sel << i;
+        for (int i = 0; i < KR; i++) bits |= (unsigned)(lo + i < hi && selected(kr[i])) << i;
+        // the word of blocks [32 (tid / q), + 32), q = 32 / KR threads: their parts OR-ed across the group
+        constexpr int Q = 32 / KR;
+        unsigned wv = bits << (KR * (tid & (Q - 1)));
+        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+        if constexpr (Q == 4) wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+        if ((tid & (Q - 1)) == 0 && tid / Q < nmw) s_mask[tid / Q] = wv;
+    } else if constexpr (KR > 0) {
+#pragma unroll
+        for (int w = 0; w < KR / 32; w++) {
+            unsigned bits = 0u;
+#pragma unroll
+            for (int i = 0; i < 32; i++) bits |= (unsigned)(lo + 32 * w + i < hi && selected(kr[32 * w + i])) << i;
+            if (tid * (KR / 32) + w < nmw) s_mask[tid * (KR / 32) + w] = bits;
         }
-        // the word of blocks [32 (tid / 4), + 32): the four threads' bytes OR-ed across the quad
-        unsigned wv = bits << (8 * (tid & 3));
-        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);
-        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);
-        if ((tid & 3) == 0 && (tid >> 2) < nmw) s_mask[tid >> 2] = wv;
     } else {
-        for (int b = lo; b < hi; b++) eq += (key(b) & fmask) == prefix;
-        int taken = block_excl_scan(eq, s_scan + 32);
         // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
         for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
             unsigned bits = 0u;
             for (int i = 0; i < 32; i++) {
                 const int b = 32 * w + i;
-                if (b < hi) {
-                    const unsigned k = key(b) & fmask;
-                    bool sel = k > prefix;
-                    if (k == prefix) sel = taken++ < need;
-                    bits |= (unsigned)sel << i;
-                }
+                if (b < hi && selected(load(b))) bits |= 1u << i;
             }
             s_mask[w] = bits;
         }
@@ -358,11 +362,10 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
 // Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [64 c, 64 c + 64) of token t; the last of
 // the token's workgroups to arrive selects. A token that selects nothing has its rows written by workgroup
 // (0, t).
-template <int IN_DT>
+template <int IN_DT, int KR>
 __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    unsigned* s_key = reinterpret_cast<unsigned*>(smem);   // [kQsaKeysLds] staged score bits
-    unsigned* s_mask = s_key + kQsaKeysLds;                 // [kQsaMaskLds] the token's selection
+    unsigned* s_mask = reinterpret_cast<unsigned*>(smem);  // [kQsaMaskLds] the token's selection
     int* s_misc = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [16]
     int* s_tot = s_misc + 16;                               // [16] spare
     int* s_scan = s_tot + 16;                               // [48]: per-wave minima, maxima, sums
@@ -450,8 +453,7 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     if (s_misc[0] != ct - 1) return;
 
     // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
-    if (nblk <= kQsaKeysLds) select_blocks<true>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_hist);
-    else select_blocks<false>(a, rs, t, nblk, s_key, s_mask, s_misc, s_scan, s_hist);
+    select_blocks<KR>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist);  // the host sizes KR for the call's last token
 }
 
 // ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
@@ -463,7 +465,7 @@ __global__ __launch_bounds__(256) void k_qsa_key_bits(QsaKeyBitsArgs a) {
 
 size_t qsa_select_lds(int IH, int ID) {
     const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)2 * 2048 * 4);
-    return (size_t)(kQsaKeysLds + kQsaMaskLds + 32 + 48) * 4 + work;
+    return (size_t)(kQsaMaskLds + 32 + 48) * 4 + work;
 }
 
 int qsa_mask_lds_words() { return kQsaMaskLds; }
@@ -476,22 +478,46 @@ hipError_t launch_qsa_pool(const QsaPoolArgs& a, int in_dtype, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s) {
-    static unsigned raised[2] = {0u, 0u};  // per device: dynamic LDS limit raised (bit per device)
-    const size_t shm = qsa_select_lds(a.IH, a.ID);
+// Keys a thread holds in the select: the smallest of 8, 16, 32, 64 that covers nmax blocks (0: read from memory).
+static int select_kr(int nmax) {
+    for (int kr = 8; kr <= 64; kr *= 2)
+        if (nmax <= kr * kQsaThreads) return kr;
+    return 0;
+}
+
+template <int IN_DT, int KR>
+static hipError_t launch_select_kr(const QsaSelectArgs& a, size_t shm, dim3 grid, hipStream_t s) {
+    static std::atomic<uint64_t> raised{0};  // per device: dynamic LDS limit raised (bit per device)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
-    auto kern = in_dtype == 0 ? k_qsa_select<0> : k_qsa_select<1>;
-    const unsigned bit = 1u << (dev & 31);
-    if (!(raised[in_dtype] & bit)) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(raised.load(std::memory_order_acquire) & bit)) {
+        const hipError_t e = hipFuncSetAttribute((const void*)k_qsa_select<IN_DT, KR>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
         if (e != hipSuccess) return e;
-        raised[in_dtype] |= bit;
+        raised.fetch_or(bit, std::memory_order_acq_rel);
     }
+    hipLaunchKernelGGL((k_qsa_select<IN_DT, KR>), grid, dim3(kQsaThreads), shm, s, a);
+    return hipGetLastError();
+}
+
+template <int IN_DT>
+static hipError_t launch_select_dt(const QsaSelectArgs& a, int kr, size_t shm, dim3 grid, hipStream_t s) {
+    switch (kr) {
+        case 8: return launch_select_kr<IN_DT, 8>(a, shm, grid, s);
+        case 16: return launch_select_kr<IN_DT, 16>(a, shm, grid, s);
+        case 32: return launch_select_kr<IN_DT, 32>(a, shm, grid, s);
+        case 64: return launch_select_kr<IN_DT, 64>(a, shm, grid, s);
+        default: return launch_select_kr<IN_DT, 0>(a, shm, grid, s);
+    }
+}
+
+hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s) {
+    const size_t shm = qsa_select_lds(a.IH, a.ID);
     const int nmax = (a.pos + a.n) / a.CR;
     const dim3 grid((nmax + kQsaChunk - 1) / kQsaChunk > 0 ? (nmax + kQsaChunk - 1) / kQsaChunk : 1, a.n);
-    hipLaunchKernelGGL(kern, grid, dim3(kQsaThreads), shm, s, a);
-    return hipGetLastError();
+    const int kr = select_kr(nmax);
+    return in_dtype == 0 ? launch_select_dt<0>(a, kr, shm, grid, s) : launch_select_dt<1>(a, kr, shm, grid, s);
 }
 
 hipError_t launch_qsa_key_bits(const QsaKeyBitsArgs& a, hipStream_t s) {

@@ -64,11 +64,15 @@ CASES = {
              "f32"),
     "block64": (QSA_BLOCK64, 8192, [(0, 2000, 1), (2000, 1, 1), (2001, 100, 1), (2101, 4, 1), (2103, 1, 1)], "bf16"),
     "odd": (QSA_ODD, 1024, [(0, 100, 1), (100, 1, 1), (101, 4, 1), (103, 2, 1), (105, 50, 1)], "f32"),
-    # 131,000+ blocks: the scores no longer fit the select's LDS, and 40 tokens take two select launches
+    # 131,000+ blocks: the select reads the scores from memory at each use, and 40 tokens take two select launches
     "long_cr2": (QsaShape(1, 64, 2, 64, 64), 262144, [(0, 262000, 0), (262000, 40, 1)], "f32"),
-    # 8,192 blocks at 32K: the staged radix passes (more blocks than the select's threads)
+    # 8,192 blocks at 32K: 8 keys a select thread
     "cr4_32k": (QsaShape(4, 128, 4, 2048, 64), 32776, [(0, 32768, 0), (32768, 1, 1), (32769, 4, 1)], "f32"),
-    # zero indexer queries: every score is 0, the lowest block ids win (staged radix and rank paths)
+    # 16,384 / 32,768 / 65,536 blocks: 16, 32 and 64 keys a select thread
+    "cr4_64k": (QsaShape(4, 128, 4, 2048, 64), 65544, [(0, 65536, 0), (65536, 1, 1), (65537, 2, 1)], "f32"),
+    "cr2_64k": (QsaShape(2, 64, 2, 512, 64), 65544, [(0, 65536, 0), (65536, 1, 1), (65537, 3, 1)], "f32"),
+    "cr4_256k": (QsaShape(1, 64, 4, 1024, 64), 262152, [(0, 262144, 0), (262144, 1, 1), (262145, 2, 1)], "f32"),
+    # zero indexer queries: every score is 0, the lowest block ids win (no histogram pass at all)
     "zeros": (QsaShape(2, 128, 4, 256, 64), 8200, [(0, 8000, 0), (8000, 2, 1), (8002, 1, 1)], "f32"),
 }
 
