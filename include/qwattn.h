@@ -285,6 +285,17 @@ int qwattn_qsa_select(qwattn_ctx* ctx, void* stream, const void* iq, int in_dtyp
                       int idx_heads, int idx_dim, int cr, int budget, const float* pooled, int pos, int n,
                       uint32_t* mask, int mask_words, uint32_t* key_bits, int kb_words);
 
+/* qwattn_qsa_pool then qwattn_qsa_select (the reference's update then select, src/qwen4_vk.cpp:942-964) in
+ * one call, with the same results and arguments as the two (ik and iq in one in_dtype). When the call
+ * completes no block ((pos + n) / cr == pos / cr: every decode step but one in cr) there is nothing to pool
+ * and the select launch appends the raw keys itself, so the pair costs one launch; otherwise the two
+ * launches run as they would. No reference counterpart of its own: it fuses two that the reference calls
+ * back to back. */
+int qwattn_qsa_index(qwattn_ctx* ctx, void* stream, const void* ik, const void* iq, int in_dtype,
+                     const float* k_gamma, const float* q_gamma, int idx_heads, int idx_dim, int cr, int budget,
+                     float* raw, float* pooled, int cap, int pos, int n, uint32_t* mask, int mask_words,
+                     uint32_t* key_bits, int kb_words);
+
 /* The per-key visibility bits from a block mask in the reference's format (mask[t][mask_words], as the
  * reference's attention_qsa_kv16 pipeline takes it: shaders/attention.comp:35-43): bit j of key_bits[t] is
  * set when block j / cr has its bit set or j >= ((pos + t + 1) / cr) * cr. */

@@ -90,11 +90,9 @@ public:
                              const float* iq_gamma, const float* ik_gamma, int idx_heads, int idx_dim, int cr,
                              int budget, float* raw, float* pooled, int cap, uint32_t* key_bits, int kb_words,
                              float* out, int pos, int n, int n_split = 0) {
-        check(ctx_, qwattn_qsa_pool(ctx_, stream, ik, idx_dtype, ik_gamma, idx_dim, cr, raw, pooled, cap, pos, n),
-              "qwattn_qsa_pool");
-        check(ctx_, qwattn_qsa_select(ctx_, stream, iq, idx_dtype, iq_gamma, idx_heads, idx_dim, cr, budget, pooled,
-                                      pos, n, nullptr, 0, key_bits, kb_words),
-              "qwattn_qsa_select");
+        check(ctx_, qwattn_qsa_index(ctx_, stream, ik, iq, idx_dtype, ik_gamma, iq_gamma, idx_heads, idx_dim, cr, budget,
+                                     raw, pooled, cap, pos, n, nullptr, 0, key_bits, kb_words),
+              "qwattn_qsa_index");
         check(ctx_, qwattn_layer_attention_qsa(ctx_, stream, slot, qg, k, v, in_dtype, qn, kn, out, pos, n, n_split,
                                                key_bits, kb_words),
               "qwattn_layer_attention_qsa");

@@ -70,6 +70,7 @@ def load_library():
         "qwattn_sync_status": [_P, _P],
         "qwattn_qsa_pool": [_P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I],
         "qwattn_qsa_select": [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I],
+        "qwattn_qsa_index": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P, _I],
         "qwattn_qsa_key_bits": [_P, _P, _P, _I, _I, _I, _I, _P, _I],
         "qwattn_attend_partial_qsa": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
         "qwattn_decode_qsa": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P],
@@ -251,6 +252,14 @@ class Attention:
             self.h, _stream(stream), _ptr(iq), _DT[iq.dtype], _ptr(q_gamma), iq.shape[1], iq.shape[2], cr, budget,
             _ptr(pooled), pos, n, _ptr(mask), 0 if mask is None else mask.shape[-1], _ptr(key_bits),
             0 if key_bits is None else key_bits.shape[-1]))
+
+    def qsa_index(self, ik, iq, k_gamma, q_gamma, cr, budget, raw, pooled, cap, pos, n, mask=None, key_bits=None,
+                  stream=None):
+        """qsa_pool then qsa_select in one call (one launch when no block completes); ik and iq in one dtype."""
+        self._check(self.lib.qwattn_qsa_index(
+            self.h, _stream(stream), _ptr(ik), _ptr(iq), _DT[iq.dtype], _ptr(k_gamma), _ptr(q_gamma), iq.shape[1],
+            iq.shape[2], cr, budget, _ptr(raw), _ptr(pooled), cap, pos, n, _ptr(mask),
+            0 if mask is None else mask.shape[-1], _ptr(key_bits), 0 if key_bits is None else key_bits.shape[-1]))
 
     def qsa_key_bits(self, mask, cr, pos, n, key_bits, stream=None):
         """Per-key visibility bits [n, kb_words] from a block mask [n, mask_words] (shaders/attention.comp:35-43)."""

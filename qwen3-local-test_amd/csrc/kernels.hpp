@@ -143,6 +143,8 @@ struct QsaSelectArgs {
     int* cnt;             // [n] arrival counters, zero between launches
     unsigned* mask;       // [n][mask_words] block bitmask, or NULL
     unsigned* kbits;      // [n][kb_words] key visibility bits, or NULL
+    const void* ik;       // with raw: the tokens' raw indexer keys [n][ID] (in_dtype), appended by the launch
+    float* raw;           // [>= pos+n][ID] the raw key cache, or NULL (no append)
     int mask_words, kb_words, stride;
     int pos, n, IH, ID, CR, top, R;
     float eps;

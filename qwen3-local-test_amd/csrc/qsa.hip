@@ -378,6 +378,8 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     const int c = blockIdx.x, t = blockIdx.y;
     const int p = a.pos + t, nblk = (p + 1) / a.CR, ID = a.ID;
     const int kb_words = a.kb_words;
+    if (a.raw != nullptr && c == 0)  // the token's raw key into the cache (no block completes in this call)
+        for (int d = tid; d < ID; d += kQsaThreads) a.raw[(size_t)p * ID + d] = load_in<IN_DT>(a.ik, (size_t)t * ID + d);
     if (nblk <= a.top) {  // dense: every key visible
         if (c == 0) {
             if (a.mask)

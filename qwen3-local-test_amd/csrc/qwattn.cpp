@@ -891,10 +891,56 @@ int qwattn_qsa_select(qwattn_ctx* c, void* stream, const void* iq, int in_dtype,
         qw::QsaSelectArgs a{(const char*)iq + (size_t)t0 * idx_heads * idx_dim * (in_dtype == QWATTN_F32 ? 4 : 2),
                             q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt,
                             mask ? mask + (size_t)t0 * mask_words : nullptr,
-                            key_bits ? key_bits + (size_t)t0 * kb_words : nullptr, mask_words, kb_words, stride,
-                            pos + t0, nt, idx_heads, idx_dim, cr, budget / cr, g.rope_dim, g.rms_eps};
+                            key_bits ? key_bits + (size_t)t0 * kb_words : nullptr, nullptr, nullptr, mask_words,
+                            kb_words, stride, pos + t0, nt, idx_heads, idx_dim, cr, budget / cr, g.rope_dim,
+                            g.rms_eps};
         HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
     }
+    return QWATTN_OK;
+}
+
+int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq, int in_dtype, const float* k_gamma,
+                     const float* q_gamma, int idx_heads, int idx_dim, int cr, int budget, float* raw, float* pooled,
+                     int cap, int pos, int n, uint32_t* mask, int mask_words, uint32_t* key_bits, int kb_words) {
+    if (!c) return QWATTN_EINVAL;
+    if (!ik || !k_gamma || !raw) return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: null pointer");
+    if (n <= 0 || pos < 0 || pos + n > cap || cap > c->cfg.max_ctx)
+        return fail(c, QWATTN_ERANGE, "qwattn_qsa_index: positions [%d, %d) beyond the capacity %d (max_ctx %d)", pos,
+                    pos + n, cap, c->cfg.max_ctx);
+    const int nmax = (pos + n) / std::max(cr, 1);
+    const int per = (int)std::max<size_t>(1, kQsaScoreBytes / ((size_t)std::max(1, nmax) * sizeof(float)));
+    if (cr < 2 || nmax != pos / cr || n > per) {
+        // a block completes (or the tokens take several select launches): the pooling launch, then the select
+        if (int rc = qwattn_qsa_pool(c, stream, ik, in_dtype, k_gamma, idx_dim, cr, raw, pooled, cap, pos, n)) return rc;
+        return qwattn_qsa_select(c, stream, iq, in_dtype, q_gamma, idx_heads, idx_dim, cr, budget, pooled, pos, n,
+                                 mask, mask_words, key_bits, kb_words);
+    }
+    // no block completes: nothing to pool, and the select launch appends the raw keys itself
+    if (!iq || !q_gamma || !pooled || (!mask && !key_bits))
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: null pointer");
+    if (in_dtype != QWATTN_F32 && in_dtype != QWATTN_BF16) return fail(c, QWATTN_EINVAL, "in_dtype %d", in_dtype);
+    const qwattn_config& g = c->cfg;
+    if (idx_dim <= 0 || idx_dim % 64 || idx_dim > 256 || idx_dim < g.rope_dim || idx_heads <= 0 ||
+        idx_heads * idx_dim > 8192)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: %d heads of %d dims (idx_dim a multiple of 64, <= 256, >= "
+                    "rope_dim %d; heads x dims <= 8192)", idx_heads, idx_dim, g.rope_dim);
+    if (budget <= 0 || budget % cr)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: budget %d with compress ratio %d (a positive multiple)",
+                    budget, cr);
+    if (n > g.max_tokens) return fail(c, QWATTN_ERANGE, "qwattn_qsa_index: n %d > max_tokens %d", n, g.max_tokens);
+    if ((nmax + 31) / 32 > qw::qsa_mask_lds_words())
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: %d complete blocks exceed the %d a launch holds", nmax,
+                    32 * qw::qsa_mask_lds_words());
+    if (mask && mask_words * 32 < nmax)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: mask_words %d < %d blocks / 32", mask_words, nmax);
+    if (key_bits && kb_words * 32 < pos + n)
+        return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: kb_words %d < %d keys / 32", kb_words, pos + n);
+    if (int rc = take_wait_error(c)) return rc;
+    DeviceGuard dg(c->device);
+    qw::QsaSelectArgs a{iq, q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, mask, key_bits, ik, raw, mask_words,
+                        kb_words, std::max(1, nmax), pos, n, idx_heads, idx_dim, cr, budget / cr, g.rope_dim,
+                        g.rms_eps};
+    HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
     return QWATTN_OK;
 }
 

@@ -126,6 +126,49 @@ def test_qsa_indexer_matches_oracle(qw, oracle, name):
     ctx.close()
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_qsa_index_equals_pool_then_select(qw, dt):
+    """qsa_index (one launch when no block completes, the select appending the raw keys) leaves the raw and
+    pooled arrays, the mask and the key bits bit for bit as qsa_pool then qsa_select do, over a call sequence
+    with and without completed blocks (blocks of 4, 8,192+ of them)."""
+    qs = QsaShape(4, 128, 4, 2048, 64)
+    max_ctx = 32800
+    calls = [(0, 32768, 0), (32768, 1, 1), (32769, 1, 1), (32770, 1, 1), (32771, 1, 1), (32772, 3, 1), (32775, 8, 1)]
+    tot = sum(c[1] for c in calls)
+    iq, ik, qg, kg = qsa_inputs(57, tot, qs)
+    tdt = torch.float32 if dt == "f32" else torch.bfloat16
+    ctx = _ctx(qw, max_ctx, R=qs.R)
+    mw = qs.mask_words(max_ctx)
+    arrs = [(torch.zeros((max_ctx, qs.ID), device=DEV), torch.zeros((max_ctx // qs.CR + 1, qs.ID), device=DEV))
+            for _ in range(2)]
+    qg_d, kg_d = dev(qg), dev(kg)
+    row = 0
+    for pos, n, sel in calls:
+        print(f"qsa_index {dt}: pos={pos} n={n} completes={(pos + n) // qs.CR != pos // qs.CR}", flush=True)
+        ik_d, iq_d = dev(ik[row:row + n]).to(tdt), dev(iq[row:row + n]).to(tdt)
+        kw = (pos + n + 31) // 32
+        outs = []
+        for k, (raw, pooled) in enumerate(arrs):
+            mask = torch.full((n, mw), -1, dtype=torch.int32, device=DEV)
+            kbits = torch.full((n, kw), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+            if not sel:
+                ctx.qsa_pool(ik_d, kg_d, qs.CR, raw, pooled, max_ctx, pos, n)
+            elif k == 0:
+                ctx.qsa_pool(ik_d, kg_d, qs.CR, raw, pooled, max_ctx, pos, n)
+                ctx.qsa_select(iq_d, qg_d, qs.CR, qs.budget, pooled, pos, n, mask, kbits)
+            else:
+                ctx.qsa_index(ik_d, iq_d, kg_d, qg_d, qs.CR, qs.budget, raw, pooled, max_ctx, pos, n, mask, kbits)
+            outs.append((host(mask), host(kbits)))
+        ctx.sync_status()
+        if sel:
+            assert np.array_equal(outs[0][0], outs[1][0]), f"mask at pos {pos}"
+            assert np.array_equal(outs[0][1], outs[1][1]), f"key bits at pos {pos}"
+        assert np.array_equal(host(arrs[0][0]), host(arrs[1][0])), f"raw keys at pos {pos}"
+        assert np.array_equal(host(arrs[0][1]), host(arrs[1][1])), f"pooled keys at pos {pos}"
+        row += n
+    ctx.close()
+
+
 def test_qsa_key_bits_from_mask(qw):
     import oracle as orc
     r = np.random.default_rng(42)
