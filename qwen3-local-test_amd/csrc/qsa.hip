@@ -219,29 +219,34 @@ __device__ __forceinline__ int block_excl_scan(int x, int* s_tot) {
 // where the count of larger keys reaches the number still needed.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int KR>
+template <int KR, bool COH>
 __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
                                               unsigned* s_mask, int* s_misc, int* s_scan, unsigned* s_hist) {
+    constexpr int AUX = COH ? kScDevice : 0;  // device-coherent loads in the scoring launch itself
     constexpr int NB = 2048;  // bins of a pass
     static_assert(NB == 2 * kQsaThreads, "two bins a thread");
     static_assert(KR == 0 || KR == 8 || KR == 16 || KR == 32 || KR == 64, "keys a thread");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int per = KR > 0 ? KR : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
     const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
-    auto load = [&](int b) -> unsigned { return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, kScDevice); };
+    auto load = [&](int b) -> unsigned { return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, AUX); };
     unsigned kr[KR > 0 ? KR : 1];
     unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
     if constexpr (KR > 0) {
-        // every load issued before any is used; keys past nblk are never counted (the buffer reads as 0 past
-        // its end)
+        // every load issued before any is used. A block past nblk holds the key ~0u: scores are >= +0, so no
+        // real key has bit 31 and that key never matches a prefix, equals the threshold or counts in the
+        // maximum (no per-key range test, whose lane masks would stay live through every pass)
 #pragma unroll
         for (int i = 0; i < KR; i += 4) {
-            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (tid * KR + i) * 4, 0, kScDevice));
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (tid * KR + i) * 4, 0, AUX));
             kr[i] = v[0], kr[i + 1] = v[1], kr[i + 2] = v[2], kr[i + 3] = v[3];
         }
+        const int nv = hi - lo;  // this thread's blocks below nblk
 #pragma unroll
-        for (int i = 0; i < KR; i++)
-            if (lo + i < hi) kmin = min(kmin, kr[i]), kmax = max(kmax, kr[i]);
+        for (int i = 0; i < KR; i++) {
+            kr[i] = i < nv ? kr[i] : 0xFFFFFFFFu;
+            kmin = min(kmin, kr[i]), kmax = max(kmax, kr[i] >> 31 ? 0u : kr[i]);
+        }
     } else {
         for (int b = lo; b < hi; b++) {
             const unsigned k = load(b);
@@ -275,8 +280,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
         };
         if constexpr (KR > 0) {
 #pragma unroll
-            for (int i = 0; i < KR; i++)
-                if (lo + i < hi) count(kr[i]);
+            for (int i = 0; i < KR; i++) count(kr[i]);
         } else {
             for (int b = lo; b < hi; b++) count(load(b));
         }
@@ -309,7 +313,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     int eq = 0;
     if constexpr (KR > 0) {
 #pragma unroll
-        for (int i = 0; i < KR; i++) eq += lo + i < hi && (kr[i] & fmask) == prefix;
+        for (int i = 0; i < KR; i++) eq += (kr[i] & fmask) == prefix;
     } else {
         for (int b = lo; b < hi; b++) eq += (load(b) & fmask) == prefix;
     }
@@ -323,7 +327,8 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     if constexpr (KR == 8 || KR == 16) {
         unsigned bits = 0u;
 #pragma unroll
-        for (int i = 0; i < KR; i++) bits |= (unsigned)(lo + i < hi && selected(kr[i])) << i;
+        for (int i = 0; i < KR; i++) bits |= (unsigned)selected(kr[i]) << i;
+        bits &= hi - lo >= KR ? (1u << KR) - 1u : (1u << (hi - lo)) - 1u;  // no bits past nblk
         // the word of blocks [32 (tid / q), + 32), q = 32 / KR threads: their parts OR-ed across the group
         constexpr int Q = 32 / KR;
         unsigned wv = bits << (KR * (tid & (Q - 1)));
@@ -335,7 +340,9 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
         for (int w = 0; w < KR / 32; w++) {
             unsigned bits = 0u;
 #pragma unroll
-            for (int i = 0; i < 32; i++) bits |= (unsigned)(lo + 32 * w + i < hi && selected(kr[32 * w + i])) << i;
+            for (int i = 0; i < 32; i++) bits |= (unsigned)selected(kr[32 * w + i]) << i;
+            const int nvw = hi - lo - 32 * w;  // this word's blocks below nblk
+            bits &= nvw >= 32 ? 0xFFFFFFFFu : (nvw > 0 ? (1u << nvw) - 1u : 0u);
             if (tid * (KR / 32) + w < nmw) s_mask[tid * (KR / 32) + w] = bits;
         }
     } else {
@@ -362,8 +369,15 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
 // Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [64 c, 64 c + 64) of token t; the last of
 // the token's workgroups to arrive selects. A token that selects nothing has its rows written by workgroup
 // (0, t).
-template <int IN_DT, int KR>
-__global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
+// MODE 0: score, then the last workgroup of each token selects (device-coherent score reads). For many
+// blocks (64 keys a thread and more) the two run as two launches instead: MODE 1 scores only, MODE 2 (one
+// workgroup a token) selects, reading the scores with plain loads (the launch boundary makes them visible):
+// the device-coherent reads of 256 KB of scores from one CU, and the select's registers in every scoring
+// workgroup, cost more than the second launch.
+// (one workgroup a CU at most in every use: the register budget of 4 waves a SIMD, 128 registers, is the
+// kernel's to use)
+template <int IN_DT, int KR, int MODE, int CH = kQsaChunk>
+__global__ __launch_bounds__(kQsaThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_qsa_select(QsaSelectArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     unsigned* s_mask = reinterpret_cast<unsigned*>(smem);  // [kQsaMaskLds] the token's selection
     int* s_misc = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [16]
@@ -381,7 +395,7 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     if (a.raw != nullptr && c == 0)  // the token's raw key into the cache (no block completes in this call)
         for (int d = tid; d < ID; d += kQsaThreads) a.raw[(size_t)p * ID + d] = load_in<IN_DT>(a.ik, (size_t)t * ID + d);
     if (nblk <= a.top) {  // dense: every key visible
-        if (c == 0) {
+        if (c == 0 && MODE != 1) {
             if (a.mask)
                 for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = 0xFFFFFFFFu;
             if (a.kbits)
@@ -389,23 +403,30 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
         }
         return;
     }
-    const int ct = (nblk + kQsaChunk - 1) / kQsaChunk;  // this token's workgroups
+    const int ct = (nblk + CH - 1) / CH;  // this token's workgroups (CH blocks each)
     if (c >= ct) return;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
+                                                                        a.stride * 4, 0x00020000);
+    if constexpr (MODE == 2) {
+        select_blocks<KR, false>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist);
+        return;
+    }
 
-    // this chunk's pooled keys, 16 lanes a key, DL = ID / 16 consecutive dims a lane: loaded first, so that
-    // their latency hides behind the query heads' prologue
-    static_assert(kQsaChunk == kQsaThreads / 16, "one key per 16-lane group");
+    // this chunk's pooled keys, 16 lanes a key (RB rounds of 64 keys), DL = ID / 16 consecutive dims a lane:
+    // loaded first, so that their latency hides behind the query heads' prologue
+    constexpr int RB = CH / (kQsaThreads / 16);
+    static_assert(RB * (kQsaThreads / 16) == CH, "whole rounds of one key per 16-lane group");
     const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
-    const int bc0 = c * kQsaChunk, bc1 = min(nblk, bc0 + kQsaChunk);
-    const int b = bc0 + grp;
-    float kv[16];
-    {
-        const float* pk = a.pooled + (size_t)min(b, bc1 - 1) * ID + sub * DL;  // past the chunk: a valid row
+    const int bc0 = c * CH, bc1 = min(nblk, bc0 + CH);
+    float kv[RB][16];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const float* pk = a.pooled + (size_t)min(bc0 + rr * (kQsaThreads / 16) + grp, bc1 - 1) * ID + sub * DL;
 #pragma unroll
         for (int i = 0; i < 16; i += 4)
-            if (i < DL) {  // DL <= 16: the host keeps ID <= 256
+            if (i < DL) {  // DL <= 16: the host keeps ID <= 256 (past the chunk: a valid row, score not stored)
                 const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
-                kv[i] = v[0], kv[i + 1] = v[1], kv[i + 2] = v[2], kv[i + 3] = v[3];
+                kv[rr][i] = v[0], kv[rr][i + 1] = v[1], kv[rr][i + 2] = v[2], kv[rr][i + 3] = v[3];
             }
     }
     // the query heads: RMS-normed (gamma as stored), rotated to p; wave w takes heads w, w + 16, ...
@@ -428,21 +449,22 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     __syncthreads();
 
     // the chunk's scores: sum over the heads of relu(q_h . key), the dot products summed over each 16-lane row
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
-                                                                        a.stride * 4, 0x00020000);
-    {
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const int b = bc0 + rr * (kQsaThreads / 16) + grp;
         float sc = 0.f;
         for (int h = 0; h < a.IH; h++) {
             const float* qh = s_q + h * ID + sub * DL;
             float dp = 0.f;
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                if (i < DL) dp = __builtin_fmaf(qh[i], kv[i], dp);
+                if (i < DL) dp = __builtin_fmaf(qh[i], kv[rr][i], dp);
             dp = sum16(dp);
             sc += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
         }
         if (sub == 0 && b < bc1) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc), rs, b * 4, 0, kScDevice);
     }
+    if constexpr (MODE == 1) return;
     // arrive: the stores are acknowledged (device-coherent) before the counter moves
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -455,7 +477,7 @@ __global__ __launch_bounds__(kQsaThreads) void k_qsa_select(QsaSelectArgs a) {
     if (s_misc[0] != ct - 1) return;
 
     // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
-    select_blocks<KR>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist);  // the host sizes KR for the call's last token
+    select_blocks<KR, true>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist);  // the host sizes KR for the call's last token
 }
 
 // ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
@@ -487,30 +509,39 @@ static int select_kr(int nmax) {
     return 0;
 }
 
-template <int IN_DT, int KR>
+template <int IN_DT, int KR, int MODE, int CH = kQsaChunk>
 static hipError_t launch_select_kr(const QsaSelectArgs& a, size_t shm, dim3 grid, hipStream_t s) {
     static std::atomic<uint64_t> raised{0};  // per device: dynamic LDS limit raised (bit per device)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load(std::memory_order_acquire) & bit)) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_qsa_select<IN_DT, KR>,
+        const hipError_t e = hipFuncSetAttribute((const void*)k_qsa_select<IN_DT, KR, MODE, CH>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((k_qsa_select<IN_DT, KR>), grid, dim3(kQsaThreads), shm, s, a);
+    hipLaunchKernelGGL((k_qsa_select<IN_DT, KR, MODE, CH>), grid, dim3(kQsaThreads), shm, s, a);
     return hipGetLastError();
 }
 
 template <int IN_DT>
 static hipError_t launch_select_dt(const QsaSelectArgs& a, int kr, size_t shm, dim3 grid, hipStream_t s) {
     switch (kr) {
-        case 8: return launch_select_kr<IN_DT, 8>(a, shm, grid, s);
-        case 16: return launch_select_kr<IN_DT, 16>(a, shm, grid, s);
-        case 32: return launch_select_kr<IN_DT, 32>(a, shm, grid, s);
-        case 64: return launch_select_kr<IN_DT, 64>(a, shm, grid, s);
-        default: return launch_select_kr<IN_DT, 0>(a, shm, grid, s);
+        case 8: return launch_select_kr<IN_DT, 8, 0>(a, shm, grid, s);
+        case 16: return launch_select_kr<IN_DT, 16, 0>(a, shm, grid, s);
+        case 32: return launch_select_kr<IN_DT, 32, 0>(a, shm, grid, s);
+        default: {
+            // many blocks: scoring (256 blocks a workgroup), then a select launch of one workgroup a token
+            // (which does not append)
+            constexpr int CH1 = 4 * kQsaChunk;
+            const int nmax = (a.pos + a.n) / a.CR;
+            if (hipError_t e = launch_select_kr<IN_DT, 8, 1, CH1>(a, shm, dim3((nmax + CH1 - 1) / CH1, grid.y), s)) return e;
+            QsaSelectArgs b = a;
+            b.raw = nullptr;
+            const dim3 g1(1, grid.y);
+            return kr == 64 ? launch_select_kr<IN_DT, 64, 2>(b, shm, g1, s) : launch_select_kr<IN_DT, 0, 2>(b, shm, g1, s);
+        }
     }
 }
 
