@@ -296,6 +296,22 @@ int qwattn_qsa_index(qwattn_ctx* ctx, void* stream, const void* ik, const void* 
                      float* raw, float* pooled, int cap, int pos, int n, uint32_t* mask, int mask_words,
                      uint32_t* key_bits, int kb_words);
 
+/* The projections either side of the attention layer: Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856) on its
+ * matrix-vector pipelines q4_matmul_q8 / q4_matmul_f32 (shaders/q4_matmul.comp, codecs C_Q8 / C_F32 of
+ * shaders/q4_codec.glsl). y[t][r] (row stride y_stride) = sum_c W[r][c] x[t][c] (row stride x_stride) for
+ * t < n, r < rows, with W planar Q8_0 when q8 != 0 (w: int8 [rows][cols], s: float [rows][cols/32], one
+ * scale per 32 consecutive weights of a row, as qwattn_q8_unpack writes them) or float [rows][cols] (s
+ * unused); post 1 then applies y = silu(y * post_scale) (the shader's `post`). fp32 arithmetic. cols a
+ * multiple of 32 (q8) or 16 (f32); x_stride >= cols and a multiple of 4; y_stride >= rows; w and x 16-byte
+ * aligned. */
+int qwattn_mat(qwattn_ctx* ctx, void* stream, const void* w, const float* s, int q8, int rows, int cols,
+               const float* x, int x_stride, float* y, int y_stride, int n, int post, float post_scale);
+
+/* GGUF Q8_0 rows (per 32 weights: an IEEE binary16 scale, then 32 int8) to the planar form qwattn_mat takes
+ * (host memory, no GPU): the reference's upload repacking, unpack_q8_row (src/qwen4_vk.cpp:98-106). cols a
+ * multiple of 32. Returns QWATTN_OK or QWATTN_EINVAL. */
+int qwattn_q8_unpack(const uint8_t* blocks, int rows, int cols, int8_t* w, float* s);
+
 /* The per-key visibility bits from a block mask in the reference's format (mask[t][mask_words], as the
  * reference's attention_qsa_kv16 pipeline takes it: shaders/attention.comp:35-43): bit j of key_bits[t] is
  * set when block j / cr has its bit set or j >= ((pos + t + 1) / cr) * cr. */

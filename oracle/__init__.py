@@ -81,7 +81,8 @@ class Oracle:
         lib.orc_qsa_select.argtypes = [_F, _F, _F, _U, _I, _F, _I, _I, _I, _I, _I, _I, _I, _I, ctypes.c_double,
                                        ctypes.c_float]
         lib.orc_attention_qsa.argtypes = [_F, _I, _F, _F, _F, _F, _I, _I, _I, _I, _I, _U, _I, _I]
-        for f in ("orc_inv_freq", "orc_rope_table", "orc_rms_mul", "orc_rmsnorm_one_plus", "orc_rope",
+        lib.orc_mat.argtypes = [ctypes.c_void_p, _F, _F, _I, _I, _I, _F, _I, _F, _I, _I, _I, ctypes.c_float]
+        for f in ("orc_mat", "orc_inv_freq", "orc_rope_table", "orc_rms_mul", "orc_rmsnorm_one_plus", "orc_rope",
                   "orc_qk_norm_rope", "orc_attention", "orc_attention_split", "orc_attention_f64",
                   "orc_qk_norm_rope_f64", "orc_qsa_pool", "orc_qsa_select", "orc_attention_qsa"):
             getattr(lib, f).restype = None
@@ -89,6 +90,24 @@ class Oracle:
 
     def set_threads(self, n):
         return self.lib.orc_set_threads(n)
+
+    def mat(self, x, w8=None, s=None, wf=None, post=0, post_scale=0.0):
+        """Y [n, rows] = X [n, cols] W^T (Qwen4Vulkan::mat): planar Q8 (w8 int8 [rows, cols], s [rows, cols/32])
+        or f32 wf [rows, cols]; post 1 applies silu(y * post_scale)."""
+        x = _f32(x)
+        n, cols = x.shape
+        q8 = w8 is not None
+        if q8:
+            w8 = np.ascontiguousarray(w8, dtype=np.int8)
+            s = _f32(s)
+            rows = w8.shape[0]
+        else:
+            wf = _f32(wf)
+            rows = wf.shape[0]
+        y = np.zeros((n, rows), np.float32)
+        self.lib.orc_mat(w8.ctypes.data if q8 else None, _fp(s) if q8 else None, None if q8 else _fp(wf), int(q8),
+                         rows, cols, _fp(x), cols, _fp(y), rows, n, post, post_scale)
+        return y
 
     def dot(self, a, b):
         a, b = _f32(a), _f32(b)
@@ -254,7 +273,18 @@ class RefQsa:
         lib.ref_qsa_run.argtypes = [_I, _I, _I, _I, _I, ctypes.c_float, ctypes.c_float, _F, _F, _I, _I, _I, _IP, _IP,
                                     _F, _F, ctypes.POINTER(ctypes.c_uint32), _I]
         lib.ref_qsa_run.restype = _I
+        lib.ref_mat_q8.argtypes = [ctypes.c_void_p, _I, _I, _F, _I, _F, _I]
+        lib.ref_mat_q8.restype = _I
         self.lib = lib
+
+    def mat_q8(self, blocks, rows, cols, x, threads=4):
+        """Y [n, rows] = X [n, cols] W^T through the reference's CPU path (gq::run_jobs) for W in GGUF Q8_0
+        blocks (uint8 [rows, cols/32*34])."""
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        x = _f32(x)
+        y = np.zeros((x.shape[0], rows), np.float32)
+        assert self.lib.ref_mat_q8(blocks.ctypes.data, rows, cols, _fp(x), x.shape[0], _fp(y), threads) == 0
+        return y
 
     def run(self, calls, iq, ik, q_gamma, k_gamma, cr, budget, R, theta, eps, max_ctx, mask_words, threads=4):
         """calls: [(pos, n), ...] in order; iq [sum n, IH, ID], ik [sum n, ID] in call order ->

@@ -19,6 +19,9 @@
 //   - QSA indexer        src/qwen4_qsa.h:38-54 (pooled block keys), :58-91 (block selection), the
 //                        bitmask of src/qwen4_vk.cpp:952-960, and the masked attention of
 //                        src/qwen4_cpu.cpp:325-344 (runs of visible keys) / shaders/attention.comp:35-43
+//   - projections        Y = X W^T of Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856, shaders/q4_matmul.comp with
+//                        the C_Q8 / C_F32 codecs of shaders/q4_codec.glsl): planar Q8_0 (int8 weights, one
+//                        f32 scale per 32, src/qwen4_vk.cpp:98-106) or f32 rows, optional silu(y * scale)
 // plus an fp64 brute-force attention used to write golden fixtures.
 //
 // Parity pins for every function here live in tests/test_oracle.py (closed forms, invariants,
@@ -396,6 +399,29 @@ void orc_attention_qsa(const float* q, int q_stride, const float* qg_gate, const
             }
         }
     });
+}
+
+// Projection Y[n][y_stride] = X[n][x_stride] W^T (Qwen4Vulkan::mat, src/qwen4_vk.cpp:848-856; per element as
+// shaders/q4_matmul.comp with q4_codec.glsl's C_Q8 / C_F32): row r of W is w8[r][cols] * s[r][cols/32] (q8) or
+// wf[r][cols] (f32); each output is accumulated in double over the dequantized weights and rounded to float
+// once (fp32-order-independent); post 1: y = silu(y * post_scale) as the shader applies it.
+void orc_mat(const int8_t* w8, const float* s, const float* wf, int q8, int rows, int cols, const float* x,
+             int x_stride, float* y, int y_stride, int n, int post, float post_scale) {
+    for (int t = 0; t < n; t++)
+        for (int r = 0; r < rows; r++) {
+            double acc = 0.0;
+            for (int c = 0; c < cols; c++) {
+                const float wv = q8 ? (float)w8[(size_t)r * cols + c] * s[(size_t)r * (cols / 32) + c / 32]
+                                    : wf[(size_t)r * cols + c];
+                acc += (double)wv * (double)x[(size_t)t * x_stride + c];
+            }
+            float v = (float)acc;
+            if (post == 1) {
+                const float u = v * post_scale;
+                v = u / (1.0f + std::exp(-u));
+            }
+            y[(size_t)t * y_stride + r] = v;
+        }
 }
 
 }  // extern "C"

@@ -1,5 +1,8 @@
 // CPU ORACLE (reference build) — test infrastructure only, see oracle.cpp.
 //
+// Also drives the reference's CPU projection (gq::run_jobs over a GGUF Q8_0 matrix, src/quant.cpp:343-...),
+// which the planar Q8 projection restated in oracle.cpp is pinned against.
+//
 // Runs the reference's own QSA indexer (class QsaIndexer, src/qwen4_qsa.h:17-115, header-only) compiled
 // in place, with its projections (gq::run_jobs, src/quant.cpp) and primitives (src/cpu_kernels.cpp).
 // The indexer takes the layer's block input xn[n][hidden] and projects it with idx_q / idx_k; here those
@@ -80,6 +83,26 @@ int ref_qsa_run(int IH, int ID, int CR, int budget, int R, float theta, float ep
         }
         row += n;
     }
+    return 0;
+}
+
+// Y[n][rows] = X[n][cols] W^T for W in GGUF Q8_0 blocks (34 bytes per 32 weights: f16 scale, 32 int8), through
+// the reference's own CPU path (gq::run_jobs on a thread pool of `threads`). Returns 0, or -1 on bad shapes.
+int ref_mat_q8(const uint8_t* blocks, int rows, int cols, const float* x, int n, float* y, int threads) {
+    if (rows <= 0 || cols <= 0 || cols % 32 || n <= 0) return -1;
+    gq::GMat m;
+    m.type = GType::Q8_0;
+    m.data = blocks;
+    m.rows = rows;
+    m.cols = cols;
+    m.row_bytes = (size_t)cols / 32 * 34;
+    ThreadPool pool(threads);
+    gq::Job j;
+    j.m = &m;
+    j.x = x;
+    j.y = y;
+    j.n = n;
+    gq::run_jobs(pool, {j});
     return 0;
 }
 

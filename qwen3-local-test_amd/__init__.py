@@ -71,6 +71,8 @@ def load_library():
         "qwattn_qsa_pool": [_P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I],
         "qwattn_qsa_select": [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I],
         "qwattn_qsa_index": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P, _I],
+        "qwattn_mat": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P, _I, _I, _I, ctypes.c_float],
+        "qwattn_q8_unpack": [_P, _I, _I, _P, _P],
         "qwattn_qsa_key_bits": [_P, _P, _P, _I, _I, _I, _I, _P, _I],
         "qwattn_attend_partial_qsa": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
         "qwattn_decode_qsa": [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P],
@@ -89,6 +91,21 @@ def load_library():
     lib.qwattn_last_error.restype = ctypes.c_char_p
     _lib = lib
     return lib
+
+
+def q8_unpack(blocks, rows, cols):
+    """GGUF Q8_0 rows (uint8 [rows, cols/32*34]) to the planar pair qwattn_mat takes: int8 [rows, cols] and
+    float32 scales [rows, cols/32] (numpy, host memory), through the library's qwattn_q8_unpack."""
+    import numpy as np
+    lib = load_library()
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    w = np.zeros((rows, cols), np.int8)
+    s = np.zeros((rows, cols // 32), np.float32)
+    rc = lib.qwattn_q8_unpack(ctypes.c_void_p(b.ctypes.data), rows, cols, ctypes.c_void_p(w.ctypes.data),
+                              ctypes.c_void_p(s.ctypes.data))
+    if rc != OK:
+        raise QwattnError(rc, "qwattn_q8_unpack: bad shape")
+    return w, s
 
 
 def header_functions():
@@ -260,6 +277,14 @@ class Attention:
             self.h, _stream(stream), _ptr(ik), _ptr(iq), _DT[iq.dtype], _ptr(k_gamma), _ptr(q_gamma), iq.shape[1],
             iq.shape[2], cr, budget, _ptr(raw), _ptr(pooled), cap, pos, n, _ptr(mask),
             0 if mask is None else mask.shape[-1], _ptr(key_bits), 0 if key_bits is None else key_bits.shape[-1]))
+
+    def mat(self, x, y, w, s=None, post=0, post_scale=0.0, stream=None):
+        """y [n, >= rows] = x [n, >= cols] W^T (Qwen4Vulkan::mat): W planar Q8 (w int8 [rows, cols] with s
+        [rows, cols/32]) or float32 w [rows, cols]; post 1 applies silu(y * post_scale)."""
+        q8 = s is not None
+        rows, cols = w.shape
+        self._check(self.lib.qwattn_mat(self.h, _stream(stream), _ptr(w), _ptr(s), int(q8), rows, cols, _ptr(x),
+                                        x.stride(0), _ptr(y), y.stride(0), x.shape[0], post, post_scale))
 
     def qsa_key_bits(self, mask, cr, pos, n, key_bits, stream=None):
         """Per-key visibility bits [n, kb_words] from a block mask [n, mask_words] (shaders/attention.comp:35-43)."""

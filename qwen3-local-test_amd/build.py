@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "lib", "libqwattn.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["norm_rope.hip", "decode.hip", "prefill.hip", "qsa.hip", "qwattn.cpp"]
+SOURCES = ["norm_rope.hip", "decode.hip", "prefill.hip", "qsa.hip", "mat.hip", "qwattn.cpp"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 

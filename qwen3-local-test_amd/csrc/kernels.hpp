@@ -160,4 +160,15 @@ struct QsaKeyBitsArgs {
 };
 hipError_t launch_qsa_key_bits(const QsaKeyBitsArgs& a, hipStream_t s);
 
+// Projection Y = X W^T (csrc/mat.hip)
+struct MatArgs {
+    const void* w;     // planar Q8: int8 [rows][cols]; f32: float [rows][cols]
+    const float* s;    // planar Q8: [rows][cols / 32] scales; f32: unused
+    const float* x;    // [n][x_stride]
+    float* y;          // [n][y_stride]
+    int rows, cols, n, x_stride, y_stride, post;
+    float post_scale;  // post 1: y = silu(y * post_scale)
+};
+hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s);
+
 }  // namespace qw

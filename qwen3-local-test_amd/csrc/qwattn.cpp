@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -941,6 +942,56 @@ int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq
                         kb_words, std::max(1, nmax), pos, n, idx_heads, idx_dim, cr, budget / cr, g.rope_dim,
                         g.rms_eps};
     HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+}  // extern "C"
+
+// IEEE 754 binary16 bits to float: sign, 5-bit exponent (bias 15), 10-bit fraction; subnormals scale the
+// fraction by 2^-24, exponent 31 is inf / NaN.
+static float half_bits_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, f = h & 1023u;
+    float v;
+    if (e == 0) v = std::ldexp((float)f, -24);
+    else if (e == 31) v = f ? NAN : INFINITY;
+    else v = std::ldexp((float)(f | 1024u), (int)e - 25);
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    b |= sign;
+    std::memcpy(&v, &b, 4);
+    return v;
+}
+
+extern "C" {
+
+int qwattn_mat(qwattn_ctx* c, void* stream, const void* w, const float* s, int q8, int rows, int cols, const float* x,
+               int x_stride, float* y, int y_stride, int n, int post, float post_scale) {
+    if (!c) return QWATTN_EINVAL;
+    if (!w || !x || !y || (q8 && !s)) return fail(c, QWATTN_EINVAL, "qwattn_mat: null pointer");
+    if (rows <= 0 || cols <= 0 || n <= 0 || cols % (q8 ? 32 : 16))
+        return fail(c, QWATTN_EINVAL, "qwattn_mat: %d x %d weights (cols a multiple of %d), n %d", rows, cols,
+                    q8 ? 32 : 16, n);
+    if (x_stride < cols || x_stride % 4 || y_stride < rows || post < 0 || post > 1)
+        return fail(c, QWATTN_EINVAL, "qwattn_mat: x_stride %d (>= cols, a multiple of 4), y_stride %d (>= rows), post %d",
+                    x_stride, y_stride, post);
+    if (((uintptr_t)w | (uintptr_t)x) & 15) return fail(c, QWATTN_EINVAL, "qwattn_mat: w and x must be 16-byte aligned");
+    DeviceGuard dg(c->device);
+    qw::MatArgs a{w, s, x, y, rows, cols, n, x_stride, y_stride, post, post_scale};
+    HIP_TRY(c, qw::launch_mat(a, q8 != 0, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
+int qwattn_q8_unpack(const uint8_t* blocks, int rows, int cols, int8_t* w, float* s) {
+    if (!blocks || !w || !s || rows <= 0 || cols <= 0 || cols % 32) return QWATTN_EINVAL;
+    for (int r = 0; r < rows; r++) {
+        const uint8_t* src = blocks + (size_t)r * (cols / 32) * 34;
+        for (int b = 0; b < cols / 32; b++, src += 34) {
+            uint16_t h;
+            std::memcpy(&h, src, 2);
+            s[(size_t)r * (cols / 32) + b] = half_bits_to_float(h);
+            std::memcpy(w + (size_t)r * cols + 32 * b, src + 2, 32);
+        }
+    }
     return QWATTN_OK;
 }
 

@@ -138,3 +138,17 @@ def cache_rows(seed, rows, s, heavy_frac=0.0, heavy_scale=8.0):
         idx = r.choice(rows, size=max(1, int(rows * heavy_frac)), replace=False)
         k[idx] *= heavy_scale
     return k.astype(np.float16), v.astype(np.float16)
+
+
+def q8_blocks(seed, rows, cols, scale=0.02):
+    """A seeded GGUF Q8_0 matrix: blocks uint8 [rows, cols/32*34] (per 32 weights an f16 scale then 32 int8),
+    and its planar form as the GPU path takes it (src/qwen4_vk.cpp:98-106): w8 int8 [rows, cols] and
+    s f32 [rows, cols/32] (the f16 scales widened)."""
+    r = np.random.default_rng(seed)
+    nb = cols // 32
+    w8 = r.integers(-127, 128, size=(rows, cols), dtype=np.int16).astype(np.int8)
+    sc16 = (scale * (0.5 + r.random((rows, nb)))).astype(np.float16)
+    blocks = np.zeros((rows, nb, 34), np.uint8)
+    blocks[:, :, 0:2] = sc16.view(np.uint8).reshape(rows, nb, 2)
+    blocks[:, :, 2:] = w8.view(np.uint8).reshape(rows, nb, 32)
+    return blocks.reshape(rows, nb * 34), w8, sc16.astype(np.float32)

@@ -50,3 +50,24 @@ def test_bad_shapes_rejected_before_any_device_call():
                       ((16, 2, 256, 63), "rope dimension"), ((16, 2, 256, 12), "rope dimension"), ((64, 1, 256, 64), "GQA group")]:
         with pytest.raises(qw.QwattnError, match=pat):
             qw.Attention(*args)
+
+
+def test_q8_unpack_host():
+    """qwattn_q8_unpack (host code, no GPU) turns GGUF Q8_0 rows into the planar int8 weights and f32 scales
+    of src/qwen4_vk.cpp:98-106: the weights byte for byte, each binary16 scale widened exactly (normal,
+    subnormal, zero, negative and infinite scales included); a bad shape is refused."""
+    import numpy as np
+    from common import q8_blocks
+    qw = common.load_package()
+    rows, cols = 5, 96
+    blocks, w8, s = q8_blocks(61, rows, cols)
+    special = np.array([0x0001, 0x03FF, 0x0000, 0x8000, 0xBC00, 0x7C00, 0x7BFF, 0x0400], np.uint16)
+    b = blocks.reshape(rows, cols // 32, 34).copy()
+    b[:, :, 0:2] = np.resize(special, (rows, cols // 32)).view(np.uint8).reshape(rows, cols // 32, 2)
+    w, sc = qw.q8_unpack(b.reshape(rows, -1), rows, cols)
+    assert np.array_equal(w, w8)
+    assert np.array_equal(sc, np.resize(special, (rows, cols // 32)).view(np.float16).astype(np.float32))
+    w, sc = qw.q8_unpack(blocks, rows, cols)
+    assert np.array_equal(w, w8) and np.array_equal(sc, s)
+    lib = qw.load_library()
+    assert lib.qwattn_q8_unpack(None, rows, cols, None, None) == qw.EINVAL

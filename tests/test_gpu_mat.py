@@ -1,0 +1,94 @@
+"""GPU parity of the projection kernel (qwattn_mat: Qwen4Vulkan::mat, src/qwen4_vk.cpp:848-856, on the
+q4_matmul_q8 / q4_matmul_f32 pipelines of shaders/q4_matmul.comp) against the CPU oracle's projection, itself
+pinned against the reference's own CPU path (tests/test_oracle.py: test_mat_q8_matches_reference).
+
+Tolerance: every output is one fp32 dot product in both, summed in different orders, so the bound is relative
+to the magnitude sum |W| |x| of that output: 1e-5 of it (a few fp32 roundings of a 4,096-term sum) plus 1e-6."""
+import numpy as np
+import pytest
+import torch
+
+from common import q8_blocks
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _ctx(qw):
+    return qw.Attention(16, 2, 256, 64, max_ctx=1024, max_tokens=64, max_splits=16)
+
+
+def _check(got, want, w_abs, x):
+    mag = w_abs.astype(np.float64) @ np.abs(x.astype(np.float64)).T  # [rows, n]
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= 1e-5 * mag.T + 1e-6), float((err / (mag.T + 1e-30)).max())
+
+
+# (rows, cols): the attention layer's projections at hidden 2,048 (query + gate, key, value, output), then odd
+# shapes: a partial last workgroup of rows, a column count that leaves lanes idle
+SHAPES = [(8192, 2048), (512, 2048), (2048, 4096), (100, 96), (37, 1056)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("n", [1, 4, 5, 13])
+def test_mat_q8_parity(qw, oracle, rows, cols, n):
+    print(f"mat q8 {rows}x{cols} n={n}", flush=True)
+    blocks, _, _ = q8_blocks(71 + rows + n, rows, cols)
+    w8, s = qw.q8_unpack(blocks, rows, cols)
+    x = np.random.default_rng(72 + n).standard_normal((n, cols)).astype(np.float32)
+    ctx = _ctx(qw)
+    y = torch.full((n, rows), float("nan"), device=DEV)
+    ctx.mat(dev(x), y, dev(w8), dev(s))
+    torch.cuda.synchronize()
+    want = oracle.mat(x, w8=w8, s=s)
+    _check(y.cpu().numpy(), want, np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)), x)
+    ctx.close()
+
+
+@pytest.mark.parametrize("rows,cols,n", [(512, 2048, 1), (300, 48, 6), (2048, 4096, 4)])
+def test_mat_f32_parity(qw, oracle, rows, cols, n):
+    print(f"mat f32 {rows}x{cols} n={n}", flush=True)
+    r = np.random.default_rng(73)
+    w = (0.05 * r.standard_normal((rows, cols))).astype(np.float32)
+    x = r.standard_normal((n, cols)).astype(np.float32)
+    ctx = _ctx(qw)
+    y = torch.full((n, rows), float("nan"), device=DEV)
+    ctx.mat(dev(x), y, dev(w))
+    torch.cuda.synchronize()
+    _check(y.cpu().numpy(), oracle.mat(x, wf=w), np.abs(w), x)
+    ctx.close()
+
+
+def test_mat_strides_and_post(qw, oracle):
+    """Row strides wider than the rows (the reference's x_stride / y_stride), outputs beyond `rows` of each y
+    row untouched, and post 1 = silu(y * post_scale)."""
+    rows, cols, n = 200, 512, 3
+    blocks, _, _ = q8_blocks(74, rows, cols)
+    w8, s = qw.q8_unpack(blocks, rows, cols)
+    x = np.random.default_rng(75).standard_normal((n, cols + 64)).astype(np.float32)
+    ctx = _ctx(qw)
+    xd = dev(x)[:, :cols]
+    y = torch.full((n, rows + 24), 7.0, device=DEV)
+    ctx.mat(xd, y, dev(w8), dev(s), post=1, post_scale=0.37)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = oracle.mat(x[:, :cols], w8=w8, s=s, post=1, post_scale=0.37)
+    _check(got[:, :rows], want, np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)), x[:, :cols])
+    assert np.all(got[:, rows:] == 7.0)
+    ctx.close()
+
+
+def test_mat_rejects_bad_shapes(qw):
+    ctx = _ctx(qw)
+    w = torch.zeros((64, 48), dtype=torch.int8, device=DEV)  # 48 columns: not whole Q8 blocks
+    s = torch.zeros((64, 1), device=DEV)
+    x = torch.zeros((1, 48), device=DEV)
+    y = torch.zeros((1, 64), device=DEV)
+    with pytest.raises(qw.QwattnError):
+        ctx.mat(x, y, w, s)
+    ctx.close()

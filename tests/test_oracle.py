@@ -433,3 +433,43 @@ def test_qsa_key_bits():
                 b = j // cr
                 vis = j >= tail or (int(mask[t, b >> 5]) >> (b & 31)) & 1 == 1
                 assert ((int(bits[t, j >> 5]) >> (j & 31)) & 1) == int(vis), (cr, t, j)
+
+
+# ---- projections (Qwen4Vulkan::mat, shaders/q4_matmul.comp C_Q8 / C_F32) ------------------------------------
+
+from common import q8_blocks  # noqa: E402
+
+
+@pytest.mark.parametrize("rows,cols,n", [(96, 256, 1), (64, 2048, 3), (40, 4096, 8)])
+def test_mat_q8_matches_reference(oracle, rows, cols, n):
+    """The oracle's planar-Q8 projection equals the reference's own CPU projection (gq::run_jobs over the same
+    GGUF Q8_0 blocks, src/quant.cpp, compiled in place) to fp32 rounding: the planar form (int8 weights, f16
+    scales widened) loses nothing, and each output is one dot product."""
+    ref = _ref_qsa()
+    blocks, w8, s = q8_blocks(51 + n, rows, cols)
+    x = np.random.default_rng(52).standard_normal((n, cols)).astype(np.float32)
+    got = oracle.mat(x, w8=w8, s=s)
+    want = ref.mat_q8(blocks, rows, cols, x)
+    mag = np.abs(w8.astype(np.float64) * np.repeat(s, 32, axis=1)) @ np.abs(x.astype(np.float64)).T  # [rows, n]
+    assert np.all(np.abs(got - want) <= 1e-6 * mag.T + 1e-7), np.abs(got - want).max()
+
+
+def test_mat_closed_forms(oracle):
+    """f32 identity and permutation matrices return x (permuted); zero weights return 0; a Q8 row of k with
+    scale 1/k sums x; post 1 is silu(y * scale) of the plain result; the product is linear in x."""
+    r = np.random.default_rng(53)
+    n, cols = 3, 64
+    x = r.standard_normal((n, cols)).astype(np.float32)
+    assert np.array_equal(oracle.mat(x, wf=np.eye(cols, dtype=np.float32)), x)
+    perm = r.permutation(cols)
+    assert np.array_equal(oracle.mat(x, wf=np.eye(cols, dtype=np.float32)[perm]), x[:, perm])
+    assert not np.any(oracle.mat(x, wf=np.zeros((5, cols), np.float32)))
+    w8 = np.full((2, cols), 8, np.int8)
+    s = np.full((2, cols // 32), 0.125, np.float32)
+    assert np.allclose(oracle.mat(x, w8=w8, s=s), np.repeat(x.sum(axis=1, keepdims=True), 2, axis=1), atol=1e-5)
+    wf = r.standard_normal((7, cols)).astype(np.float32)
+    y = oracle.mat(x, wf=wf)
+    u = y * 0.7
+    assert np.allclose(oracle.mat(x, wf=wf, post=1, post_scale=0.7), u / (1 + np.exp(-u)), rtol=1e-6, atol=1e-7)
+    x2 = r.standard_normal((n, cols)).astype(np.float32)
+    assert np.allclose(oracle.mat(2 * x - x2, wf=wf), 2 * y - oracle.mat(x2, wf=wf), rtol=1e-5, atol=1e-5)
