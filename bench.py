@@ -22,7 +22,12 @@ the reference's CPU attention timed on this host's cores over a bounded sample.
 Two QSA workloads (the block-sparse path past the indexer's budget, src/qwen4_vk.cpp:942-984) time the whole
 layer step on the GPU at 32K: pool the new indexer key, select the token's blocks (4 indexer heads of 128
 dims, a budget of 2,048 keys, blocks of 4 or 64 keys), and the one-launch decode over the tiles the
-selection leaves visible; their bytes are the K/V bytes of the visible keys.
+selection leaves visible; their bytes are the K/V bytes of the visible keys. QSA at 256K runs against the
+dense 256K step.
+
+Two projection workloads (proj_q8_n1, proj_q8_n4) time the layer's four projections around the attention
+(Qwen4Vulkan::mat on planar Q8_0 weights: query + gate, key, value, output at hidden 2,048) for one decode
+token and a 4-token verify pass; their bytes are the weights, read once a step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -223,6 +228,61 @@ _SLEEP_PER_MS = None
 KERNEL_BATCHES = 50  # batches of 16 launches timed for the dominant kernel's duration (median reported)
 
 
+class MatWorkload:
+    """The attention layer's four projections (Qwen4Vulkan::mat, src/qwen4_vk.cpp:848-856, on the q4_matmul_q8
+    pipeline) for n tokens at hidden 2,048: query + gate (8,192 x 2,048), key and value (512 x 2,048 each) and
+    output (2,048 x 4,096), planar Q8_0 weights (seeded int8, scales 0.02 x U(0.5, 1.5)); every layer slot has
+    its own weights (30.7 MB a slot), rotated like the K/V caches. Bytes: the weights read once (one byte per
+    weight plus a float scale per 32)."""
+    HIDDEN = 2048
+
+    def __init__(self, qw, name, n, slots, seed=0):
+        import torch
+        self.name, self.n, self.slots = name, n, slots
+        self.shapes = [(NH * 2 * D, self.HIDDEN), (NKV * D, self.HIDDEN), (NKV * D, self.HIDDEN), (self.HIDDEN, NH * D)]
+        self.att = qw.Attention(NH, NKV, D, R, THETA, EPS, max_ctx=1024, max_tokens=64, max_splits=16)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 2000)
+        self.w = []
+        for _ in range(slots):
+            mats = []
+            for rows, cols in self.shapes:
+                w8 = torch.randint(-127, 128, (rows, cols), dtype=torch.int8, device="cuda", generator=g)
+                sc = 0.02 * (0.5 + torch.rand((rows, cols // 32), device="cuda", generator=g))
+                mats.append((w8, sc))
+            self.w.append(mats)
+        self.x = torch.randn((n, self.HIDDEN), device="cuda", generator=g)
+        self.xo = torch.randn((n, NH * D), device="cuda", generator=g)
+        self.ys = [torch.zeros((n, rows), device="cuda") for rows, _ in self.shapes]
+        self.out = self.ys[0]
+        self.bytes = sum(rows * cols + rows * cols // 32 * 4 for rows, cols in self.shapes)
+        self.mat = True
+        torch.cuda.synchronize()
+
+    def _one(self, slot, k):
+        w8, sc = self.w[slot][k]
+        self.att.mat(self.xo if k == 3 else self.x, self.ys[k], w8, sc)
+
+    def step(self, slot):
+        for k in range(4):
+            self._one(slot, k)
+
+    def step_events(self, slot, ev):
+        ev[0].record()
+        self._one(slot, 0)
+        ev[1].record()
+        for k in range(1, 4):
+            self._one(slot, k)
+        ev[2].record()
+
+    def main_only(self, slot):
+        self._one(slot, 0)
+
+    def close(self):
+        self.w = []
+        self.att.close()
+
+
 def gpu_sleep(ms):
     """Keeps the stream busy for about `ms` milliseconds, so that the launches queued behind it start
     back to back and their HIP events time the kernels, not the host's launch latency."""
@@ -313,7 +373,10 @@ def run_workload(wl, steps, warmup, graph):
     r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all),
          "us_main": statistics.median(per_launch), "us_main_batches": len(per_launch),
          "us_main_min": min(per_launch)}
-    if getattr(wl, "qsa", False):
+    if getattr(wl, "mat", False):
+        r.update({"kernel": "k_mat<q8> (four projections a step; the per-launch figure is the 8,192 x 2,048 "
+                            "query + gate projection)", "us_first_event": statistics.mean(k_first)})
+    elif getattr(wl, "qsa", False):
         vis, tile_keys = wl.visible()
         r.update({"kernel": "k_decode_ld<256,1,0,QSA> (one launch, visible tiles only) after k_qsa_select (raw-key append folded in: no block completes at this position)",
                   "us_indexer": statistics.mean(k_first), "us_main_each_event": statistics.mean(k_second),
@@ -454,6 +517,9 @@ def main():
         ("decode_32k_qsa_cr64", 32768, 1, args.slots, 0, "f32", 64),
         ("decode_256k_qsa_cr4", 262144, 1, 2, 0, "f32", 4),
         ("decode_256k_qsa_cr64", 262144, 1, 2, 0, "f32", 64),
+        # the layer's projections (planar Q8_0 weights), one decode token and a 4-token verify pass
+        ("proj_q8_n1", 0, 1, args.slots, 0, "f32", 0.0),
+        ("proj_q8_n4", 0, 4, args.slots, 0, "f32", 0.0),
     ]
     results = {}
     for name, pos, n, slots, n_split, dt, heavy in configs:
@@ -461,15 +527,26 @@ def main():
             continue
         print(f"[bench] {name}: pos={pos} n={n} slots={slots} splits={n_split or 'auto'}", file=sys.stderr,
               flush=True)
-        if "_qsa" in name:
+        if name.startswith("proj_"):
+            wl = MatWorkload(qw, name, n, slots, seed=len(results))
+        elif "_qsa" in name:
             wl = QsaWorkload(qw, name, pos, n, slots, int(heavy), seed=len(results))
         else:
             wl = Workload(qw, name, pos, n, slots, n_split, dt, heavy, seed=len(results))
         r = run_workload(wl, args.steps, args.warmup, graph)
+        wl_bytes = getattr(wl, "bytes", 0)
         wl.close()
         del wl
         torch.cuda.empty_cache()
-        if "_qsa" in name:
+        if name.startswith("proj_"):
+            # the weights read once; the per-launch figure is the largest projection's
+            r["value"] = wl_bytes / (r["us_per_step"] * 1e-6) / 1e9
+            r["unit"] = "GB/s (weights)"
+            r["algorithmic_bytes"] = wl_bytes
+            r["frac_hbm_step"] = wl_bytes / (r["us_per_step"] * 1e-6) / HBM_PEAK
+            q_bytes = NH * 2 * D * 2048 * (1 + 4 / 32)
+            r["frac_hbm_kernel"] = q_bytes / (r["us_main"] * 1e-6) / HBM_PEAK
+        elif "_qsa" in name:
             # the K/V bytes of the keys the selection leaves visible (each fp16 row once)
             byts = 2 * r["visible_keys"] * NKV * D * 2
             r["value"] = byts / (r["us_per_step"] * 1e-6) / 1e9
@@ -493,7 +570,7 @@ def main():
             r["frac_mfma_step"] = fl / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
             r["frac_mfma_kernel"] = fl / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
             r["algorithmic_flops"] = fl
-        if n * (NH // NKV) <= 32 and "_qsa" not in name:
+        if n * (NH // NKV) <= 32 and "_qsa" not in name and not name.startswith("proj_"):
             r["splits_requested"] = n_split or "auto"
         results[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)

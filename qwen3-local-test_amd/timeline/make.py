@@ -100,7 +100,7 @@ def cc(path):
     if r.returncode:
         print(r.stderr[-3000:]); sys.exit(1)
     return obj
-srcs = [os.path.join(OUT, "decode.hip")] + [os.path.join(CSRC, f) for f in ("norm_rope.hip", "prefill.hip", "qsa.hip", "qwattn.cpp")]
+srcs = [os.path.join(OUT, "decode.hip")] + [os.path.join(CSRC, f) for f in ("norm_rope.hip", "prefill.hip", "qsa.hip", "mat.hip", "qwattn.cpp")]
 with concurrent.futures.ThreadPoolExecutor(4) as ex:
     objs = list(ex.map(cc, srcs))
 r = subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", os.path.join(OUT, "libqwattn_timeline.so")], capture_output=True, text=True)
