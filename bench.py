@@ -27,7 +27,8 @@ dense 256K step.
 
 Two projection workloads (proj_q8_n1, proj_q8_n4) time the layer's four projections around the attention
 (Qwen4Vulkan::mat on planar Q8_0 weights: query + gate, key, value, output at hidden 2,048) for one decode
-token and a 4-token verify pass; their bytes are the weights, read once a step.
+token and a 4-token verify pass; their bytes are the weights, read once a step. A third (proj_q8_n2048) runs
+them over a 2,048-token prefill chunk on the tiled MFMA GEMM and reports TFLOP/s (2 n rows cols a projection).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -235,11 +236,12 @@ class MatWorkload:
     its own weights (30.7 MB a slot), rotated like the K/V caches. Bytes: the weights read once (one byte per
     weight plus a float scale per 32)."""
     HIDDEN = 2048
+    SHAPES = [(NH * 2 * D, HIDDEN), (NKV * D, HIDDEN), (NKV * D, HIDDEN), (HIDDEN, NH * D)]
 
     def __init__(self, qw, name, n, slots, seed=0):
         import torch
         self.name, self.n, self.slots = name, n, slots
-        self.shapes = [(NH * 2 * D, self.HIDDEN), (NKV * D, self.HIDDEN), (NKV * D, self.HIDDEN), (self.HIDDEN, NH * D)]
+        self.shapes = self.SHAPES
         self.att = qw.Attention(NH, NKV, D, R, THETA, EPS, max_ctx=1024, max_tokens=64, max_splits=16)
         g = torch.Generator(device="cuda")
         g.manual_seed(seed + 2000)
@@ -374,7 +376,8 @@ def run_workload(wl, steps, warmup, graph):
          "us_main": statistics.median(per_launch), "us_main_batches": len(per_launch),
          "us_main_min": min(per_launch)}
     if getattr(wl, "mat", False):
-        r.update({"kernel": "k_mat<q8> (four projections a step; the per-launch figure is the 8,192 x 2,048 "
+        kern = "k_gemm<q8> (tiled MFMA GEMM" if wl.n >= 16 else "k_mat_q8 (matrix-vector"
+        r.update({"kernel": kern + "; four projections a step; the per-launch figure is the 8,192 x 2,048 "
                             "query + gate projection)", "us_first_event": statistics.mean(k_first)})
     elif getattr(wl, "qsa", False):
         vis, tile_keys = wl.visible()
@@ -520,6 +523,8 @@ def main():
         # the layer's projections (planar Q8_0 weights), one decode token and a 4-token verify pass
         ("proj_q8_n1", 0, 1, args.slots, 0, "f32", 0.0),
         ("proj_q8_n4", 0, 4, args.slots, 0, "f32", 0.0),
+        # and a 2,048-token prefill chunk (the tiled MFMA GEMM)
+        ("proj_q8_n2048", 0, 2048, 8, 0, "f32", 0.0),
     ]
     results = {}
     for name, pos, n, slots, n_split, dt, heavy in configs:
@@ -538,7 +543,15 @@ def main():
         wl.close()
         del wl
         torch.cuda.empty_cache()
-        if name.startswith("proj_"):
+        if name.startswith("proj_") and n >= 16:
+            # 2 n rows cols flops a projection; the per-launch figure is the 8,192 x 2,048 projection's
+            flops = 2 * n * sum(rows * cols for rows, cols in MatWorkload.SHAPES)
+            r["value"] = flops / (r["us_per_step"] * 1e-6) / 1e12
+            r["unit"] = "TFLOP/s"
+            r["algorithmic_flops"] = flops
+            r["frac_mfma_step"] = flops / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
+            r["frac_mfma_kernel"] = 2 * n * NH * 2 * D * 2048 / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
+        elif name.startswith("proj_"):
             # the weights read once; the per-launch figure is the largest projection's
             r["value"] = wl_bytes / (r["us_per_step"] * 1e-6) / 1e9
             r["unit"] = "GB/s (weights)"

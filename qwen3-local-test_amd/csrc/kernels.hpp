@@ -169,6 +169,9 @@ struct MatArgs {
     int rows, cols, n, x_stride, y_stride, post;
     float post_scale;  // post 1: y = silu(y * post_scale)
 };
+// Token counts from which launch_mat runs the tiled MFMA GEMM (columns a multiple of 32) instead of the
+// matrix-vector kernel.
+constexpr int kGemmMinN = 16;
 hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s);
 
 }  // namespace qw

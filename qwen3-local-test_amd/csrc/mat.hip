@@ -20,6 +20,7 @@ namespace qw {
 
 namespace {
 
+
 constexpr int kMatRW = 4;   // rows a wave
 constexpr int kMatNTP = 4;  // tokens a workgroup
 
@@ -165,9 +166,220 @@ __global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
         }
 }
 
+// ---- many tokens: tiled MFMA GEMM ------------------------------------------------------------------
+// Replaces the q4_gemm_q8 / q4_gemm_f32 pipelines (shaders/q4_gemm.comp) that Qwen4Vulkan::mat selects from
+// nine tokens on (src/qwen4_vk.cpp:852-853). A workgroup owns a 128-row x BN-token tile of Y, walks the
+// columns one 32-column step at a time (one Q8 block) through two LDS stages, and its four waves each own a
+// 64-row x BN/2-token quarter as 4 x BN/32 v_mfma_f32_16x16x32_bf16 tiles (A = weight rows, B = token rows).
+// fp32 accuracy from bf16 products: an int8 weight is exact in bf16, and an fp32 x is split into
+// x_hi = bf16(x) and x_lo = bf16(x - x_hi), which leaves |x - x_hi - x_lo| <= 2^-18 |x|; a product's two
+// MFMAs then carry it to within 2^-18 |w x| before the fp32 accumulation. Q8: each 32-column step's
+// product (a fresh accumulator) is scaled by its rows' block scales into the running sum, as the reference
+// applies the scale per block. f32 weights are split the same way (four MFMAs a tile: hi.hi, hi.lo,
+// lo.hi, lo.lo). The next step's global loads are in flight while the current step's MFMAs run; tiles are
+// assigned so that each XCD takes a contiguous range of row tiles (its weights stay in its L2).
+constexpr int kGemmBM = 128;  // rows a workgroup
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Byte offset of 16-byte chunk g (k = 8 g .. 8 g + 7) of tile row r in an LDS tile of [rows][32] bf16: the
+// chunks of rows 4 j .. 4 j + 3 are rotated by j % 4, so the 16 rows one MFMA operand read touches spread
+// over all banks.
+__device__ __forceinline__ int gemm_off(int r, int g) { return r * 64 + ((g ^ ((r >> 2) & 3)) << 4); }
+
+__device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        hi[i] = (__bf16)v[i];
+        lo[i] = (__bf16)(v[i] - (float)hi[i]);
+    }
+}
+
+template <bool Q8, int BN>
+__global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
+    constexpr int NT = BN / 32;                      // 16-token tiles a wave
+    constexpr int W_B = kGemmBM * 64;                // one bf16 weight plane of a stage
+    constexpr int X_B = BN * 64;                     // one bf16 token plane
+    constexpr int STAGE = (Q8 ? W_B + kGemmBM * 4 : 2 * W_B) + 2 * X_B;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+    const int wr = wave & 1, wt = wave >> 1;
+
+    const int RT = (a.rows + kGemmBM - 1) / kGemmBM, TT = (a.n + BN - 1) / BN, T = RT * TT;
+    const int b = blockIdx.x;
+    const int idx = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);  // XCD b % 8 takes tiles [x T/8, (x+1) T/8)
+    const int r0 = (idx / TT) * kGemmBM, t0 = (idx % TT) * BN;
+    const int nkb = a.cols >> 5;
+
+    // loader roles: weight row lr (two threads a row, 16 columns each); token row lt
+    const int lr = tid >> 1, lh = tid & 1;
+    const size_t wrow = (size_t)min(r0 + lr, a.rows - 1);
+    constexpr int XT = 256 / BN;                      // threads a token row (2 or 4)
+    constexpr int XC = 32 / XT;                       // columns a thread (16 or 8)
+    const int lt = tid / XT, lq = tid % XT;
+    const float* xrow = a.x + (size_t)min(t0 + lt, a.n - 1) * a.x_stride + lq * XC;
+
+    // one step's global data in registers
+    struct Pre {
+        u32x4 w;       // Q8: 16 int8 weights
+        float f[16];   // f32: 16 weights
+        float sc;      // Q8: block scale of row `tid` (threads 0..127)
+        float x[XC];
+    };
+    auto load = [&](Pre& P, int kb) {
+        const int k0 = kb * 32;
+        if constexpr (Q8) {
+            P.w = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(a.w) + wrow * a.cols + k0 + 16 * lh);
+            if (tid < kGemmBM) P.sc = a.s[(size_t)min(r0 + tid, a.rows - 1) * nkb + kb];
+        } else {
+            const float* wp = static_cast<const float*>(a.w) + wrow * a.cols + k0 + 16 * lh;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(wp + i);
+                P.f[i] = v[0], P.f[i + 1] = v[1], P.f[i + 2] = v[2], P.f[i + 3] = v[3];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XC; i += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xrow + k0 + i);
+            P.x[i] = v[0], P.x[i + 1] = v[1], P.x[i + 2] = v[2], P.x[i + 3] = v[3];
+        }
+    };
+    auto store = [&](const Pre& P, int st) {
+        unsigned char* S = smem + st * STAGE;
+        if constexpr (Q8) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                bf16x8 v;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int q = (int)P.w[2 * h + j / 4];
+                    v[j] = (__bf16)(float)((q << (24 - 8 * (j % 4))) >> 24);
+                }
+                *reinterpret_cast<bf16x8*>(S + gemm_off(lr, 2 * lh + h)) = v;
+            }
+            if (tid < kGemmBM) reinterpret_cast<float*>(S + W_B + 2 * X_B)[tid] = P.sc;
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float v8[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v8[j] = P.f[8 * h + j];
+                bf16x8 hi, lo;
+                split_bf16(v8, hi, lo);
+                *reinterpret_cast<bf16x8*>(S + gemm_off(lr, 2 * lh + h)) = hi;
+                *reinterpret_cast<bf16x8*>(S + W_B + 2 * X_B + gemm_off(lr, 2 * lh + h)) = lo;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < XC / 8; h++) {
+            float v8[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v8[j] = P.x[8 * h + j];
+            bf16x8 hi, lo;
+            split_bf16(v8, hi, lo);
+            const int gc = lq * (XC / 8) + h;
+            *reinterpret_cast<bf16x8*>(S + W_B + gemm_off(lt, gc)) = hi;
+            *reinterpret_cast<bf16x8*>(S + W_B + X_B + gemm_off(lt, gc)) = lo;
+        }
+    };
+
+    f32x4 acc[4][NT];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int st) {
+        const unsigned char* S = smem + st * STAGE;
+        bf16x8 A[4], Bh[NT], Bl[NT];
+#pragma unroll
+        for (int m = 0; m < 4; m++) A[m] = *reinterpret_cast<const bf16x8*>(S + gemm_off(wr * 64 + m * 16 + c, g));
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int r = wt * (BN / 2) + t * 16 + c;
+            Bh[t] = *reinterpret_cast<const bf16x8*>(S + W_B + gemm_off(r, g));
+            Bl[t] = *reinterpret_cast<const bf16x8*>(S + W_B + X_B + gemm_off(r, g));
+        }
+        if constexpr (Q8) {
+            const float* sS = reinterpret_cast<const float*>(S + W_B + 2 * X_B);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const f32x4 sc = *reinterpret_cast<const f32x4*>(sS + wr * 64 + m * 16 + 4 * g);
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[m], Bh[t], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[m], Bl[t], p, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[m][t][i] = __builtin_fmaf(sc[i], p[i], acc[m][t][i]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const bf16x8 Al = *reinterpret_cast<const bf16x8*>(S + W_B + 2 * X_B + gemm_off(wr * 64 + m * 16 + c, g));
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[m], Bh[t], acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[m], Bl[t], acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bh[t], acc[m][t], 0, 0, 0);
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bl[t], acc[m][t], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // stage kb % 2 holds step kb; step kb + 1's global loads are in flight while its MFMAs run, then
+    // converted into the other stage (whose last readers passed the previous barrier)
+    Pre P;
+    load(P, 0);
+    store(P, 0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb++) {
+        if (kb + 1 < nkb) load(P, kb + 1);
+        compute(kb & 1);
+        if (kb + 1 < nkb) store(P, (kb + 1) & 1);
+        __syncthreads();
+    }
+
+    // lane (c, g) holds rows 4 g .. 4 g + 3 of each tile for token c
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int tok = t0 + wt * (BN / 2) + t * 16 + c;
+        if (tok >= a.n) continue;
+        float* yr = a.y + (size_t)tok * a.y_stride;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int row = r0 + wr * 64 + m * 16 + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = acc[m][t][i];
+                if (a.post == 1) {
+                    const float u = v * a.post_scale;
+                    v = u / (1.0f + __expf(-u));
+                }
+                if (row + i < a.rows) yr[row + i] = v;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s) {
+    if (a.n >= kGemmMinN && a.cols % 32 == 0) {
+        const int rt = (a.rows + kGemmBM - 1) / kGemmBM;
+        if (a.n >= 1024) {  // 128-token tiles: half the weight re-reads; below, 64 (twice the workgroups)
+            const dim3 grid(rt * ((a.n + 127) / 128));
+            if (q8) hipLaunchKernelGGL((k_gemm<true, 128>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((k_gemm<false, 128>), grid, dim3(256), 0, s, a);
+        } else {
+            const dim3 grid(rt * ((a.n + 63) / 64));
+            if (q8) hipLaunchKernelGGL((k_gemm<true, 64>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((k_gemm<false, 64>), grid, dim3(256), 0, s, a);
+        }
+        return hipGetLastError();
+    }
     // one token (a decode step): a workgroup's waves take one token; else four tokens a workgroup
     const int ntp = a.n == 1 ? 1 : kMatNTP;
     const dim3 grid((a.rows + 4 * kMatRW - 1) / (4 * kMatRW), (a.n + ntp - 1) / ntp), block(256);

@@ -92,3 +92,82 @@ def test_mat_rejects_bad_shapes(qw):
     with pytest.raises(qw.QwattnError):
         ctx.mat(x, y, w, s)
     ctx.close()
+
+
+# The tiled MFMA GEMM (16 tokens and up, columns a multiple of 32): partial row and token tiles, both token
+# tile widths (64 below 1,024 tokens, 128 from there), the attention layer's shapes
+GEMM_CASES = [(512, 2048, 16), (512, 2048, 200), (100, 96, 33), (37, 1056, 130), (2048, 4096, 64),
+              (8192, 2048, 20), (300, 64, 257), (160, 256, 1100), (64, 64, 1500)]
+
+
+@pytest.mark.parametrize("rows,cols,n", GEMM_CASES, ids=lambda v: str(v))
+def test_gemm_q8_parity(qw, oracle, rows, cols, n):
+    print(f"gemm q8 {rows}x{cols} n={n}", flush=True)
+    blocks, _, _ = q8_blocks(81 + rows + n, rows, cols)
+    w8, s = qw.q8_unpack(blocks, rows, cols)
+    x = np.random.default_rng(82 + n).standard_normal((n, cols)).astype(np.float32)
+    ctx = _ctx(qw)
+    y = torch.full((n, rows), float("nan"), device=DEV)
+    ctx.mat(dev(x), y, dev(w8), dev(s))
+    torch.cuda.synchronize()
+    want = oracle.mat(x, w8=w8, s=s)
+    _check(y.cpu().numpy(), want, np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)), x)
+    ctx.close()
+
+
+@pytest.mark.parametrize("rows,cols,n", [(300, 64, 40), (512, 2048, 130), (130, 96, 17), (200, 128, 1030)],
+                         ids=lambda v: str(v))
+def test_gemm_f32_parity(qw, oracle, rows, cols, n):
+    print(f"gemm f32 {rows}x{cols} n={n}", flush=True)
+    r = np.random.default_rng(83)
+    w = (0.05 * r.standard_normal((rows, cols))).astype(np.float32)
+    x = r.standard_normal((n, cols)).astype(np.float32)
+    ctx = _ctx(qw)
+    y = torch.full((n, rows), float("nan"), device=DEV)
+    ctx.mat(dev(x), y, dev(w))
+    torch.cuda.synchronize()
+    _check(y.cpu().numpy(), oracle.mat(x, wf=w), np.abs(w), x)
+    ctx.close()
+
+
+def test_gemm_strides_post_and_scale_range(qw, oracle):
+    """GEMM with x_stride / y_stride wider than the rows, post 1, outputs beyond `rows` untouched, and inputs
+    whose magnitudes span 2^-20 .. 2^20 (the hi / lo split keeps fp32 range and relative accuracy)."""
+    rows, cols, n = 200, 512, 40
+    blocks, _, _ = q8_blocks(84, rows, cols)
+    w8, s = qw.q8_unpack(blocks, rows, cols)
+    r = np.random.default_rng(85)
+    x = (r.standard_normal((n, cols + 32)) * np.exp2(r.integers(-20, 21, (n, cols + 32)))).astype(np.float32)
+    ctx = _ctx(qw)
+    y = torch.full((n, rows + 8), 7.0, device=DEV)
+    ctx.mat(dev(x)[:, :cols], y, dev(w8), dev(s), post=1, post_scale=1e-3)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = oracle.mat(x[:, :cols], w8=w8, s=s, post=1, post_scale=1e-3)
+    _check(got[:, :rows], want, np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)), x[:, :cols])
+    assert np.all(got[:, rows:] == 7.0)
+    ctx.close()
+
+
+def test_gemm_full_prefill_matches_matvec(qw):
+    """At the full prefill size (2,048 tokens through the 8,192 x 2,048 query + gate projection, too large for
+    the CPU oracle in a test) each token's outputs do not depend on the batch: the GEMM's rows for a spread of
+    tokens equal the matrix-vector kernel's outputs for those tokens alone (both kernels are pinned to the
+    oracle above), to the same tolerance."""
+    rows, cols, n = 8192, 2048, 2048
+    blocks, _, _ = q8_blocks(86, rows, cols)
+    w8, s = qw.q8_unpack(blocks, rows, cols)
+    x = np.random.default_rng(87).standard_normal((n, cols)).astype(np.float32)
+    ctx = _ctx(qw)
+    wd, sd, xd = dev(w8), dev(s), dev(x)
+    y = torch.empty((n, rows), device=DEV)
+    ctx.mat(xd, y, wd, sd)
+    pick = [0, 1, 63, 64, 127, 128, 1000, 2047]
+    ys = torch.empty((len(pick), rows), device=DEV)
+    ctx.mat(xd[pick].contiguous(), ys, wd, sd)  # 8 tokens: the matrix-vector kernel
+    torch.cuda.synchronize()
+    mag = np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)).astype(np.float64) @ np.abs(x[pick]).T.astype(np.float64)
+    err = np.abs(y.cpu().numpy()[pick].astype(np.float64) - ys.cpu().numpy())
+    assert np.all(err <= 2e-5 * mag.T + 2e-6), float((err / mag.T).max())
+    assert np.isfinite(y.cpu().numpy()).all()
+    ctx.close()
