@@ -21,7 +21,6 @@ namespace qw {
 namespace {
 
 
-constexpr int kMatRW = 4;   // rows a wave
 constexpr int kMatNTP = 4;  // tokens a workgroup
 
 // Sum over the 64 lanes, in every lane.
@@ -32,16 +31,16 @@ __device__ __forceinline__ float mat_wave_sum(float x) {
 }
 
 // f32 weights: a wave's RW rows a 16-column group at a time (f32 projections are the small ones)
-template <int NTP>
+template <int NTP, int RW>
 __global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r0 = (blockIdx.x * 4 + wave) * kMatRW;
+    const int r0 = (blockIdx.x * 4 + wave) * RW;
     const int t0 = blockIdx.y * NTP;
     const int nt = min(NTP, a.n - t0);
     if (r0 >= a.rows) return;  // whole waves
-    float acc[kMatRW][NTP];
+    float acc[RW][NTP];
 #pragma unroll
-    for (int r = 0; r < kMatRW; r++)
+    for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int t = 0; t < NTP; t++) acc[r][t] = 0.f;
     for (int c = lane * 16; c < a.cols; c += 1024) {
@@ -56,7 +55,7 @@ __global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
             }
         }
 #pragma unroll
-        for (int r = 0; r < kMatRW; r++) {
+        for (int r = 0; r < RW; r++) {
             const float* wr = static_cast<const float*>(a.w) + (size_t)min(r0 + r, a.rows - 1) * a.cols + c;
             float wv[16];
 #pragma unroll
@@ -71,7 +70,7 @@ __global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
         }
     }
 #pragma unroll
-    for (int r = 0; r < kMatRW; r++)
+    for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int t = 0; t < NTP; t++) {
             float v = mat_wave_sum(acc[r][t]);
@@ -88,30 +87,30 @@ __global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
 // matrix in flight at once (the stream is the bound: the loads have to overlap); then per chunk the token
 // rows' 16 columns (cached: every wave reads them) and the dot products
 constexpr int kMatK = 4;
-template <int NTP>
+template <int NTP, int RW>
 __global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r0 = (blockIdx.x * 4 + wave) * kMatRW;
+    const int r0 = (blockIdx.x * 4 + wave) * RW;
     const int t0 = blockIdx.y * NTP;
     const int nt = min(NTP, a.n - t0);
     if (r0 >= a.rows) return;  // whole waves
     const int8_t* w8 = static_cast<const int8_t*>(a.w);
     const int nsb = a.cols >> 5;  // scales a row
-    float acc[kMatRW][NTP];
+    float acc[RW][NTP];
 #pragma unroll
-    for (int r = 0; r < kMatRW; r++)
+    for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int t = 0; t < NTP; t++) acc[r][t] = 0.f;
     for (int cb = 0; cb < a.cols; cb += kMatK * 1024) {
-        u32x4 q[kMatRW][kMatK];
-        float sc[kMatRW][kMatK];
+        u32x4 q[RW][kMatK];
+        float sc[RW][kMatK];
 #pragma unroll
         for (int k = 0; k < kMatK; k++) {
             if (cb + k * 1024 >= a.cols) break;  // the whole chunk lies past the row (wave-uniform)
             const int c = min(cb + k * 1024 + lane * 16, a.cols - 16);  // past the row: a valid group, unused
 #pragma unroll
-            for (int r = 0; r < kMatRW; r++) {
+            for (int r = 0; r < RW; r++) {
                 const int row = min(r0 + r, a.rows - 1);  // past the last row: a valid row, result not stored
                 q[r][k] = *reinterpret_cast<const u32x4*>(w8 + (size_t)row * a.cols + c);
                 sc[r][k] = a.s[(size_t)row * nsb + (c >> 5)];
@@ -133,7 +132,7 @@ __global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
                 }
             }
 #pragma unroll
-            for (int r = 0; r < kMatRW; r++) {
+            for (int r = 0; r < RW; r++) {
                 float wv[16];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -154,7 +153,7 @@ __global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
         }
     }
 #pragma unroll
-    for (int r = 0; r < kMatRW; r++)
+    for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int t = 0; t < NTP; t++) {
             float v = mat_wave_sum(acc[r][t]);
@@ -197,7 +196,7 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& hi, bf16
 
 template <bool Q8, int BN>
 __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
-    constexpr int NT = BN / 32;                      // 16-token tiles a wave
+    constexpr int NT = BN / 32;                      // 16-token tiles a wave (BN = 32, 64 or 128)
     constexpr int W_B = kGemmBM * 64;                // one bf16 weight plane of a stage
     constexpr int X_B = BN * 64;                     // one bf16 token plane
     constexpr int STAGE = (Q8 ? W_B + kGemmBM * 4 : 2 * W_B) + 2 * X_B;
@@ -214,10 +213,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
     // loader roles: weight row lr (two threads a row, 16 columns each); token row lt
     const int lr = tid >> 1, lh = tid & 1;
     const size_t wrow = (size_t)min(r0 + lr, a.rows - 1);
-    constexpr int XT = 256 / BN;                      // threads a token row (2 or 4)
+    constexpr int XT = BN >= 64 ? 256 / BN : 4;       // threads a token row (2 or 4)
     constexpr int XC = 32 / XT;                       // columns a thread (16 or 8)
     const int lt = tid / XT, lq = tid % XT;
-    const float* xrow = a.x + (size_t)min(t0 + lt, a.n - 1) * a.x_stride + lq * XC;
+    const bool xl = BN * XT == 256 || tid < BN * XT;  // BN = 32: threads 0..127 load the token rows
+    const float* xrow = a.x + (size_t)min(t0 + min(lt, BN - 1), a.n - 1) * a.x_stride + lq * XC;
 
     // one step's global data in registers
     struct Pre {
@@ -239,10 +239,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
                 P.f[i] = v[0], P.f[i + 1] = v[1], P.f[i + 2] = v[2], P.f[i + 3] = v[3];
             }
         }
+        if (xl) {
 #pragma unroll
-        for (int i = 0; i < XC; i += 4) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(xrow + k0 + i);
-            P.x[i] = v[0], P.x[i + 1] = v[1], P.x[i + 2] = v[2], P.x[i + 3] = v[3];
+            for (int i = 0; i < XC; i += 4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(xrow + k0 + i);
+                P.x[i] = v[0], P.x[i + 1] = v[1], P.x[i + 2] = v[2], P.x[i + 3] = v[3];
+            }
         }
     };
     auto store = [&](const Pre& P, int st) {
@@ -273,6 +275,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
         }
 #pragma unroll
         for (int h = 0; h < XC / 8; h++) {
+            if (!xl) break;
             float v8[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) v8[j] = P.x[8 * h + j];
@@ -368,27 +371,45 @@ __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
 
 hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s) {
     if (a.n >= kGemmMinN && a.cols % 32 == 0) {
+        // the widest token tile that still gives two workgroups a CU (fewer weight re-reads), else the
+        // narrowest (the most workgroups)
         const int rt = (a.rows + kGemmBM - 1) / kGemmBM;
-        if (a.n >= 1024) {  // 128-token tiles: half the weight re-reads; below, 64 (twice the workgroups)
-            const dim3 grid(rt * ((a.n + 127) / 128));
-            if (q8) hipLaunchKernelGGL((k_gemm<true, 128>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((k_gemm<false, 128>), grid, dim3(256), 0, s, a);
+        const auto tiles = [&](int bn) { return rt * ((a.n + bn - 1) / bn); };
+        const int bn = tiles(128) >= 512 ? 128 : tiles(64) >= 512 ? 64 : 32;
+        const dim3 grid(tiles(bn)), block(256);
+        if (bn == 128) {
+            if (q8) hipLaunchKernelGGL((k_gemm<true, 128>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_gemm<false, 128>), grid, block, 0, s, a);
+        } else if (bn == 64) {
+            if (q8) hipLaunchKernelGGL((k_gemm<true, 64>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_gemm<false, 64>), grid, block, 0, s, a);
         } else {
-            const dim3 grid(rt * ((a.n + 63) / 64));
-            if (q8) hipLaunchKernelGGL((k_gemm<true, 64>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((k_gemm<false, 64>), grid, dim3(256), 0, s, a);
+            if (q8) hipLaunchKernelGGL((k_gemm<true, 32>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_gemm<false, 32>), grid, block, 0, s, a);
         }
         return hipGetLastError();
     }
-    // one token (a decode step): a workgroup's waves take one token; else four tokens a workgroup
+    // matrix-vector: one token a workgroup for a decode step, else four; four rows a wave when that still
+    // gives 256 workgroups a token group, else one (small matrices: more rows in flight at once)
     const int ntp = a.n == 1 ? 1 : kMatNTP;
-    const dim3 grid((a.rows + 4 * kMatRW - 1) / (4 * kMatRW), (a.n + ntp - 1) / ntp), block(256);
+    const bool rw4 = a.rows >= 4096;
+    const dim3 grid((a.rows + (rw4 ? 15 : 3)) / (rw4 ? 16 : 4), (a.n + ntp - 1) / ntp), block(256);
     if (q8) {
-        if (ntp == 1) hipLaunchKernelGGL(k_mat_q8<1>, grid, block, 0, s, a);
-        else hipLaunchKernelGGL(k_mat_q8<kMatNTP>, grid, block, 0, s, a);
+        if (ntp == 1) {
+            if (rw4) hipLaunchKernelGGL((k_mat_q8<1, 4>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_mat_q8<1, 1>), grid, block, 0, s, a);
+        } else {
+            if (rw4) hipLaunchKernelGGL((k_mat_q8<kMatNTP, 4>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_mat_q8<kMatNTP, 1>), grid, block, 0, s, a);
+        }
     } else {
-        if (ntp == 1) hipLaunchKernelGGL(k_mat_f32<1>, grid, block, 0, s, a);
-        else hipLaunchKernelGGL(k_mat_f32<kMatNTP>, grid, block, 0, s, a);
+        if (ntp == 1) {
+            if (rw4) hipLaunchKernelGGL((k_mat_f32<1, 4>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_mat_f32<1, 1>), grid, block, 0, s, a);
+        } else {
+            if (rw4) hipLaunchKernelGGL((k_mat_f32<kMatNTP, 4>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((k_mat_f32<kMatNTP, 1>), grid, block, 0, s, a);
+        }
     }
     return hipGetLastError();
 }

@@ -30,8 +30,9 @@ def _check(got, want, w_abs, x):
 
 
 # (rows, cols): the attention layer's projections at hidden 2,048 (query + gate, key, value, output), then odd
-# shapes: a partial last workgroup of rows, a column count that leaves lanes idle
-SHAPES = [(8192, 2048), (512, 2048), (2048, 4096), (100, 96), (37, 1056)]
+# shapes: a partial last workgroup of rows (one row a wave below 4,096 rows, four from there), a column count
+# that leaves lanes idle
+SHAPES = [(8192, 2048), (512, 2048), (2048, 4096), (100, 96), (37, 1056), (4100, 96)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES, ids=lambda v: str(v))
@@ -94,10 +95,12 @@ def test_mat_rejects_bad_shapes(qw):
     ctx.close()
 
 
-# The tiled MFMA GEMM (16 tokens and up, columns a multiple of 32): partial row and token tiles, both token
-# tile widths (64 below 1,024 tokens, 128 from there), the attention layer's shapes
+# The tiled MFMA GEMM (16 tokens and up, columns a multiple of 32): partial row and token tiles and each token
+# tile width (128 when that still gives 512 workgroups, else 64 when that does, else 32), the attention
+# layer's shapes
 GEMM_CASES = [(512, 2048, 16), (512, 2048, 200), (100, 96, 33), (37, 1056, 130), (2048, 4096, 64),
-              (8192, 2048, 20), (300, 64, 257), (160, 256, 1100), (64, 64, 1500)]
+              (8192, 2048, 20), (300, 64, 257), (160, 256, 1100), (64, 64, 1500),
+              (8192, 64, 512), (8000, 96, 530), (8192, 64, 1100), (8000, 96, 1030)]
 
 
 @pytest.mark.parametrize("rows,cols,n", GEMM_CASES, ids=lambda v: str(v))
@@ -115,7 +118,8 @@ def test_gemm_q8_parity(qw, oracle, rows, cols, n):
     ctx.close()
 
 
-@pytest.mark.parametrize("rows,cols,n", [(300, 64, 40), (512, 2048, 130), (130, 96, 17), (200, 128, 1030)],
+@pytest.mark.parametrize("rows,cols,n", [(300, 64, 40), (512, 2048, 130), (130, 96, 17), (200, 128, 1030),
+                                          (8000, 64, 530), (8192, 64, 1030)],
                          ids=lambda v: str(v))
 def test_gemm_f32_parity(qw, oracle, rows, cols, n):
     print(f"gemm f32 {rows}x{cols} n={n}", flush=True)
