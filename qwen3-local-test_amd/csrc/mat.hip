@@ -182,9 +182,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Byte offset of 16-byte chunk g (k = 8 g .. 8 g + 7) of tile row r in an LDS tile of [rows][32] bf16: the
-// chunks of rows 4 j .. 4 j + 3 are rotated by j % 4, so the 16 rows one MFMA operand read touches spread
-// over all banks.
-__device__ __forceinline__ int gemm_off(int r, int g) { return r * 64 + ((g ^ ((r >> 2) & 3)) << 4); }
+// chunk index is XORed with (r / 2) % 4, so any 8 consecutive rows' chunk g (an MFMA operand read) and any
+// 4 rows' chunk pairs (the loaders' writes) land in 8 distinct 16-byte bank groups (no bank conflicts,
+// counted by SQ_LDS_BANK_CONFLICT).
+__device__ __forceinline__ int gemm_off(int r, int g) { return r * 64 + ((g ^ ((r >> 1) & 3)) << 4); }
 
 __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
 #pragma unroll
