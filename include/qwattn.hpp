@@ -80,6 +80,14 @@ public:
               "qwattn_layer_attention");
     }
 
+    // A projection, Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856): y[n][y_stride] = x[n][x_stride] W^T, W planar
+    // Q8_0 (w int8 [rows][cols], s fp32 [rows][cols/32]) or fp32 (s unused); post 1: silu(y * post_scale).
+    void mat(void* stream, const void* w, const float* s, bool q8, int rows, int cols, const float* x, int x_stride,
+             float* y, int y_stride, int n, int post = 0, float post_scale = 0.f) {
+        check(ctx_, qwattn_mat(ctx_, stream, w, s, q8 ? 1 : 0, rows, cols, x, x_stride, y, y_stride, n, post, post_scale),
+              "qwattn_mat");
+    }
+
     // A QSA layer past its budget (Qwen4Vulkan::attention with `masked`, src/qwen4_vk.cpp:942-984): cache
     // and pool the pass's projected indexer keys, select each token's blocks into per-key visibility bits,
     // and run the layer's attention over the visible keys. raw [max_ctx][idx_dim] and pooled

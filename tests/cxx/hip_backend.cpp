@@ -2,8 +2,9 @@
 // written against the reference's own interfaces (class Backend, src/backend.h:9-41; Q4Config and
 // Q4Weights, src/qwen4.h:22-107). Compiled by tests/test_integration_cxx.py with -fsyntax-only, against
 // include/qwattn.hpp alone and, where the reference sources are present, with -DQW_WITH_REFERENCE against
-// the reference's headers. The rest of a backend — weight upload, the projections, DeltaNet, MoE,
-// hyper-connections, sampling — is not part of libqwattn and is left declared, not defined.
+// the reference's headers. The full-attention layers' projections run through qwattn_mat; the rest of a
+// backend — weight upload, DeltaNet, MoE, hyper-connections, sampling — is not part of libqwattn and is
+// left declared, not defined.
 #include <algorithm>
 #include <vector>
 
@@ -63,6 +64,29 @@ public:
     void accept(int keep) override { pos_ = spec_pos0_ + keep; }
 
 private:
+    // A matrix as uploaded: planar Q8_0 (int8 weights, fp32 scale per 32) as the reference's upload repacks
+    // GGUF Q8_0 (src/qwen4_vk.cpp:98-106; qwattn_q8_unpack on the host), or fp32.
+    struct DevMat {
+        const void* w = nullptr;
+        const float* s = nullptr;
+        bool q8 = false;
+        int rows = 0, cols = 0;
+    };
+    // Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856)
+    void mat(const DevMat& m, const float* x, float* y, int n, int x_stride) {
+        att_.mat(stream_, m.w, m.s, m.q8, m.rows, m.cols, x, x_stride, y, m.rows, n);
+    }
+    // A full-attention layer l for n tokens on its normed input xn [n][hidden]: the q (query | gate), k and v
+    // projections, the attention body, then o_proj into h [n][hidden] (src/qwen4_vk.cpp:965-967, 994).
+    void full_attention_layer(int l, int n, const float* xn, float* h) {
+        const LayerMats& m = mats_[l];
+        mat(m.q, xn, qg_, n, cfg_.hidden);
+        mat(m.k, xn, k_, n, cfg_.hidden);
+        mat(m.v, xn, v_, n, cfg_.hidden);
+        attention(l, n, qg_, k_, v_, att_out_);
+        mat(m.o, att_out_, h, n, cfg_.n_heads * cfg_.head_dim);
+    }
+
     // The body of one full-attention layer l for n tokens at the current position, between its q/k/v
     // projections (qg [n][NH][2D] = query | gate per head, k and v [n][NKV][D], fp32 device buffers)
     // and o_proj (out [n][NH][D]), where src/qwen4_vk.cpp:1198/1255 call attention(l, n, pos_).
@@ -73,8 +97,9 @@ private:
     }
 
     // the rest of the backend (not libqwattn): weights upload — the norm gammas minus one, as
-    // up_norm_minus1 (src/qwen4_vk.cpp:444-448), into q_norm_dev_/k_norm_dev_ — the layer stack calling
-    // attention() for the full-attention layers, and the recurrent state
+    // up_norm_minus1 (src/qwen4_vk.cpp:444-448), into q_norm_dev_/k_norm_dev_, the q/k/v/o matrices into
+    // mats_ and the layer buffers qg_, k_, v_, att_out_ — the layer stack calling full_attention_layer() for
+    // the full-attention layers, and the recurrent state
     void upload_norms();
     void run(const int* tokens, int n, float* logits, bool all_logits);
     void reset_recurrent();
@@ -88,6 +113,11 @@ private:
     qwattn::Context att_;
     std::vector<int> slot_;  // K/V slot of each layer (-1: not a full-attention layer)
     std::vector<const float*> q_norm_dev_, k_norm_dev_;
+    struct LayerMats {
+        DevMat q, k, v, o;
+    };
+    std::vector<LayerMats> mats_;
+    float *qg_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_out_ = nullptr;  // [max_tokens][...] device buffers
     int pos_ = 0, saved_pos_ = 0, spec_pos0_ = 0;
 };
 
@@ -105,6 +135,9 @@ struct AttentionLayers {
                const float* kn, float* out, int n) {
         att.kv_grow(stream, pos + n);
         att.layer_attention(stream, slot, qg, k, v, QWATTN_F32, qn, kn, out, pos, n);
+    }
+    void project(void* stream, const void* w8, const float* s, int rows, int cols, const float* x, float* y, int n) {
+        att.mat(stream, w8, s, true, rows, cols, x, cols, y, rows, n);
     }
 };
 
