@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from common import QWEN3_NEXT, TINY, TINY_GGUF
-from tiny_model import OracleAttention, TinyModel, greedy_schedule, run, top2_margin
+from tiny_model import OracleAttention, TinyModel, greedy_schedule, rmsnorm, run, top2_margin
 
 LAYERS = 2
 VOCAB = 512
@@ -66,4 +66,55 @@ def test_hip_attention_same_argmax(qw, oracle, s, hidden, n0, steps, seed):
     # the logits (unit scale) track the reference to the attention-output tolerance
     err = float(np.max(np.abs(got - ref)))
     print(f"{s}: logits max-abs diff {err:.2e}, smallest reference top-2 margin {np.min(top2_margin(ref)):.2e}")
+    assert err <= 5e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("s,hidden,n0,steps,seed", CASES, ids=lambda v: repr(v))
+def test_hip_layer_with_projections_same_argmax(qw, oracle, s, hidden, n0, steps, seed):
+    """GPU: the whole full-attention layer on the device — the q|gate, k, v projections and o_proj through
+    qwattn_mat (fp32 weights: the tiled MFMA GEMM for the prompt, the matrix-vector kernel for the verify
+    pass and the decode steps) around qwattn_layer_attention — leaves every argmax of the logits unchanged
+    against the host fp32 projections and the CPU oracle's attention."""
+    import torch
+    model, prompt, sched, ref, ctx = _setup(oracle, s, hidden, n0, steps, seed)
+    att = qw.Attention(s.NH, s.NKV, s.D, s.R, s.theta, s.eps, max_ctx=ctx, max_tokens=n0, max_splits=256)
+    att.kv_alloc(LAYERS, ctx)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to("cuda:0")
+    # W^T rows: y[n][rows] = x[n][cols] W^T is x @ w for w [cols][rows]
+    dev_w = [{k: d(w[k].T) for k in ("wqg", "wk", "wv", "wo")} | {"qn": d(w["qn"]), "kn": d(w["kn"])}
+             for w in model.lw]
+
+    class DeviceLayers(TinyModel):
+        def forward(self, ids, pos, attend):
+            n = len(ids)
+            x = self.emb[np.asarray(ids)]
+            for li, w in enumerate(self.lw):
+                dw = dev_w[li]
+                h = d(rmsnorm(x, w["norm"]))
+                qg = torch.empty((n, s.NH * 2 * s.D), device="cuda:0")
+                k = torch.empty((n, s.NKV * s.D), device="cuda:0")
+                v = torch.empty((n, s.NKV * s.D), device="cuda:0")
+                att.mat(h, qg, dw["wqg"])
+                att.mat(h, k, dw["wk"])
+                att.mat(h, v, dw["wv"])
+                o = torch.zeros((n, s.NH * s.D), device="cuda:0")
+                att.layer_attention(li, qg, k, v, dw["qn"], dw["kn"], o, pos, n)
+                y = torch.empty((n, self.hidden), device="cuda:0")
+                att.mat(o, y, dw["wo"])
+                x = x + y.cpu().numpy()
+            return rmsnorm(x, self.fnorm) @ self.lm_head
+
+    dev_model = DeviceLayers.__new__(DeviceLayers)
+    dev_model.__dict__.update(model.__dict__)
+    try:
+        got = run(dev_model, None, prompt, sched)
+    finally:
+        att.close()
+    am_ref, am_got = np.argmax(ref, -1), np.argmax(got, -1)
+    bad = np.nonzero(am_ref != am_got)[0]
+    assert bad.size == 0, (f"argmax differs at positions {bad.tolist()[:10]} (reference top-2 margins "
+                           f"{top2_margin(ref[bad]).tolist()[:10]})")
+    err = float(np.max(np.abs(got - ref)))
+    print(f"{s}: logits max-abs diff {err:.2e} with device projections")
     assert err <= 5e-3
