@@ -27,7 +27,8 @@ dense 256K step.
 
 Two projection workloads (proj_q8_n1, proj_q8_n4) time the layer's four projections around the attention
 (Qwen4Vulkan::mat on planar Q8_0 weights: query + gate, key, value, output at hidden 2,048) for one decode
-token and a 4-token verify pass; their bytes are the weights, read once a step. A third (proj_q8_n2048) runs
+token and a 4-token verify pass (query + gate, key and value in one qwattn_mat_multi call, which shares the
+layer input, then the output projection); their bytes are the weights, read once a step. A third (proj_q8_n2048) runs
 them over a 2,048-token prefill chunk on the tiled MFMA GEMM and reports TFLOP/s (2 n rows cols a projection).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -265,16 +266,19 @@ class MatWorkload:
         w8, sc = self.w[slot][k]
         self.att.mat(self.xo if k == 3 else self.x, self.ys[k], w8, sc)
 
+    def _qkv(self, slot):
+        # the query + gate, key and value projections share the layer input: one qwattn_mat_multi call
+        self.att.mat_multi(self.x, [(self.ys[k], *self.w[slot][k]) for k in range(3)])
+
     def step(self, slot):
-        for k in range(4):
-            self._one(slot, k)
+        self._qkv(slot)
+        self._one(slot, 3)
 
     def step_events(self, slot, ev):
         ev[0].record()
-        self._one(slot, 0)
+        self._qkv(slot)
         ev[1].record()
-        for k in range(1, 4):
-            self._one(slot, k)
+        self._one(slot, 3)
         ev[2].record()
 
     def main_only(self, slot):
@@ -376,9 +380,10 @@ def run_workload(wl, steps, warmup, graph):
          "us_main": statistics.median(per_launch), "us_main_batches": len(per_launch),
          "us_main_min": min(per_launch)}
     if getattr(wl, "mat", False):
-        kern = "k_gemm<q8> (tiled MFMA GEMM" if wl.n >= 16 else "k_mat_q8 (matrix-vector"
-        r.update({"kernel": kern + "; four projections a step; the per-launch figure is the 8,192 x 2,048 "
-                            "query + gate projection)", "us_first_event": statistics.mean(k_first)})
+        kern = ("k_gemm<q8> (tiled MFMA GEMM, one launch a projection" if wl.n >= 16 else
+                "k_mat_multi<q8> + k_mat_q8 (matrix-vector: query + gate, key and value in one launch, then output")
+        r.update({"kernel": kern + "; the per-launch figure is the 8,192 x 2,048 query + gate projection alone)",
+                  "us_first_event": statistics.mean(k_first)})
     elif getattr(wl, "qsa", False):
         vis, tile_keys = wl.visible()
         r.update({"kernel": "k_decode_ld<256,1,0,QSA> (one launch, visible tiles only) after k_qsa_select (raw-key append folded in: no block completes at this position)",

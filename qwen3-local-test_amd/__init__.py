@@ -36,6 +36,12 @@ class Config(ctypes.Structure):
                 ("max_ctx", ctypes.c_int), ("max_tokens", ctypes.c_int), ("max_splits", ctypes.c_int)]
 
 
+class MatOut(ctypes.Structure):
+    """qwattn_mat_out: one matrix of qwattn_mat_multi and its output."""
+    _fields_ = [("w", ctypes.c_void_p), ("s", ctypes.c_void_p), ("rows", ctypes.c_int), ("y", ctypes.c_void_p),
+                ("y_stride", ctypes.c_int), ("post", ctypes.c_int), ("post_scale", ctypes.c_float)]
+
+
 _lib = None
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -72,6 +78,7 @@ def load_library():
         "qwattn_qsa_select": [_P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I],
         "qwattn_qsa_index": [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P, _I],
         "qwattn_mat": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P, _I, _I, _I, ctypes.c_float],
+        "qwattn_mat_multi": [_P, _P, _P, _I, _I, _I, _P, _I, _I],
         "qwattn_q8_unpack": [_P, _I, _I, _P, _P],
         "qwattn_qsa_key_bits": [_P, _P, _P, _I, _I, _I, _I, _P, _I],
         "qwattn_attend_partial_qsa": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P],
@@ -285,6 +292,16 @@ class Attention:
         rows, cols = w.shape
         self._check(self.lib.qwattn_mat(self.h, _stream(stream), _ptr(w), _ptr(s), int(q8), rows, cols, _ptr(x),
                                         x.stride(0), _ptr(y), y.stride(0), x.shape[0], post, post_scale))
+
+    def mat_multi(self, x, outs, stream=None):
+        """Several projections of x in one call (qwattn_mat_multi): outs = [(y, w, s), ...] (s None for float32
+        weights, all of one kind), each as in mat."""
+        q8 = outs[0][2] is not None
+        arr = (MatOut * len(outs))()
+        for i, (y, w, s) in enumerate(outs):
+            arr[i] = MatOut(_ptr(w), _ptr(s), w.shape[0], _ptr(y), y.stride(0), 0, 0.0)
+        self._check(self.lib.qwattn_mat_multi(self.h, _stream(stream), ctypes.cast(arr, ctypes.c_void_p), len(outs),
+                                              int(q8), x.shape[1], _ptr(x), x.stride(0), x.shape[0]))
 
     def qsa_key_bits(self, mask, cr, pos, n, key_bits, stream=None):
         """Per-key visibility bits [n, kb_words] from a block mask [n, mask_words] (shaders/attention.comp:35-43)."""

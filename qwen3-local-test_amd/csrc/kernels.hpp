@@ -174,4 +174,14 @@ struct MatArgs {
 constexpr int kGemmMinN = 16;
 hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s);
 
+// Up to kMatMulti matrices with the same input (x, cols, n, x_stride) in one launch; wg_end is filled by
+// launch_mat_multi.
+constexpr int kMatMulti = 4;
+struct MatMultiArgs {
+    MatArgs m[kMatMulti];
+    int wg_end[kMatMulti];
+    int count;
+};
+hipError_t launch_mat_multi(const MatMultiArgs& a, bool q8, hipStream_t s);
+
 }  // namespace qw

@@ -32,9 +32,9 @@ __device__ __forceinline__ float mat_wave_sum(float x) {
 
 // f32 weights: a wave's RW rows a 16-column group at a time (f32 projections are the small ones)
 template <int NTP, int RW>
-__global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
+__device__ __forceinline__ void mat_f32_body(const MatArgs& a, int bx) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r0 = (blockIdx.x * 4 + wave) * RW;
+    const int r0 = (bx * 4 + wave) * RW;
     const int t0 = blockIdx.y * NTP;
     const int nt = min(NTP, a.n - t0);
     if (r0 >= a.rows) return;  // whole waves
@@ -88,10 +88,10 @@ __global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
 // rows' 16 columns (cached: every wave reads them) and the dot products
 constexpr int kMatK = 4;
 template <int NTP, int RW>
-__global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
+__device__ __forceinline__ void mat_q8_body(const MatArgs& a, int bx) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r0 = (blockIdx.x * 4 + wave) * RW;
+    const int r0 = (bx * 4 + wave) * RW;
     const int t0 = blockIdx.y * NTP;
     const int nt = min(NTP, a.n - t0);
     if (r0 >= a.rows) return;  // whole waves
@@ -163,6 +163,26 @@ __global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
             }
             if (lane == 0 && r0 + r < a.rows && t < nt) a.y[(size_t)(t0 + t) * a.y_stride + r0 + r] = v;
         }
+}
+
+template <int NTP, int RW>
+__global__ __launch_bounds__(256) void k_mat_q8(MatArgs a) {
+    mat_q8_body<NTP, RW>(a, blockIdx.x);
+}
+template <int NTP, int RW>
+__global__ __launch_bounds__(256) void k_mat_f32(MatArgs a) {
+    mat_f32_body<NTP, RW>(a, blockIdx.x);
+}
+
+// Several matrices on one input in one launch: workgroups [wg_end[i-1], wg_end[i]) run matrix i (a
+// wave-uniform choice), so a decode step's query, key and value projections stream as one burst.
+template <bool Q8, int NTP, int RW>
+__global__ __launch_bounds__(256) void k_mat_multi(MatMultiArgs a) {
+    int i = 0;
+    while (i + 1 < a.count && (int)blockIdx.x >= a.wg_end[i]) i++;
+    const int bx = (int)blockIdx.x - (i ? a.wg_end[i - 1] : 0);
+    if constexpr (Q8) mat_q8_body<NTP, RW>(a.m[i], bx);
+    else mat_f32_body<NTP, RW>(a.m[i], bx);
 }
 
 // ---- many tokens: tiled MFMA GEMM ------------------------------------------------------------------
@@ -412,6 +432,38 @@ hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s) {
             else hipLaunchKernelGGL((k_mat_f32<kMatNTP, 1>), grid, block, 0, s, a);
         }
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_mat_multi(const MatMultiArgs& a0, bool q8, hipStream_t s) {
+    const MatArgs& f = a0.m[0];
+    if (f.n >= kGemmMinN && f.cols % 32 == 0) {  // the GEMM: one launch a matrix (each fills the chip)
+        for (int i = 0; i < a0.count; i++) {
+            const hipError_t e = launch_mat(a0.m[i], q8, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    MatMultiArgs a = a0;
+    int rows = 0;
+    for (int i = 0; i < a.count; i++) rows += a.m[i].rows;
+    const int ntp = f.n == 1 ? 1 : kMatNTP;
+    const bool rw4 = rows >= 4096;
+    int wg = 0;
+    for (int i = 0; i < a.count; i++) {
+        wg += (a.m[i].rows + (rw4 ? 15 : 3)) / (rw4 ? 16 : 4);
+        a.wg_end[i] = wg;
+    }
+    const dim3 grid(wg, (f.n + ntp - 1) / ntp), block(256);
+#define QW_MULTI(Q, N, R) hipLaunchKernelGGL((k_mat_multi<Q, N, R>), grid, block, 0, s, a)
+    if (q8) {
+        if (ntp == 1) { if (rw4) QW_MULTI(true, 1, 4); else QW_MULTI(true, 1, 1); }
+        else { if (rw4) QW_MULTI(true, kMatNTP, 4); else QW_MULTI(true, kMatNTP, 1); }
+    } else {
+        if (ntp == 1) { if (rw4) QW_MULTI(false, 1, 4); else QW_MULTI(false, 1, 1); }
+        else { if (rw4) QW_MULTI(false, kMatNTP, 4); else QW_MULTI(false, kMatNTP, 1); }
+    }
+#undef QW_MULTI
     return hipGetLastError();
 }
 

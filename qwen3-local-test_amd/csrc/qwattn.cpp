@@ -981,6 +981,29 @@ int qwattn_mat(qwattn_ctx* c, void* stream, const void* w, const float* s, int q
     return QWATTN_OK;
 }
 
+int qwattn_mat_multi(qwattn_ctx* c, void* stream, const qwattn_mat_out* mats, int count, int q8, int cols,
+                     const float* x, int x_stride, int n) {
+    if (!c) return QWATTN_EINVAL;
+    if (!mats || count < 1 || count > qw::kMatMulti)
+        return fail(c, QWATTN_EINVAL, "qwattn_mat_multi: %d matrices (1..%d)", count, qw::kMatMulti);
+    if (!x || cols <= 0 || n <= 0 || cols % (q8 ? 32 : 16) || x_stride < cols || x_stride % 4 || ((uintptr_t)x & 15))
+        return fail(c, QWATTN_EINVAL, "qwattn_mat_multi: cols %d (a multiple of %d), n %d, x_stride %d (>= cols, a multiple "
+                    "of 4), x 16-byte aligned", cols, q8 ? 32 : 16, n, x_stride);
+    qw::MatMultiArgs a{};
+    a.count = count;
+    for (int i = 0; i < count; i++) {
+        const qwattn_mat_out& m = mats[i];
+        if (!m.w || !m.y || (q8 && !m.s) || m.rows <= 0 || m.y_stride < m.rows || m.post < 0 || m.post > 1 ||
+            ((uintptr_t)m.w & 15))
+            return fail(c, QWATTN_EINVAL, "qwattn_mat_multi: matrix %d: rows %d, y_stride %d (>= rows), post %d, w and y set "
+                        "(w 16-byte aligned), s set for q8", i, m.rows, m.y_stride, m.post);
+        a.m[i] = qw::MatArgs{m.w, m.s, x, m.y, m.rows, cols, n, x_stride, m.y_stride, m.post, m.post_scale};
+    }
+    DeviceGuard dg(c->device);
+    HIP_TRY(c, qw::launch_mat_multi(a, q8 != 0, (hipStream_t)stream));
+    return QWATTN_OK;
+}
+
 int qwattn_q8_unpack(const uint8_t* blocks, int rows, int cols, int8_t* w, float* s) {
     if (!blocks || !w || !s || rows <= 0 || cols <= 0 || cols % 32) return QWATTN_EINVAL;
     for (int r = 0; r < rows; r++) {

@@ -175,3 +175,47 @@ def test_gemm_full_prefill_matches_matvec(qw):
     assert np.all(err <= 2e-5 * mag.T + 2e-6), float((err / mag.T).max())
     assert np.isfinite(y.cpu().numpy()).all()
     ctx.close()
+
+
+@pytest.mark.parametrize("n", [1, 4, 5, 40])
+def test_mat_multi_equals_separate_calls(qw, oracle, n):
+    """qwattn_mat_multi (one matrix-vector launch over several matrices below 16 tokens, one GEMM a matrix
+    from 16) gives each matrix the bits of its own qwattn_mat call, and the oracle's values: the attention
+    layer's query + gate, key and value projections of one input (8,192 + 512 + 512 rows, one row a wave
+    below 4,096 rows in total, four from there), then three small ones."""
+    print(f"mat_multi n={n}", flush=True)
+    ctx = _ctx(qw)
+    for shapes, cols in (([8192, 512, 512], 2048), ([100, 36, 64], 96)):
+        x = np.random.default_rng(91 + n).standard_normal((n, cols)).astype(np.float32)
+        xd = dev(x)
+        mats, outs, sep = [], [], []
+        for i, rows in enumerate(shapes):
+            blocks, _, _ = q8_blocks(92 + i + rows, rows, cols)
+            w8, s = qw.q8_unpack(blocks, rows, cols)
+            mats.append((w8, s))
+            wd, sd = dev(w8), dev(s)
+            y = torch.full((n, rows + 3), 7.0, device=DEV)[:, :rows]
+            outs.append((y, wd, sd))
+            ys = torch.empty((n, rows), device=DEV)
+            ctx.mat(xd, ys, wd, sd)
+            sep.append(ys)
+        ctx.mat_multi(xd, outs)
+        torch.cuda.synchronize()
+        for (y, _, _), ys, (w8, s) in zip(outs, sep, mats):
+            assert torch.equal(y, ys)
+            want = oracle.mat(x, w8=w8, s=s)
+            _check(y.cpu().numpy(), want, np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)), x)
+    ctx.close()
+
+
+def test_mat_multi_rejects_bad_input(qw):
+    ctx = _ctx(qw)
+    x = torch.zeros((1, 64), device=DEV)
+    w = torch.zeros((32, 64), dtype=torch.int8, device=DEV)
+    s = torch.zeros((32, 2), device=DEV)
+    y = torch.zeros((1, 32), device=DEV)
+    with pytest.raises(qw.QwattnError):
+        ctx.mat_multi(x, [(y, w, s)] * 5)  # more than 4 matrices
+    with pytest.raises(qw.QwattnError):
+        ctx.mat_multi(x[:, :48], [(y, w[:, :48], s)])  # 48 columns: not whole Q8 blocks
+    ctx.close()
