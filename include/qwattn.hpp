@@ -88,6 +88,12 @@ public:
               "qwattn_mat");
     }
 
+    // count projections of one input (qwattn_mat_multi: one launch below 16 tokens).
+    void mat_multi(void* stream, const qwattn_mat_out* mats, int count, bool q8, int cols, const float* x, int x_stride,
+                   int n) {
+        check(ctx_, qwattn_mat_multi(ctx_, stream, mats, count, q8 ? 1 : 0, cols, x, x_stride, n), "qwattn_mat_multi");
+    }
+
     // A QSA layer past its budget (Qwen4Vulkan::attention with `masked`, src/qwen4_vk.cpp:942-984): cache
     // and pool the pass's projected indexer keys, select each token's blocks into per-key visibility bits,
     // and run the layer's attention over the visible keys. raw [max_ctx][idx_dim] and pooled

@@ -77,12 +77,15 @@ private:
         att_.mat(stream_, m.w, m.s, m.q8, m.rows, m.cols, x, x_stride, y, m.rows, n);
     }
     // A full-attention layer l for n tokens on its normed input xn [n][hidden]: the q (query | gate), k and v
-    // projections, the attention body, then o_proj into h [n][hidden] (src/qwen4_vk.cpp:965-967, 994).
+    // projections, the attention body, then o_proj into h [n][hidden] (src/qwen4_vk.cpp:965-967, 994). The
+    // layer's matrices are all Q8_0 or all fp32, as the reference's upload makes them.
     void full_attention_layer(int l, int n, const float* xn, float* h) {
         const LayerMats& m = mats_[l];
-        mat(m.q, xn, qg_, n, cfg_.hidden);
-        mat(m.k, xn, k_, n, cfg_.hidden);
-        mat(m.v, xn, v_, n, cfg_.hidden);
+        // q, k and v share xn: one qwattn_mat_multi call (one launch for decode and verify passes)
+        const qwattn_mat_out qkv[3] = {{m.q.w, m.q.s, m.q.rows, qg_, m.q.rows, 0, 0.f},
+                                       {m.k.w, m.k.s, m.k.rows, k_, m.k.rows, 0, 0.f},
+                                       {m.v.w, m.v.s, m.v.rows, v_, m.v.rows, 0, 0.f}};
+        att_.mat_multi(stream_, qkv, 3, m.q.q8, cfg_.hidden, xn, cfg_.hidden, n);
         attention(l, n, qg_, k_, v_, att_out_);
         mat(m.o, att_out_, h, n, cfg_.n_heads * cfg_.head_dim);
     }
