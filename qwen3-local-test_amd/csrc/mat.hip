@@ -414,6 +414,7 @@ hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s) {
     // gives 256 workgroups a token group, else one (small matrices: more rows in flight at once)
     const int ntp = a.n == 1 ? 1 : kMatNTP;
     const bool rw4 = a.rows >= 4096;
+    if ((a.n + ntp - 1) / ntp > 65535) return hipErrorInvalidConfiguration;  // grid y limit (f32, cols % 32 != 0)
     const dim3 grid((a.rows + (rw4 ? 15 : 3)) / (rw4 ? 16 : 4), (a.n + ntp - 1) / ntp), block(256);
     if (q8) {
         if (ntp == 1) {
@@ -449,6 +450,7 @@ hipError_t launch_mat_multi(const MatMultiArgs& a0, bool q8, hipStream_t s) {
     for (int i = 0; i < a.count; i++) rows += a.m[i].rows;
     const int ntp = f.n == 1 ? 1 : kMatNTP;
     const bool rw4 = rows >= 4096;
+    if ((f.n + ntp - 1) / ntp > 65535) return hipErrorInvalidConfiguration;  // grid y limit (f32, cols % 32 != 0)
     int wg = 0;
     for (int i = 0; i < a.count; i++) {
         wg += (a.m[i].rows + (rw4 ? 15 : 3)) / (rw4 ? 16 : 4);
