@@ -3,11 +3,12 @@
 //
 // Replaces Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856) on its matrix-vector pipelines q4_matmul_q8 /
 // q4_matmul_f32 (shaders/q4_matmul.comp with the C_Q8 / C_F32 codecs of shaders/q4_codec.glsl; the planar
-// repacking of GGUF Q8_0 is src/qwen4_vk.cpp:98-106): every output is the fp32 dot product of a dequantized
+// repacking of GGUF Q8_0 is src/qwen4_vk.cpp:98-106) below 16 tokens, and on its tiled GEMM pipelines
+// q4_gemm_q8 / q4_gemm_f32 from 16 (further down): every output is the fp32 dot product of a dequantized
 // weight row (int8 times its block's scale) with a token's input row, then optionally silu(y * post_scale).
 //
-// MI355X design: the weights are read once per launch and are the bound (a decode step's projections are
-// memory-bound); a wave owns RW rows and a workgroup NTP tokens (one for a single token), lane l covering the
+// MI355X design of the matrix-vector kernels: the weights are read once per launch and are the bound (a
+// decode step's projections are memory-bound); a wave owns RW rows and a workgroup NTP tokens (one for a single token), lane l covering the
 // 16 consecutive columns 16 l + 1,024 k of every row, so a wave reads a kilobyte of each row per chunk in
 // one 16-byte load a lane (plus one scale a lane pair), and every weight load of a wave's rows is issued
 // before the first is used. A 16-column group never crosses a 32-weight block, so the lane applies its
@@ -19,7 +20,6 @@
 namespace qw {
 
 namespace {
-
 
 constexpr int kMatNTP = 4;  // tokens a workgroup
 
