@@ -471,6 +471,9 @@ def cpu_baseline(threads, budget_s):
                    f"{'reference cpu_kernels.cpp primitives compiled in place' if kind == 'reference' else 'C++ restatement'}"
                    f"; host {model}, {ncpu} CPUs visible"),
         "one_thread": {"value": round(byts / t1 / 1e9, 3), "ms_per_call": round(t1 * 1e3, 3), "calls": calls1},
+        # what the reference's CPU path actually streams: every Q head reads its group's K and V rows in fp32
+        "fp32_bytes_streamed": NH * 2 * (pos + n) * D * 4,
+        "fp32_streamed_GBps": round(NH * 2 * (pos + n) * D * 4 / t / 1e9, 3),
     }
 
 
