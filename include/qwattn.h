@@ -299,7 +299,8 @@ int qwattn_qsa_index(qwattn_ctx* ctx, void* stream, const void* ik, const void* 
 /* The projections either side of the attention layer: Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856) on its
  * matrix-vector pipelines q4_matmul_q8 / q4_matmul_f32 (shaders/q4_matmul.comp, codecs C_Q8 / C_F32 of
  * shaders/q4_codec.glsl) and, from 16 tokens, its tiled GEMM pipelines q4_gemm_q8 / q4_gemm_f32
- * (shaders/q4_gemm.comp; here on MFMA with fp32-level accuracy). y[t][r] (row stride y_stride) = sum_c W[r][c] x[t][c] (row stride x_stride) for
+ * (shaders/q4_gemm.comp; here on MFMA with fp32-level accuracy: a skinny kernel for Q8 up to 64 tokens, a
+ * tiled GEMM beyond). y[t][r] (row stride y_stride) = sum_c W[r][c] x[t][c] (row stride x_stride) for
  * t < n, r < rows, with W planar Q8_0 when q8 != 0 (w: int8 [rows][cols], s: float [rows][cols/32], one
  * scale per 32 consecutive weights of a row, as qwattn_q8_unpack writes them) or float [rows][cols] (s
  * unused); post 1 then applies y = silu(y * post_scale) (the shader's `post`). fp32 arithmetic. cols a
@@ -323,7 +324,7 @@ typedef struct qwattn_mat_out {
  * No counterpart in the reference, which issues one Qwen4Vulkan::mat per matrix (the query, key and value
  * projections of a full-attention layer: src/qwen4_vk.cpp:965-967); for callers that project one input
  * several ways: below 16 tokens one matrix-vector launch streams every matrix (one launch's latency
- * instead of count), from 16 tokens each matrix runs qwattn_mat's GEMM. All matrices share cols, q8, x,
+ * instead of count), from 16 tokens each matrix runs as its own qwattn_mat call. All matrices share cols, q8, x,
  * x_stride and n; each is checked as qwattn_mat checks it. */
 int qwattn_mat_multi(qwattn_ctx* ctx, void* stream, const qwattn_mat_out* mats, int count, int q8, int cols,
                      const float* x, int x_stride, int n);

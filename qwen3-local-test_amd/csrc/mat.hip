@@ -4,7 +4,8 @@
 // Replaces Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856) on its matrix-vector pipelines q4_matmul_q8 /
 // q4_matmul_f32 (shaders/q4_matmul.comp with the C_Q8 / C_F32 codecs of shaders/q4_codec.glsl; the planar
 // repacking of GGUF Q8_0 is src/qwen4_vk.cpp:98-106) below 16 tokens, and on its tiled GEMM pipelines
-// q4_gemm_q8 / q4_gemm_f32 from 16 (further down): every output is the fp32 dot product of a dequantized
+// q4_gemm_q8 / q4_gemm_f32 from 16 (further down: a skinny MFMA kernel for Q8 up to 64 tokens, a tiled
+// MFMA GEMM beyond): every output is the fp32 dot product of a dequantized
 // weight row (int8 times its block's scale) with a token's input row, then optionally silu(y * post_scale).
 //
 // MI355X design of the matrix-vector kernels: the weights are read once per launch and are the bound (a
@@ -215,6 +216,120 @@ __device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& hi, bf16
     }
 }
 
+// ---- a few tokens (16 to a few hundred), Q8: skinny MFMA kernel ------------------------------------
+// The tiled GEMM keeps too little in flight there (its 128-row tiles give the 8,192-row projection only 64
+// workgroups below 32 tokens). Here a workgroup owns 32 rows x 16 tokens and its four waves split the
+// columns; a wave loads its weights straight from HBM in the MFMA operand layout (lane (c, g): row c, the
+// 8 columns 8 g .. 8 g + 7 of a 32-column block, one 8-byte load), kSkK blocks at a time, all issued before
+// the first is used, with the token rows (fp32, split into bf16 hi / lo as in the GEMM) and the block
+// scales of its accumulator rows. Per block and 16-row tile: two MFMAs (hi, lo) into a fresh accumulator,
+// scaled into the running sum. The four waves' sums meet in LDS.
+#ifndef QW_SKINNY_MAX
+#define QW_SKINNY_MAX 64
+#endif
+constexpr int kSkinnyMaxN = QW_SKINNY_MAX;  // token counts the skinny kernel takes (from 16)
+// TT 16-token tiles a workgroup, KK blocks a batch
+template <int TT, int KK>
+__global__ __launch_bounds__(256) void k_mat_skinny(MatArgs a) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    __shared__ f32x4 s_acc[3][2][TT][64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+    const int r0 = blockIdx.x * 32, t0 = blockIdx.y * 16 * TT;
+    const int nkb = a.cols >> 5;
+    const int kb0 = wave * nkb / 4, kb1 = (wave + 1) * nkb / 4;  // this wave's blocks
+    const int8_t* w8 = static_cast<const int8_t*>(a.w);
+    const size_t arow[2] = {(size_t)min(r0 + c, a.rows - 1) * a.cols, (size_t)min(r0 + 16 + c, a.rows - 1) * a.cols};
+    int srow[2][4];  // accumulator rows of this lane: 16 m + 4 g + i
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) srow[m][i] = min(r0 + 16 * m + 4 * g + i, a.rows - 1);
+    const float* xrow[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) xrow[t] = a.x + (size_t)min(t0 + 16 * t + c, a.n - 1) * a.x_stride + 8 * g;
+    f32x4 acc[2][TT];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = kb0; kb < kb1; kb += KK) {
+        u32x2 wq[2][KK];
+        f32x4 xv[KK][TT][2];
+        float sc[2][4][KK];
+#pragma unroll
+        for (int j = 0; j < KK; j++) {
+            const int b = min(kb + j, kb1 - 1);  // past this wave's range: a repeat, unused
+#pragma unroll
+            for (int m = 0; m < 2; m++) wq[m][j] = *reinterpret_cast<const u32x2*>(w8 + arow[m] + b * 32 + 8 * g);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                xv[j][t][0] = *reinterpret_cast<const f32x4*>(xrow[t] + b * 32);
+                xv[j][t][1] = *reinterpret_cast<const f32x4*>(xrow[t] + b * 32 + 4);
+            }
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sc[m][i][j] = a.s[(size_t)srow[m][i] * nkb + b];
+        }
+#pragma unroll
+        for (int j = 0; j < KK; j++) {
+            if (kb + j >= kb1) break;  // uniform
+            bf16x8 av[2];
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int q = (int)wq[m][j][e / 4];
+                    av[m][e] = (__bf16)(float)((q << (24 - 8 * (e % 4))) >> 24);
+                }
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                float v8[8] = {xv[j][t][0][0], xv[j][t][0][1], xv[j][t][0][2], xv[j][t][0][3],
+                               xv[j][t][1][0], xv[j][t][1][1], xv[j][t][1][2], xv[j][t][1][3]};
+                bf16x8 bh, bl;
+                split_bf16(v8, bh, bl);
+#pragma unroll
+                for (int m = 0; m < 2; m++) {
+                    f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], bh, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], bl, p, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[m][t][i] = __builtin_fmaf(sc[m][i][j], p[i], acc[m][t][i]);
+                }
+            }
+        }
+    }
+    // the four waves' column ranges: sum in LDS, wave 0 writes (lane (c, g): token 16 t + c, rows 16 m + 4 g + i)
+    if (wave > 0) {
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int t = 0; t < TT; t++) s_acc[wave - 1][m][t][lane] = acc[m][t];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const int tok = t0 + 16 * t + c;
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                f32x4 v = acc[m][t];
+#pragma unroll
+                for (int w = 0; w < 3; w++) v += s_acc[w][m][t][lane];  // waves 1..3 in order
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int row = r0 + 16 * m + 4 * g + i;
+                    float y = v[i];
+                    if (a.post == 1) {
+                        const float u = y * a.post_scale;
+                        y = u / (1.0f + __expf(-u));
+                    }
+                    if (tok < a.n && row < a.rows) a.y[(size_t)tok * a.y_stride + row] = y;
+                }
+            }
+        }
+    }
+}
+
 template <bool Q8, int BN>
 __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
     constexpr int NT = BN / 32;                      // 16-token tiles a wave (BN = 32, 64 or 128)
@@ -391,6 +506,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
 }  // namespace
 
 hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s) {
+    if (q8 && a.n >= kGemmMinN && a.n <= kSkinnyMaxN && a.cols % 32 == 0) {
+        // 16 tokens a workgroup up to 16, 32 up to 32, then 64 (the weights re-read once per token group)
+        const int tt = a.n <= 16 ? 1 : a.n <= 32 ? 2 : 4;
+        const dim3 grid((a.rows + 31) / 32, (a.n + 16 * tt - 1) / (16 * tt));
+        if (tt == 1) hipLaunchKernelGGL((k_mat_skinny<1, 8>), grid, dim3(256), 0, s, a);
+        else if (tt == 2) hipLaunchKernelGGL((k_mat_skinny<2, 4>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_mat_skinny<4, 2>), grid, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     if (a.n >= kGemmMinN && a.cols % 32 == 0) {
         // the widest token tile that still gives two workgroups a CU (fewer weight re-reads), else the
         // narrowest (the most workgroups)

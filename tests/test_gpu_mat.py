@@ -95,12 +95,14 @@ def test_mat_rejects_bad_shapes(qw):
     ctx.close()
 
 
-# The tiled MFMA GEMM (16 tokens and up, columns a multiple of 32): partial row and token tiles and each token
-# tile width (128 when that still gives 512 workgroups, else 64 when that does, else 32), the attention
-# layer's shapes
+# The MFMA kernels from 16 tokens (columns a multiple of 32). Q8 up to 64 tokens: the skinny kernel with 16,
+# 32 or 64 tokens a workgroup (partial row and token tiles, waves with no column blocks at 96 columns);
+# beyond, and fp32 weights: the tiled GEMM with each token tile width (128 when that still gives 512
+# workgroups, else 64 when that does, else 32). The attention layer's shapes among them.
 GEMM_CASES = [(512, 2048, 16), (512, 2048, 200), (100, 96, 33), (37, 1056, 130), (2048, 4096, 64),
               (8192, 2048, 20), (300, 64, 257), (160, 256, 1100), (64, 64, 1500),
-              (8192, 64, 512), (8000, 96, 530), (8192, 64, 1100), (8000, 96, 1030)]
+              (8192, 64, 512), (8000, 96, 530), (8192, 64, 1100), (8000, 96, 1030),
+              (70, 64, 24), (45, 160, 17), (8192, 2048, 64), (33, 2048, 61)]
 
 
 @pytest.mark.parametrize("rows,cols,n", GEMM_CASES, ids=lambda v: str(v))
@@ -134,10 +136,12 @@ def test_gemm_f32_parity(qw, oracle, rows, cols, n):
     ctx.close()
 
 
-def test_gemm_strides_post_and_scale_range(qw, oracle):
-    """GEMM with x_stride / y_stride wider than the rows, post 1, outputs beyond `rows` untouched, and inputs
-    whose magnitudes span 2^-20 .. 2^20 (the hi / lo split keeps fp32 range and relative accuracy)."""
-    rows, cols, n = 200, 512, 40
+@pytest.mark.parametrize("n", [40, 200])
+def test_gemm_strides_post_and_scale_range(qw, oracle, n):
+    """The MFMA kernels (skinny at 40 tokens, tiled at 200) with x_stride / y_stride wider than the rows,
+    post 1, outputs beyond `rows` untouched, and inputs whose magnitudes span 2^-20 .. 2^20 (the hi / lo
+    split keeps fp32 range and relative accuracy)."""
+    rows, cols = 200, 512
     blocks, _, _ = q8_blocks(84, rows, cols)
     w8, s = qw.q8_unpack(blocks, rows, cols)
     r = np.random.default_rng(85)
