@@ -5,7 +5,9 @@
 // nonzero status into a qwattn::Error, the way a HipBackend would.
 //
 // Input (little-endian): int32 NH, NKV, D, R, npass, then npass int32 token counts, float32 theta, eps,
-// qn[D], kn[D], then per pass qg[n][NH][2D], k[n][NKV][D], v[n][NKV][D] (fp32). Output: per pass
+// qn[D], kn[D], then per pass qg[n][NH][2D], k[n][NKV][D], v[n][NKV][D] (fp32). A negative count -r is a
+// speculative rollback, not a pass: the position moves back r tokens (accept(keep) after a verify pass,
+// src/qwen4_vk.cpp:278-300; no call into the library, the next pass rewrites the rows). Output: per pass
 // out[n][NH][D] (fp32). Exit status: 0 ok, 2 bad input, 3 a qwattn::Error (message on stderr), 4 a HIP
 // runtime failure.
 #include <hip/hip_runtime_api.h>
@@ -51,10 +53,12 @@ int main(int argc, char** argv) {
     if (!read(in, ns.data(), npass) || !read(in, te, 2) || !read(in, qn.data(), D) || !read(in, kn.data(), D)) return 2;
     int total = 0, nmax = 0;
     for (int n : ns) {
-        if (n <= 0 || n > 1024) return 2;
+        if (n == 0 || n > 1024 || n < -1024) return 2;
+        if (n < 0) continue;
         total += n;
         nmax = std::max(nmax, n);
     }
+    if (nmax == 0) return 2;
     std::vector<float> out_all;
     try {
         qwattn::Context att(0, qwattn_config{NH, NKV, D, R, te[0], te[1], /*max_ctx*/ 4096, /*max_tokens*/ 1024,
@@ -74,6 +78,11 @@ int main(int argc, char** argv) {
         int pos = 0;
         for (int p = 0; p < npass; p++) {
             const int n = ns[p];
+            if (n < 0) {  // rollback: reject the last -n tokens
+                if (pos + n < 0) return 2;
+                pos += n;
+                continue;
+            }
             std::vector<float> hqg((size_t)n * NH * 2 * D), hk((size_t)n * NKV * D), hv((size_t)n * NKV * D),
                 hout((size_t)n * NH * D);
             if (!read(in, hqg.data(), hqg.size()) || !read(in, hk.data(), hk.size()) || !read(in, hv.data(), hv.size()))

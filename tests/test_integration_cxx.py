@@ -58,6 +58,9 @@ def _write_input(path, s, ns, seed=0):
         f.write(qn.astype("<f4").tobytes())
         f.write(kn.astype("<f4").tobytes())
         for i, n in enumerate(ns):
+            if n < 0:  # a rollback entry carries no data
+                qg_all.append(None), k_all.append(None), v_all.append(None)
+                continue
             qg, k, v, _, _ = projections(seed + 10 + i, n, s)
             f.write(qg.astype("<f4").tobytes())
             f.write(k.astype("<f4").tobytes())
@@ -83,17 +86,21 @@ def test_driver_throws_without_gpu(tmp_path):
 @pytest.mark.gpu
 def test_driver_matches_oracle(oracle, tmp_path):
     s = QWEN3_NEXT
-    ns = [300, 4, 1, 1]  # prefill chunk, 1 + 3 drafts, then decode steps
+    ns = [300, 4, -2, 1, 1]  # prefill chunk, 1 + 3 drafts, accept(2) (two drafts rejected), then decode steps
     inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
     qgs, ks, vs, qn, kn = _write_input(inp, s, ns, seed=5)
     print(f"layer_driver over {ns}", flush=True)
     r = subprocess.run([_driver(), str(inp), str(outp)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, (r.returncode, r.stderr)
     got = np.fromfile(outp, dtype="<f4")
-    ref_k = np.zeros((sum(ns), s.NKV, s.D), np.float32)
-    ref_v = np.zeros((sum(ns), s.NKV, s.D), np.float32)
+    rows = sum(n for n in ns if n > 0)
+    ref_k = np.zeros((rows, s.NKV, s.D), np.float32)
+    ref_v = np.zeros((rows, s.NKV, s.D), np.float32)
     pos, off = 0, 0
     for i, n in enumerate(ns):
+        if n < 0:  # rollback: the next pass rewrites the rejected rows
+            pos += n
+            continue
         rq, rk, rv = oracle.qk_norm_rope(qgs[i], ks[i], vs[i], 1 + qn, 1 + kn, pos, s.R, s.theta, s.eps)
         ref_k[pos:pos + n] = rk[pos:pos + n].astype(np.float16)
         ref_v[pos:pos + n] = rv[pos:pos + n].astype(np.float16)
