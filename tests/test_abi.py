@@ -71,3 +71,11 @@ def test_q8_unpack_host():
     assert np.array_equal(w, w8) and np.array_equal(sc, s)
     lib = qw.load_library()
     assert lib.qwattn_q8_unpack(None, rows, cols, None, None) == qw.EINVAL
+
+
+def test_projection_entry_points_need_a_context():
+    """qwattn_mat and qwattn_mat_multi without a context return QWATTN_EINVAL (no device touched)."""
+    qw = common.load_package()
+    lib = qw.load_library()
+    assert lib.qwattn_mat(None, None, None, None, 1, 64, 64, None, 64, None, 64, 1, 0, 0.0) == qw.EINVAL
+    assert lib.qwattn_mat_multi(None, None, None, 1, 1, 64, None, 64, 1) == qw.EINVAL
