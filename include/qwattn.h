@@ -299,8 +299,8 @@ int qwattn_qsa_index(qwattn_ctx* ctx, void* stream, const void* ik, const void* 
 /* The projections either side of the attention layer: Qwen4Vulkan::mat (src/qwen4_vk.cpp:848-856) on its
  * matrix-vector pipelines q4_matmul_q8 / q4_matmul_f32 (shaders/q4_matmul.comp, codecs C_Q8 / C_F32 of
  * shaders/q4_codec.glsl) and, from 16 tokens, its tiled GEMM pipelines q4_gemm_q8 / q4_gemm_f32
- * (shaders/q4_gemm.comp; here on MFMA with fp32-level accuracy: a skinny kernel for Q8 up to 64 tokens, a
- * tiled GEMM beyond). y[t][r] (row stride y_stride) = sum_c W[r][c] x[t][c] (row stride x_stride) for
+ * (shaders/q4_gemm.comp; here on MFMA with fp32-level accuracy: a skinny kernel for Q8 up to 64 tokens and
+ * for Q8 matrices of up to 1,024 rows, a tiled GEMM otherwise). y[t][r] (row stride y_stride) = sum_c W[r][c] x[t][c] (row stride x_stride) for
  * t < n, r < rows, with W planar Q8_0 when q8 != 0 (w: int8 [rows][cols], s: float [rows][cols/32], one
  * scale per 32 consecutive weights of a row, as qwattn_q8_unpack writes them) or float [rows][cols] (s
  * unused); post 1 then applies y = silu(y * post_scale) (the shader's `post`). fp32 arithmetic. cols a
