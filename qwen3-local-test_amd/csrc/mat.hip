@@ -504,10 +504,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(MatArgs a) {
 }  // namespace
 
 hipError_t launch_mat(const MatArgs& a, bool q8, hipStream_t s) {
-    // the skinny kernel up to 64 tokens, and at any token count for matrices of up to 1,024 rows (whose
-    // 128-row GEMM tiles would leave most CUs idle: 512 x 2,048 at 2,048 tokens 51 -> 45 us, at 256 tokens
-    // 39 -> 26 us)
-    if (q8 && a.n >= kGemmMinN && (a.n <= kSkinnyMaxN || a.rows <= kSkinnyMaxRows) && a.cols % 32 == 0) {
+    // the skinny kernel up to 64 tokens, at any token count for matrices of up to 1,024 rows, and wherever
+    // the GEMM would have fewer than 256 tiles of 128 rows x 32 tokens (it would leave most CUs idle:
+    // 512 x 2,048 at 2,048 tokens 51 -> 45 us, at 256 tokens 39 -> 26 us; 2,048 x 4,096 at 256 tokens
+    // 89 -> 48 us)
+    const int t32 = ((a.rows + kGemmBM - 1) / kGemmBM) * ((a.n + 31) / 32);
+    if (q8 && a.n >= kGemmMinN && (a.n <= kSkinnyMaxN || a.rows <= kSkinnyMaxRows || t32 < 256) && a.cols % 32 == 0) {
         // 16 tokens a workgroup up to 16, 32 up to 32, then 64 (the weights re-read once per token group)
         const int tt = a.n <= 16 ? 1 : a.n <= 32 ? 2 : 4;
         const dim3 grid((a.rows + 31) / 32, (a.n + 16 * tt - 1) / (16 * tt));

@@ -95,15 +95,15 @@ def test_mat_rejects_bad_shapes(qw):
     ctx.close()
 
 
-# The MFMA kernels from 16 tokens (columns a multiple of 32). Q8 up to 64 tokens, and Q8 matrices of up to
-# 1,024 rows at any token count: the skinny kernel with 16, 32 or 64 tokens a workgroup (partial row and
+# The MFMA kernels from 16 tokens (columns a multiple of 32). Q8 up to 64 tokens, Q8 matrices of up to 1,024
+# rows at any token count, and Q8 launches the GEMM would cut into fewer than 256 tiles: the skinny kernel with 16, 32 or 64 tokens a workgroup (partial row and
 # token groups, waves with no column blocks at 96 columns); otherwise, and fp32 weights: the tiled GEMM with
 # each token tile width (128 when that still gives 512 workgroups, else 64 when that does, else 32). The
 # attention layer's shapes among them.
 GEMM_CASES = [(512, 2048, 16), (512, 2048, 200), (100, 96, 33), (37, 1056, 130), (2048, 4096, 64),
               (8192, 2048, 20), (300, 64, 257), (160, 256, 1100), (64, 64, 1500),
               (8192, 64, 512), (8000, 96, 530), (8192, 64, 1100), (8000, 96, 1030),
-              (70, 64, 24), (45, 160, 17), (8192, 2048, 64), (33, 2048, 61), (2000, 96, 100), (1100, 64, 300)]
+              (70, 64, 24), (45, 160, 17), (8192, 2048, 64), (33, 2048, 61), (2000, 96, 100), (1100, 64, 300), (4096, 64, 300), (2048, 64, 100)]
 
 
 @pytest.mark.parametrize("rows,cols,n", GEMM_CASES, ids=lambda v: str(v))
