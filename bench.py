@@ -30,6 +30,8 @@ Two projection workloads (proj_q8_n1, proj_q8_n4) time the layer's four projecti
 token and a 4-token verify pass (query + gate, key and value in one qwattn_mat_multi call, which shares the
 layer input, then the output projection); their bytes are the weights, read once a step. A third (proj_q8_n2048) runs
 them over a 2,048-token prefill chunk on the tiled MFMA GEMM and reports TFLOP/s (2 n rows cols a projection).
+layer_32k_q8 times a whole full-attention layer at decode (32,768 cached + 1): the query + gate, key and value
+projections, the attention layer body and the output projection; its bytes are the K/V rows and the weights.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -289,6 +291,50 @@ class MatWorkload:
         self.att.close()
 
 
+class LayerWorkload(Workload):
+    """A whole full-attention layer step at decode: the query + gate, key and value projections of the layer
+    input (one qwattn_mat_multi call), the attention layer body (the one-launch decode), then the output
+    projection, on planar Q8_0 weights of the MatWorkload shapes; every layer slot has its own cache and its
+    own weights. Bytes: the K/V rows and the weights, each read once."""
+
+    def __init__(self, qw, name, pos, n, slots, seed=0):
+        import torch
+        super().__init__(qw, name, pos, n, slots, 0, "f32", 0.0, seed)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 3000)
+        self.w = []
+        for _ in range(slots):
+            mats = []
+            for rows, cols in MatWorkload.SHAPES:
+                w8 = torch.randint(-127, 128, (rows, cols), dtype=torch.int8, device="cuda", generator=g)
+                sc = 0.002 * (0.5 + torch.rand((rows, cols // 32), device="cuda", generator=g))
+                mats.append((w8, sc))
+            self.w.append(mats)
+        self.x = torch.randn((n, MatWorkload.HIDDEN), device="cuda", generator=g)
+        self.h = torch.zeros((n, MatWorkload.HIDDEN), device="cuda")
+        self.layer = True
+        self.weight_bytes = sum(rows * cols + rows * cols // 32 * 4 for rows, cols in MatWorkload.SHAPES)
+        torch.cuda.synchronize()
+
+    def _qkv(self, slot):
+        n = self.n
+        self.att.mat_multi(self.x, [(self.qg.view(n, -1), *self.w[slot][0]), (self.k.view(n, -1), *self.w[slot][1]),
+                                    (self.v.view(n, -1), *self.w[slot][2])])
+
+    def step(self, slot):
+        self._qkv(slot)
+        super().step(slot)
+        self.att.mat(self.out.view(self.n, -1), self.h, *self.w[slot][3])
+
+    def step_events(self, slot, ev):
+        ev[0].record()
+        self._qkv(slot)
+        ev[1].record()
+        super().step(slot)
+        self.att.mat(self.out.view(self.n, -1), self.h, *self.w[slot][3])
+        ev[2].record()
+
+
 def gpu_sleep(ms):
     """Keeps the stream busy for about `ms` milliseconds, so that the launches queued behind it start
     back to back and their HIP events time the kernels, not the host's launch latency."""
@@ -379,7 +425,11 @@ def run_workload(wl, steps, warmup, graph):
     r = {"timed_steps": timed_steps, "us_per_step": wall / timed_steps * 1e6, "us_kernels": statistics.mean(k_all),
          "us_main": statistics.median(per_launch), "us_main_batches": len(per_launch),
          "us_main_min": min(per_launch)}
-    if getattr(wl, "mat", False):
+    if getattr(wl, "layer", False):
+        r.update({"kernel": "k_mat_multi (query + gate, key, value) + k_decode_ld (attention) + k_mat_q8 (output)",
+                  "us_qkv_projections": statistics.mean(k_first), "us_attention_and_output": statistics.mean(k_second),
+                  "us_main_is": "k_decode_ld alone"})
+    elif getattr(wl, "mat", False):
         kern = ("k_gemm<q8> (tiled MFMA GEMM, one launch a projection" if wl.n >= 16 else
                 "k_mat_multi<q8> + k_mat_q8 (matrix-vector: query + gate, key and value in one launch, then output")
         r.update({"kernel": kern + "; the per-launch figure is the 8,192 x 2,048 query + gate projection alone)",
@@ -533,6 +583,8 @@ def main():
         ("proj_q8_n4", 0, 4, args.slots, 0, "f32", 0.0),
         # and a 2,048-token prefill chunk (the tiled MFMA GEMM)
         ("proj_q8_n2048", 0, 2048, 8, 0, "f32", 0.0),
+        # the whole full-attention layer at decode: projections around the attention body
+        ("layer_32k_q8", 32768, 1, args.slots, 0, "f32", 0.0),
     ]
     results = {}
     for name, pos, n, slots, n_split, dt, heavy in configs:
@@ -542,12 +594,15 @@ def main():
               flush=True)
         if name.startswith("proj_"):
             wl = MatWorkload(qw, name, n, slots, seed=len(results))
+        elif name.startswith("layer_"):
+            wl = LayerWorkload(qw, name, pos, n, slots, seed=len(results))
         elif "_qsa" in name:
             wl = QsaWorkload(qw, name, pos, n, slots, int(heavy), seed=len(results))
         else:
             wl = Workload(qw, name, pos, n, slots, n_split, dt, heavy, seed=len(results))
         r = run_workload(wl, args.steps, args.warmup, graph)
         wl_bytes = getattr(wl, "bytes", 0)
+        wl_weight_bytes = getattr(wl, "weight_bytes", 0)
         wl.close()
         del wl
         torch.cuda.empty_cache()
@@ -559,6 +614,13 @@ def main():
             r["algorithmic_flops"] = flops
             r["frac_mfma_step"] = flops / (r["us_per_step"] * 1e-6) / MFMA_F16_PEAK
             r["frac_mfma_kernel"] = 2 * n * NH * 2 * D * 2048 / (r["us_main"] * 1e-6) / MFMA_F16_PEAK
+        elif name.startswith("layer_"):
+            # the K/V rows and the weights, each read once a step; us_first_event = the q/k/v projections
+            byts = kv_bytes(pos + n) + wl_weight_bytes
+            r["value"] = byts / (r["us_per_step"] * 1e-6) / 1e9
+            r["unit"] = "GB/s (K/V + weights)"
+            r["algorithmic_bytes"] = byts
+            r["frac_hbm_step"] = byts / (r["us_per_step"] * 1e-6) / HBM_PEAK
         elif name.startswith("proj_"):
             # the weights read once; the per-launch figure is the largest projection's
             r["value"] = wl_bytes / (r["us_per_step"] * 1e-6) / 1e9
