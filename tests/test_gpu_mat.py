@@ -224,3 +224,31 @@ def test_mat_multi_rejects_bad_input(qw):
     with pytest.raises(qw.QwattnError):
         ctx.mat_multi(x[:, :48], [(y, w[:, :48], s)])  # 48 columns: not whole Q8 blocks
     ctx.close()
+
+
+@pytest.mark.parametrize("n", [1, 4, 20])
+def test_mat_multi_f32_equals_separate_calls(qw, oracle, n):
+    """qwattn_mat_multi on fp32 weights (the matrix-vector kernel below 16 tokens, the GEMM from 16): each
+    matrix gets the bits of its own qwattn_mat call and the oracle's values."""
+    print(f"mat_multi f32 n={n}", flush=True)
+    ctx = _ctx(qw)
+    r = np.random.default_rng(95 + n)
+    cols = 128
+    x = r.standard_normal((n, cols)).astype(np.float32)
+    xd = dev(x)
+    outs, sep, ws = [], [], []
+    for rows in (96, 40, 200):
+        w = (0.05 * r.standard_normal((rows, cols))).astype(np.float32)
+        ws.append(w)
+        wd = dev(w)
+        y = torch.empty((n, rows), device=DEV)
+        outs.append((y, wd, None))
+        ys = torch.empty((n, rows), device=DEV)
+        ctx.mat(xd, ys, wd)
+        sep.append(ys)
+    ctx.mat_multi(xd, outs)
+    torch.cuda.synchronize()
+    for (y, _, _), ys, w in zip(outs, sep, ws):
+        assert torch.equal(y, ys)
+        _check(y.cpu().numpy(), oracle.mat(x, wf=w), np.abs(w), x)
+    ctx.close()
