@@ -103,6 +103,11 @@ int qwattn_sync_status(qwattn_ctx* ctx, void* stream);
  * combine waits for; nonzero makes every flag look stale, so the wait gives up after spin_max polls while
  * every kernel still ends normally. Production code leaves both at 0. */
 int qwattn_set_wait_limits(qwattn_ctx* ctx, int spin_max, int epoch_skew);
+/* Test hook of the K/V allocation failure path (no reference counterpart). nth > 0: the nth K/V buffer
+ * allocation of the next qwattn_kv_alloc or qwattn_kv_grow fails as an out-of-memory hipMalloc would (slot
+ * order, K before V; counted within that call), then the hook clears itself. 0 = off. Production code never
+ * calls it. */
+int qwattn_set_alloc_fault(qwattn_ctx* ctx, int nth);
 int qwattn_get_config(const qwattn_ctx* ctx, qwattn_config* cfg);
 /* Device address of the context's rope table ([max_ctx][R/2][2] fp32). */
 int qwattn_rope_table(const qwattn_ctx* ctx, const float** rope);
@@ -114,11 +119,14 @@ int qwattn_fill_rope(qwattn_ctx* ctx, void* stream, float* rope, int n_pos);
 /* ---- KV cache owned by the context (reference: alloc_state / ensure_kv, src/qwen4_vk.cpp:565-574,
  * 657-685) ---- */
 /* Allocates n_slots (one per full-attention layer) K and V caches of `cap` tokens (rounded up to a
- * multiple of 32, at most max_ctx rounded up), zero-filled. Any previous caches are freed. */
+ * multiple of 32, at most max_ctx rounded up), zero-filled. Any previous caches are freed. On failure
+ * (QWATTN_ENOMEM) no cache is left allocated. Reference: alloc_state, src/qwen4_vk.cpp:565-574. */
 int qwattn_kv_alloc(qwattn_ctx* ctx, int n_slots, int cap);
 /* Grows every slot to hold `tokens` positions: new capacity max(2*cap, tokens), at most max_ctx,
  * copying each slot's rows; no-op when tokens <= cap. Synchronizes `stream`. Same contract as
- * ensure_kv: call between passes. */
+ * ensure_kv (src/qwen4_vk.cpp:657-685): call between passes. All or nothing: on QWATTN_ENOMEM (the
+ * reference's "out of VRAM growing the K/V caches") or another error every slot, its contents and the
+ * capacity are as before the call. */
 int qwattn_kv_grow(qwattn_ctx* ctx, void* stream, int tokens);
 /* Current capacity in tokens and the device addresses of one slot's caches. */
 int qwattn_kv_slot(const qwattn_ctx* ctx, int slot, void** kcache, void** vcache, int* cap);
@@ -329,9 +337,11 @@ typedef struct qwattn_mat_out {
 int qwattn_mat_multi(qwattn_ctx* ctx, void* stream, const qwattn_mat_out* mats, int count, int q8, int cols,
                      const float* x, int x_stride, int n);
 
-/* GGUF Q8_0 rows (per 32 weights: an IEEE binary16 scale, then 32 int8) to the planar form qwattn_mat takes
- * (host memory, no GPU): the reference's upload repacking, unpack_q8_row (src/qwen4_vk.cpp:98-106). cols a
- * multiple of 32. Returns QWATTN_OK or QWATTN_EINVAL. */
+/* GGUF Q8_0 rows (per 32 weights: a binary16 scale, then 32 int8) to the planar form qwattn_mat takes
+ * (host memory, no GPU): the reference's upload repacking, unpack_q8_row (src/qwen4_vk.cpp:98-106). Each
+ * scale is widened as ck::half_to_f32 widens it (src/cpu_kernels.cpp:20-34), bit for bit: exponent 31 is an
+ * ordinary exponent there (0x7C00 gives 65536, not inf). cols a multiple of 32. Returns QWATTN_OK or
+ * QWATTN_EINVAL. */
 int qwattn_q8_unpack(const uint8_t* blocks, int rows, int cols, int8_t* w, float* s);
 
 /* The per-key visibility bits from a block mask in the reference's format (mask[t][mask_words], as the

@@ -89,6 +89,7 @@ def load_library():
         "qwattn_decode_noalloc": [_I, _P, ctypes.POINTER(Config), _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I,
                                   _I, _P, ctypes.POINTER(_I)],
         "qwattn_set_wait_limits": [_P, _I, _I],
+        "qwattn_set_alloc_fault": [_P, _I],
     }
     for name, args in sig.items():
         f = getattr(lib, name)
@@ -132,6 +133,34 @@ def _stream(stream):
 
 
 _DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+def _check_weights(w, s):
+    """(rows, cols) of a projection's weights: int8 [rows, cols] with float32 scales s [rows, cols/32] (planar
+    Q8_0), or float32 [rows, cols] with s None; both contiguous, as the C ABI reads them."""
+    if w.dim() != 2 or not w.is_contiguous():
+        raise ValueError(f"weights must be a contiguous [rows, cols] matrix, got shape {tuple(w.shape)}")
+    rows, cols = w.shape
+    if s is None:
+        if w.dtype != torch.float32:
+            raise ValueError(f"float weights must be float32, got {w.dtype} (int8 weights need scales)")
+    else:
+        if w.dtype != torch.int8:
+            raise ValueError(f"Q8 weights must be int8, got {w.dtype}")
+        if s.dtype != torch.float32 or not s.is_contiguous() or tuple(s.shape) != (rows, cols // 32):
+            raise ValueError(f"Q8 scales must be contiguous float32 [{rows}, {cols // 32}], got {s.dtype} "
+                             f"{tuple(s.shape)}")
+    return rows, cols
+
+
+def _check_rows(t, name, width, n=None):
+    """A float32 [n, >= width] operand with unit column stride (row stride free)."""
+    if t.dtype != torch.float32 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be float32 [n, >= {width}] with unit column stride")
+    if t.shape[1] < width:
+        raise ValueError(f"{name} has {t.shape[1]} columns, needs >= {width}")
+    if n is not None and t.shape[0] < n:
+        raise ValueError(f"{name} has {t.shape[0]} rows, needs >= {n}")
 
 
 BLK = 32  # positions per cache block
@@ -288,20 +317,31 @@ class Attention:
     def mat(self, x, y, w, s=None, post=0, post_scale=0.0, stream=None):
         """y [n, >= rows] = x [n, >= cols] W^T (Qwen4Vulkan::mat): W planar Q8 (w int8 [rows, cols] with s
         [rows, cols/32]) or float32 w [rows, cols]; post 1 applies silu(y * post_scale)."""
-        q8 = s is not None
-        rows, cols = w.shape
-        self._check(self.lib.qwattn_mat(self.h, _stream(stream), _ptr(w), _ptr(s), int(q8), rows, cols, _ptr(x),
-                                        x.stride(0), _ptr(y), y.stride(0), x.shape[0], post, post_scale))
+        rows, cols = _check_weights(w, s)
+        _check_rows(x, "x", cols)
+        _check_rows(y, "y", rows, n=x.shape[0])
+        self._check(self.lib.qwattn_mat(self.h, _stream(stream), _ptr(w), _ptr(s), int(s is not None), rows, cols,
+                                        _ptr(x), x.stride(0), _ptr(y), y.stride(0), x.shape[0], post, post_scale))
 
     def mat_multi(self, x, outs, stream=None):
         """Several projections of x in one call (qwattn_mat_multi): outs = [(y, w, s), ...] (s None for float32
-        weights, all of one kind), each as in mat."""
+        weights, all of one kind and one column count), each as in mat."""
+        if not outs:
+            raise ValueError("mat_multi: no matrices")
         q8 = outs[0][2] is not None
+        cols = _check_weights(outs[0][1], outs[0][2])[1]
+        _check_rows(x, "x", cols)
         arr = (MatOut * len(outs))()
         for i, (y, w, s) in enumerate(outs):
-            arr[i] = MatOut(_ptr(w), _ptr(s), w.shape[0], _ptr(y), y.stride(0), 0, 0.0)
+            if (s is not None) != q8:
+                raise ValueError(f"mat_multi: matrix {i} mixes Q8 and float32 weights")
+            rows, c = _check_weights(w, s)
+            if c != cols:
+                raise ValueError(f"mat_multi: matrix {i} has {c} columns, matrix 0 has {cols}")
+            _check_rows(y, f"y[{i}]", rows, n=x.shape[0])
+            arr[i] = MatOut(_ptr(w), _ptr(s), rows, _ptr(y), y.stride(0), 0, 0.0)
         self._check(self.lib.qwattn_mat_multi(self.h, _stream(stream), ctypes.cast(arr, ctypes.c_void_p), len(outs),
-                                              int(q8), x.shape[1], _ptr(x), x.stride(0), x.shape[0]))
+                                              int(q8), cols, _ptr(x), x.stride(0), x.shape[0]))
 
     def qsa_key_bits(self, mask, cr, pos, n, key_bits, stream=None):
         """Per-key visibility bits [n, kb_words] from a block mask [n, mask_words] (shaders/attention.comp:35-43)."""
@@ -372,6 +412,10 @@ class Attention:
     def set_wait_limits(self, spin_max=0, epoch_skew=0):
         """Test hook of the decode kernels' bounded waits (0, 0 = production defaults)."""
         self._check(self.lib.qwattn_set_wait_limits(self.h, spin_max, epoch_skew))
+
+    def set_alloc_fault(self, nth):
+        """Test hook: the nth K/V buffer allocation of the next kv_alloc / kv_grow fails (0 = off)."""
+        self._check(self.lib.qwattn_set_alloc_fault(self.h, nth))
 
     def layer_attention(self, slot, qg, k, v, qn, kn, out, pos, n, n_split=0, stream=None):
         self._check(self.lib.qwattn_layer_attention(self.h, _stream(stream), slot, _ptr(qg), _ptr(k), _ptr(v),

@@ -509,15 +509,22 @@ static int select_kr(int nmax) {
     return 0;
 }
 
+// Largest indexer width the host accepts (heads x dims); the select's dynamic LDS grows with it.
+constexpr int kQsaMaxHeadDims = 8192;
+
 template <int IN_DT, int KR, int MODE, int CH = kQsaChunk>
 static hipError_t launch_select_kr(const QsaSelectArgs& a, size_t shm, dim3 grid, hipStream_t s) {
-    static std::atomic<uint64_t> raised{0};  // per device: dynamic LDS limit raised (bit per device)
+    // The dynamic LDS limit is raised once per device to what the widest accepted indexer needs, so a later
+    // call with more heads x dims than the first one still fits it.
+    static std::atomic<uint64_t> raised{0};  // bit per device
+    static const size_t shm_max = qsa_select_lds(1, kQsaMaxHeadDims);
+    if (shm > shm_max) return hipErrorInvalidValue;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load(std::memory_order_acquire) & bit)) {
         const hipError_t e = hipFuncSetAttribute((const void*)k_qsa_select<IN_DT, KR, MODE, CH>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm_max);
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }

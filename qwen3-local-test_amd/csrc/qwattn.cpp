@@ -45,6 +45,7 @@ struct qwattn_ctx {
     int* wait_err_dev = nullptr;   // its device address
     int spin_max = qw::kSpinDefault;
     int epoch_skew = 0;
+    int alloc_fault = 0;         // test hook: the alloc_fault-th K/V buffer allocation of the next call fails
     std::string err;
 };
 
@@ -331,28 +332,59 @@ int qwattn_fill_rope(qwattn_ctx* c, void* stream, float* rope, int n_pos) {
 
 // ---- KV cache ---------------------------------------------------------------------------------------
 
+// One K/V cache buffer; fails as hipMalloc does when the test hook qwattn_set_alloc_fault names this
+// allocation (counted from 1 within the calling qwattn_kv_alloc / qwattn_kv_grow).
+static hipError_t kv_malloc(qwattn_ctx* c, uint16_t** p, size_t bytes, int& nth) {
+    *p = nullptr;
+    if (c->alloc_fault && ++nth == c->alloc_fault) {
+        c->alloc_fault = 0;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc((void**)p, bytes);
+}
+
+static void free_all(std::vector<uint16_t*>& v) {
+    for (auto*& p : v) {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+    }
+}
+
 int qwattn_kv_alloc(qwattn_ctx* c, int n_slots, int cap) {
     if (!c) return QWATTN_EINVAL;
     if (n_slots <= 0 || cap <= 0) return fail(c, QWATTN_EINVAL, "qwattn_kv_alloc: %d slots of %d tokens", n_slots, cap);
     cap = std::min((cap + 31) / 32 * 32, (c->cfg.max_ctx + 31) / 32 * 32);
     DeviceGuard dg(c->device);
-    for (auto* p : c->kc) (void)hipFree(p);
-    for (auto* p : c->vc) (void)hipFree(p);
+    free_all(c->kc);
+    free_all(c->vc);
     c->kc.assign(n_slots, nullptr);
     c->vc.assign(n_slots, nullptr);
     c->kv_cap = 0;
     const size_t bytes = (size_t)cap * c->cfg.n_kv_heads * c->cfg.head_dim * 2;
-    for (int s = 0; s < n_slots; s++) {
-        if (hipMalloc(&c->kc[s], bytes) != hipSuccess || hipMalloc(&c->vc[s], bytes) != hipSuccess)
-            return fail(c, QWATTN_ENOMEM, "out of device memory allocating the K/V caches");
-        HIP_TRY(c, hipMemset(c->kc[s], 0, bytes));
-        HIP_TRY(c, hipMemset(c->vc[s], 0, bytes));
+    int nth = 0;
+    hipError_t e = hipSuccess;
+    for (int s = 0; s < n_slots && e == hipSuccess; s++) {
+        e = kv_malloc(c, &c->kc[s], bytes, nth);
+        if (e == hipSuccess) e = kv_malloc(c, &c->vc[s], bytes, nth);
+        if (e == hipSuccess) e = hipMemset(c->kc[s], 0, bytes);
+        if (e == hipSuccess) e = hipMemset(c->vc[s], 0, bytes);
     }
-    HIP_TRY(c, hipDeviceSynchronize());
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {  // nothing half-allocated stays behind: no cache at all, as before the first call
+        free_all(c->kc);
+        free_all(c->vc);
+        c->kc.clear();
+        c->vc.clear();
+        return e == hipErrorOutOfMemory ? fail(c, QWATTN_ENOMEM, "out of device memory allocating the K/V caches")
+                                        : fail(c, QWATTN_EHIP, "qwattn_kv_alloc: %s", hipGetErrorString(e));
+    }
     c->kv_cap = cap;
     return QWATTN_OK;
 }
 
+// All or nothing, as src/qwen4_vk.cpp:657-685 throws before touching the old caches: every slot's new
+// buffers are allocated and filled first; any failure frees them and leaves every slot and kv_cap as they
+// were. Only then are the old buffers freed and the new ones swapped in.
 int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
     if (!c) return QWATTN_EINVAL;
     if (c->kc.empty()) return fail(c, QWATTN_ESTATE, "qwattn_kv_grow: no K/V cache allocated");
@@ -366,32 +398,48 @@ int qwattn_kv_grow(qwattn_ctx* c, void* stream, int tokens) {
     const int nkv = c->cfg.n_kv_heads;
     const size_t per = (size_t)c->cfg.head_dim * 2;  // bytes per position and KV head
     const size_t old_head = (size_t)c->kv_cap * per, new_head = (size_t)cap * per, bytes = nkv * new_head;
-    for (size_t i = 0; i < c->kc.size(); i++) {
-        uint16_t* nk = nullptr;
-        uint16_t* nv = nullptr;
-        if (hipMalloc(&nk, bytes) != hipSuccess || hipMalloc(&nv, bytes) != hipSuccess) {
-            if (nk) (void)hipFree(nk);
-            return fail(c, QWATTN_ENOMEM, "out of VRAM growing the K/V caches");
-        }
-        // the blocked layout keeps each KV head's 32-position blocks in order, so a head's old region is a
-        // prefix of its new one
-        HIP_TRY(c, hipMemsetAsync(nk, 0, bytes, s));
-        HIP_TRY(c, hipMemsetAsync(nv, 0, bytes, s));
-        for (int h = 0; h < nkv; h++) {
-            HIP_TRY(c, hipMemcpyAsync(reinterpret_cast<char*>(nk) + h * new_head,
-                                      reinterpret_cast<char*>(c->kc[i]) + h * old_head, old_head,
-                                      hipMemcpyDeviceToDevice, s));
-            HIP_TRY(c, hipMemcpyAsync(reinterpret_cast<char*>(nv) + h * new_head,
-                                      reinterpret_cast<char*>(c->vc[i]) + h * old_head, old_head,
-                                      hipMemcpyDeviceToDevice, s));
-        }
-        HIP_TRY(c, hipStreamSynchronize(s));
-        (void)hipFree(c->kc[i]);
-        (void)hipFree(c->vc[i]);
-        c->kc[i] = nk;
-        c->vc[i] = nv;
+    const size_t slots = c->kc.size();
+    std::vector<uint16_t*> nk(slots, nullptr), nv(slots, nullptr);
+    int nth = 0;
+    hipError_t e = hipSuccess;
+    for (size_t i = 0; i < slots && e == hipSuccess; i++) {
+        e = kv_malloc(c, &nk[i], bytes, nth);
+        if (e == hipSuccess) e = kv_malloc(c, &nv[i], bytes, nth);
     }
+    // the blocked layout keeps each KV head's 32-position blocks in order, so a head's old region is a
+    // prefix of its new one; the rest starts at zero
+    for (size_t i = 0; i < slots && e == hipSuccess; i++) {
+        e = hipMemsetAsync(nk[i], 0, bytes, s);
+        if (e == hipSuccess) e = hipMemsetAsync(nv[i], 0, bytes, s);
+        for (int h = 0; h < nkv && e == hipSuccess; h++) {
+            e = hipMemcpyAsync(reinterpret_cast<char*>(nk[i]) + h * new_head,
+                               reinterpret_cast<char*>(c->kc[i]) + h * old_head, old_head, hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(reinterpret_cast<char*>(nv[i]) + h * new_head,
+                                   reinterpret_cast<char*>(c->vc[i]) + h * old_head, old_head, hipMemcpyDeviceToDevice,
+                                   s);
+        }
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);  // no copy may still read or write the buffers freed here
+        free_all(nk);
+        free_all(nv);
+        return e == hipErrorOutOfMemory ? fail(c, QWATTN_ENOMEM, "out of VRAM growing the K/V caches")
+                                        : fail(c, QWATTN_EHIP, "qwattn_kv_grow: %s", hipGetErrorString(e));
+    }
+    free_all(c->kc);
+    free_all(c->vc);
+    c->kc.swap(nk);
+    c->vc.swap(nv);
     c->kv_cap = (int)cap;
+    return QWATTN_OK;
+}
+
+int qwattn_set_alloc_fault(qwattn_ctx* c, int nth) {
+    if (!c) return QWATTN_EINVAL;
+    if (nth < 0) return fail(c, QWATTN_EINVAL, "qwattn_set_alloc_fault: %d", nth);
+    c->alloc_fault = nth;
     return QWATTN_OK;
 }
 
@@ -947,13 +995,14 @@ int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq
 
 }  // extern "C"
 
-// IEEE 754 binary16 bits to float: sign, 5-bit exponent (bias 15), 10-bit fraction; subnormals scale the
-// fraction by 2^-24, exponent 31 is inf / NaN.
+// binary16 bits to float as the reference's upload widens Q8_0 scales (ck::half_to_f32,
+// src/cpu_kernels.cpp:20-34): sign, 5-bit exponent (bias 15), 10-bit fraction; subnormals scale the
+// fraction by 2^-24. Exponent 31 has no inf / NaN case there: it is a normal exponent, so 0x7C00 widens to
+// 65536 and 0x7FFF to 131008, and the planar scales stay bit-identical to the reference's.
 static float half_bits_to_float(uint16_t h) {
     const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, f = h & 1023u;
     float v;
     if (e == 0) v = std::ldexp((float)f, -24);
-    else if (e == 31) v = f ? NAN : INFINITY;
     else v = std::ldexp((float)(f | 1024u), (int)e - 25);
     uint32_t b;
     std::memcpy(&b, &v, 4);

@@ -45,6 +45,23 @@ def assert_parity(out, ref, what="", atol=ATOL, rtol=RTOL):
     return max_abs, rel
 
 
+def assert_rows_parity(out, ref, what="", atol=ATOL, rtol=RTOL):
+    """assert_parity for every token row of out/ref [n, ...] at once: each token's max-abs error <= atol and
+    its relative L2 error <= rtol; the message names the worst token. Returns (max_abs, worst rel_l2)."""
+    out = np.asarray(out, np.float64).reshape(len(out), -1)
+    ref = np.asarray(ref, np.float64).reshape(len(ref), -1)
+    assert out.shape == ref.shape, f"{what}: shapes {out.shape} vs {ref.shape}"
+    assert np.all(np.isfinite(out)), f"{what}: non-finite output at tokens {np.nonzero(~np.isfinite(out).all(1))[0][:8]}"
+    d = out - ref
+    max_abs = np.abs(d).max(axis=1)
+    rel = np.linalg.norm(d, axis=1) / np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+    bad = np.nonzero((max_abs > atol) | (rel > rtol))[0]
+    t = int(bad[0]) if bad.size else int(np.argmax(max_abs))
+    assert not bad.size, (f"{what}: {bad.size} of {len(out)} tokens off, first token {t}: max_abs {max_abs[t]:.3e} "
+                          f"rel_l2 {rel[t]:.3e}")
+    return float(max_abs.max()), float(rel.max())
+
+
 class Shape:
     def __init__(self, NH, NKV, D, R, theta=1e7, eps=1e-6):
         self.NH, self.NKV, self.D, self.R, self.theta, self.eps = NH, NKV, D, R, theta, eps

@@ -221,8 +221,42 @@ def test_mat_multi_rejects_bad_input(qw):
     y = torch.zeros((1, 32), device=DEV)
     with pytest.raises(qw.QwattnError):
         ctx.mat_multi(x, [(y, w, s)] * 5)  # more than 4 matrices
+    w48 = torch.zeros((32, 48), dtype=torch.int8, device=DEV)
     with pytest.raises(qw.QwattnError):
-        ctx.mat_multi(x[:, :48], [(y, w[:, :48], s)])  # 48 columns: not whole Q8 blocks
+        ctx.mat_multi(x[:, :48], [(y, w48, s[:, :1].contiguous())])  # 48 columns: not whole Q8 blocks
+    with pytest.raises(ValueError):
+        ctx.mat_multi(x, [(y, w, s), (y, torch.zeros((32, 96), dtype=torch.int8, device=DEV), s)])  # column counts
+    with pytest.raises(ValueError):
+        ctx.mat_multi(x[:, :32], [(y, w, s)])  # x narrower than the weights
+    ctx.close()
+
+
+@pytest.mark.parametrize("n", [1, 4, 20])
+def test_mat_multi_padded_x(qw, oracle, n):
+    """A padded input (x wider than the weights' columns, row stride beyond them) gives each matrix of
+    qwattn_mat_multi the bits of qwattn_mat on the same operands: the column count is the weights', not x's."""
+    print(f"mat_multi padded x n={n}", flush=True)
+    ctx = _ctx(qw)
+    rows_list, cols, pad = (96, 40, 64), 128, 64
+    x = np.random.default_rng(97 + n).standard_normal((n, cols + pad)).astype(np.float32)
+    xd = dev(x)
+    outs, sep, mats = [], [], []
+    for i, rows in enumerate(rows_list):
+        blocks, _, _ = q8_blocks(98 + i, rows, cols)
+        w8, s = qw.q8_unpack(blocks, rows, cols)
+        mats.append((w8, s))
+        wd, sd = dev(w8), dev(s)
+        y = torch.empty((n, rows), device=DEV)
+        outs.append((y, wd, sd))
+        ys = torch.empty((n, rows), device=DEV)
+        ctx.mat(xd, ys, wd, sd)
+        sep.append(ys)
+    ctx.mat_multi(xd, outs)
+    torch.cuda.synchronize()
+    for (y, _, _), ys, (w8, s) in zip(outs, sep, mats):
+        assert torch.equal(y, ys)
+        _check(y.cpu().numpy(), oracle.mat(x[:, :cols], w8=w8, s=s),
+               np.abs(w8.astype(np.float32) * np.repeat(s, 32, axis=1)), x[:, :cols])
     ctx.close()
 
 

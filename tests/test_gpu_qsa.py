@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import QSA_BLOCK64, QSA_ODD, QSA_TINY, QSA_WIDE, QWEN3_NEXT, QsaShape, qsa_inputs
+from common import QSA_BLOCK64, QSA_ODD, QSA_TINY, QSA_WIDE, QWEN3_NEXT, QsaShape, assert_rows_parity, qsa_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -37,7 +37,9 @@ def _bits(m, b):
 
 
 def assert_selection(got, want, scores, qs, pos, n, what):
-    """got/want [n, mask_words] uint32; scores [n, nblk] from the oracle (NaN for dense tokens)."""
+    """got/want [n, mask_words] uint32; scores [n, nblk] from the oracle (NaN for dense tokens). Returns the
+    number of near-tie swaps the comparison allowed (blocks selected on one side only)."""
+    swaps = 0
     for t in range(n):
         nblk = (pos + t + 1) // qs.CR
         if nblk <= qs.top:
@@ -53,7 +55,9 @@ def assert_selection(got, want, scores, qs, pos, n, what):
         assert len(g) == qs.top, f"{what}: token {t} selected {len(g)} blocks"
         for b in g ^ w:
             assert abs(s[b] - thr) <= tol, f"{what}: token {t} block {b} score {s[b]} vs threshold {thr}"
+        swaps += len(g ^ w) // 2
         assert not np.any(got[t, (nblk + 31) // 32:]), f"{what}: token {t} bits past its complete blocks"
+    return swaps
 
 
 # (pos, n, select): indexer calls in order (select False: keys cached and pooled only, as for a long prompt
@@ -79,8 +83,20 @@ CASES = {
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_qsa_indexer_matches_oracle(qw, oracle, name):
+    _indexer_case(qw, oracle, name, *CASES[name])
+
+
+def test_qsa_select_widest_indexer_after_narrow(qw, oracle):
+    """The select's dynamic LDS grows with heads x dims; a call at the widest indexer the host accepts
+    (32 heads x 256 dims = 8,192) right after a narrow one in the same process launches and selects the
+    oracle's blocks."""
+    _indexer_case(qw, oracle, "tiny", *CASES["tiny"])
+    _indexer_case(qw, oracle, "heads32_dims256", QsaShape(32, 256, 4, 256, 64), 2056,
+                  [(0, 2000, 0), (2000, 1, 1), (2001, 3, 1)], "f32")
+
+
+def _indexer_case(qw, oracle, name, qs, max_ctx, calls, dt):
     import oracle as orc
-    qs, max_ctx, calls, dt = CASES[name]
     tot = sum(c[1] for c in calls)
     iq, ik, qg, kg = qsa_inputs(41, tot, qs)
     if name == "zeros":
@@ -116,7 +132,9 @@ def test_qsa_indexer_matches_oracle(qw, oracle, name):
             got = host(mask).view(np.uint32)
             want, scores = oracle.qsa_select(iq[row:row + n], qg, pooled_ref, pos, qs.CR, qs.top, qs.R, qs.theta,
                                              qs.eps, mw, with_scores=True)
-            assert_selection(got, want, scores, qs, pos, n, f"{name} pos={pos}")
+            swaps = assert_selection(got, want, scores, qs, pos, n, f"{name} pos={pos}")
+            print(f"qsa {name} pos={pos} n={n}: {swaps} near-tie swap(s) of {n * qs.top} selected blocks",
+                  flush=True)
             # the key bits follow the GPU's own selection by the reference's visibility rule
             assert np.array_equal(host(kbits).view(np.uint32), orc.qsa_key_bits(got, pos, n, qs.CR))
         row += n
@@ -362,10 +380,9 @@ def test_prefill_qsa_parity(qw, oracle, s, pos, n, dt, cr, density, path):
     kcache = host(qw.k_rows(kc, cap, s.NKV, s.D)[:rows])
     vcache = host(qw.v_rows(vc, cap, s.NKV, s.D)[:rows])
     qg_h, out = host(qg_d), host(out)
-    toks = np.arange(n) if n <= 120 else np.unique(np.r_[0, 1, np.linspace(0, n - 1, 40).astype(int), n - 1])
-    for t in toks:
-        ref = oracle.attention_qsa(rq[t:t + 1], kcache, vcache, pos + t, mask[t:t + 1], cr, qg_h[t:t + 1])
-        assert_parity(out[t:t + 1], ref, f"qsa prefill {s} pos={pos} n={n} token {t}")
+    # every token row, one batched oracle call
+    ref = oracle.attention_qsa(rq, kcache, vcache, pos, mask, cr, qg_h)
+    assert_rows_parity(out, ref, f"qsa prefill {s} pos={pos} n={n}")
 
 
 def test_prefill_qsa_all_visible_equals_dense(qw):

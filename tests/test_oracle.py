@@ -454,6 +454,40 @@ def test_mat_q8_matches_reference(oracle, rows, cols, n):
     assert np.all(np.abs(got - want) <= 1e-6 * mag.T + 1e-7), np.abs(got - want).max()
 
 
+def test_mat_q8_exponent31_scales_match_reference(oracle, qw):
+    """Q8_0 blocks whose binary16 scale has exponent 31 (0x7C00, 0x7FFF, 0xFE01, 0x7C01: inf / NaN in IEEE,
+    finite 65536, 131008, -98368, 65600 in the reference's ck::half_to_f32), repacked by qwattn_q8_unpack and
+    multiplied by the oracle, give what the reference's GPU path computes from its upload (unpack_q8_row,
+    src/qwen4_vk.cpp:98-106, which widens with half_to_f32): an fp64 product over the reference's own compiled
+    half_to_f32 of each pattern. Rows without such a scale also equal the reference's CPU projection
+    (gq::run_jobs). That CPU path widens scales with F16C on AVX-512 hosts (src/quant.cpp:17-25), i.e. IEEE
+    inf / NaN, so the reference's CPU and GPU paths disagree on exactly these rows; this build follows the GPU
+    upload it replaces."""
+    ref = _ref_qsa()
+    prim = _ref()
+    rows, cols, n = 24, 256, 2
+    blocks, w8, _ = q8_blocks(57, rows, cols)
+    b = blocks.reshape(rows, cols // 32, 34).copy()
+    hot = np.array([0x7C00, 0x7FFF, 0xFE01, 0x7C01], np.uint16)
+    hot_rows = np.arange(rows) % 3 == 0
+    for r in np.nonzero(hot_rows)[0]:
+        b[r, r % (cols // 32), 0:2] = hot[r % 4:r % 4 + 1].view(np.uint8)
+    bits = b[:, :, 0:2].copy().view(np.uint16)[:, :, 0]
+    b = b.reshape(rows, -1)
+    w, s = qw.q8_unpack(b, rows, cols)
+    want_s = np.array([[prim.lib.ref_half_to_f32(int(h)) for h in row] for row in bits], np.float32)
+    assert np.array_equal(w, w8) and np.array_equal(s.view(np.uint32), want_s.view(np.uint32))
+    assert s.max() == 131008.0 and s.min() == -98368.0
+    x = np.random.default_rng(58).standard_normal((n, cols)).astype(np.float32)
+    got = oracle.mat(x, w8=w, s=s)
+    wf = w8.astype(np.float64) * np.repeat(want_s.astype(np.float64), 32, axis=1)
+    exact = x.astype(np.float64) @ wf.T
+    mag = np.abs(wf) @ np.abs(x.astype(np.float64)).T
+    assert np.all(np.abs(got - exact) <= 1e-6 * mag.T + 1e-7), np.abs(got - exact).max()
+    cpu = ref.mat_q8(b, rows, cols, x)
+    assert np.all(np.abs(got - cpu)[:, ~hot_rows] <= 1e-6 * mag.T[:, ~hot_rows] + 1e-7)
+
+
 def test_mat_closed_forms(oracle):
     """f32 identity and permutation matrices return x (permuted); zero weights return 0; a Q8 row of k with
     scale 1/k sums x; post 1 is silu(y * scale) of the plain result; the product is linear in x."""
