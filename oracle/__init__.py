@@ -241,6 +241,101 @@ class Oracle:
         return out
 
 
+TINY_GGUF = os.path.join(HERE, "_ref", "tiny_qwen4exp.gguf")
+RQ4_KINDS = ("qg", "k", "v", "ik", "iq", "att")
+_RQ4_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, _I, _I, _I, _I, _F, ctypes.c_long)
+
+
+class RefQwen4:
+    """The reference's own qwen4exp CPU engine (Qwen4Cpu behind make_qwen4_cpu_backend, src/qwen4_cpu.cpp)
+    compiled in place (oracle/_ref/libref_qwen4.so; see ref_qwen4_driver.cpp), on a GGUF model file.
+
+    `hook(layer, kind, pos, n, arr)` (optional) sees, for every full-attention layer call, the engine's own
+    arrays: kinds "qg" [n, NH, 2D], "k" / "v" [n, NKV, D], "ik" [n, ID], "iq" [n, IH, ID] (the indexer's raw
+    projections; "iq" only on calls that select) and "att" [n, NH, D], the attention body's output just before
+    o_proj reads it. `arr` is a numpy view of the engine's buffer: writing into the "att" array replaces the
+    attention output the engine projects."""
+
+    def __init__(self, gguf=TINY_GGUF, max_ctx=4096, threads=4,
+                 path=os.path.join(HERE, "_ref", f"libref_qwen4{_SUFFIX}.so")):
+        for f in (path, gguf):
+            if not os.path.exists(f):
+                raise FileNotFoundError(f)
+        lib = ctypes.CDLL(path)
+        P = ctypes.c_void_p
+        lib.rq4_open.argtypes = [ctypes.c_char_p, _I, _I]
+        lib.rq4_open.restype = P
+        lib.rq4_error.argtypes = [P]
+        lib.rq4_error.restype = ctypes.c_char_p
+        lib.rq4_close.argtypes = [P]
+        lib.rq4_info.argtypes = [P, ctypes.POINTER(_I), _F]
+        lib.rq4_layer.argtypes = [P, _I, ctypes.POINTER(_I)]
+        lib.rq4_norms.argtypes = [P, _I, _F, _F, _F, _F]
+        lib.rq4_set_callback.argtypes = [P, _RQ4_CB, P]
+        lib.rq4_forward.argtypes = [P, ctypes.POINTER(_I), _I, _F]
+        for f in ("rq4_pos", "rq4_reset", "rq4_save_state", "rq4_restore_state"):
+            getattr(lib, f).argtypes = [P]
+        self.lib = lib
+        self.h = lib.rq4_open(gguf.encode(), max_ctx, threads)
+        if not self.h:
+            raise RuntimeError(lib.rq4_error(None).decode())
+        iv, fv = (_I * 10)(), (ctypes.c_float * 2)()
+        lib.rq4_info(self.h, iv, fv)
+        (self.hidden, self.n_layers, self.vocab, self.NH, self.NKV, self.D, self.R, self.IH, self.ID,
+         self.budget) = list(iv)
+        self.eps, self.theta = float(fv[0]), float(fv[1])
+        self.layers = []
+        for l in range(self.n_layers):
+            lv = (_I * 2)()
+            lib.rq4_layer(self.h, l, lv)
+            self.layers.append((bool(lv[0]), int(lv[1])))
+        self.hook = None
+        self._cb = _RQ4_CB(self._on_array)  # kept alive with the engine
+        lib.rq4_set_callback(self.h, self._cb, None)
+
+    def _on_array(self, user, layer, kind, pos, n, data, count):
+        if self.hook is None:
+            return
+        shapes = {0: (n, self.NH, 2 * self.D), 1: (n, self.NKV, self.D), 2: (n, self.NKV, self.D), 3: (n, self.ID),
+                  4: (n, self.IH, self.ID), 5: (n, self.NH, self.D)}
+        arr = np.ctypeslib.as_array(data, shape=(count,)).reshape(shapes[kind])
+        self.hook(layer, RQ4_KINDS[kind], pos, n, arr)
+
+    def full_layers(self):
+        return [l for l, (full, _) in enumerate(self.layers) if full]
+
+    def norms(self, layer):
+        """(q_norm, k_norm, idx_q_norm, idx_k_norm) of a full-attention layer, as the engine holds them (the
+        GGUF gammas, already 1 + w); the indexer's are zeros on a dense layer."""
+        qn, kn = np.zeros(self.D, np.float32), np.zeros(self.D, np.float32)
+        iqn, ikn = np.zeros(self.ID, np.float32), np.zeros(self.ID, np.float32)
+        assert self.lib.rq4_norms(self.h, layer, _fp(qn), _fp(kn), _fp(iqn), _fp(ikn)) == 0
+        return qn, kn, iqn, ikn
+
+    def forward(self, tokens):
+        """Backend::forward: the tokens at the current position; returns the last token's logits [vocab]."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.zeros(self.vocab, np.float32)
+        rc = self.lib.rq4_forward(self.h, t.ctypes.data_as(ctypes.POINTER(_I)), len(t), _fp(logits))
+        if rc:
+            raise RuntimeError(self.lib.rq4_error(self.h).decode())
+        return logits
+
+    def pos(self):
+        return self.lib.rq4_pos(self.h)
+
+    def save_state(self):
+        self.lib.rq4_save_state(self.h)
+
+    def restore_state(self):
+        self.lib.rq4_restore_state(self.h)
+
+    def close(self):
+        if self.h:
+            self.lib.rq4_close(self.h)
+            self.h = None
+
+
 def qsa_key_bits(mask, pos, n, cr):
     """The per-key visibility the block-sparse kernels consume: bits [n, ceil((pos + n) / 32)] uint32, bit j
     of token t set when key j is in a complete block whose mask bit is set or in the tail block (keys from
