@@ -18,13 +18,14 @@ from common import QWEN3_NEXT, assert_parity, projections
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CXX = os.path.join(ROOT, "tests", "cxx")
 REF_SRC = "/root/reference/src"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 sys.path.insert(0, CXX)
 import build as cxx_build  # noqa: E402
 
 
 def _syntax(extra, std):
-    cmd = ["g++", f"-std={std}", "-fsyntax-only", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
-           *extra, os.path.join(CXX, "hip_backend.cpp")]
+    cmd = ["g++", f"-std={std}", "-fsyntax-only", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROCM, "include"), *extra, os.path.join(CXX, "hip_backend.cpp")]
     r = subprocess.run(cmd, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
 
@@ -37,7 +38,8 @@ def test_wrapper_compiles(std):
 @pytest.mark.skipif(not os.path.exists(os.path.join(REF_SRC, "backend.h")), reason="reference sources not present")
 def test_binding_compiles_against_reference_headers():
     """HipBackend : Backend overrides every pure virtual and uses Q4Config's own field names."""
-    r = subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-DQW_WITH_REFERENCE", "-I", os.path.join(ROOT, "include"),
+    r = subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-Wall", "-Wextra", "-Werror", "-DQW_WITH_REFERENCE",
+                        "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROCM, "include"),
                         "-I", REF_SRC, os.path.join(CXX, "hip_backend.cpp")], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
 
