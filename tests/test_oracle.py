@@ -507,3 +507,35 @@ def test_mat_closed_forms(oracle):
     assert np.allclose(oracle.mat(x, wf=wf, post=1, post_scale=0.7), u / (1 + np.exp(-u)), rtol=1e-6, atol=1e-7)
     x2 = r.standard_normal((n, cols)).astype(np.float32)
     assert np.allclose(oracle.mat(2 * x - x2, wf=wf), 2 * y - oracle.mat(x2, wf=wf), rtol=1e-5, atol=1e-5)
+
+
+def test_fp16_cache_cost_against_fp32_cache(oracle):
+    """The FP8 model's Vulkan path keeps fp32 K/V caches (src/vk_backend.cpp:297-299, 584-610; the CPU paths
+    too, src/qwen4_cpu.cpp:318-319); this build serves every model with fp16 caches. The cost, on the oracle
+    at the Qwen3-Next shape over 4,097 keys: with N(0,1) cache rows the outputs from fp16-rounded rows differ
+    from fp32 rows by a relative 3e-4 (max-abs ~2e-5); with 1% of the keys x8 (the long-context config's
+    stress) by a relative 4e-4, max-abs ~3e-3 on outputs of magnitude up to ~3.4, i.e. ~1e-3 of the output
+    scale. The check also sees that the difference is more than fp32 rounding."""
+    from common import QWEN3_NEXT as s
+    for heavy, rel_max, scaled_max in ((0, 1e-3, 1e-3), (8, 1e-3, 2e-3)):
+        r = np.random.default_rng(77)
+        pos, n = 4096, 4
+        qg = r.standard_normal((n, s.NH, 2 * s.D)).astype(np.float32)
+        k = r.standard_normal((pos + n, s.NKV, s.D)).astype(np.float32)
+        v = r.standard_normal((pos + n, s.NKV, s.D)).astype(np.float32)
+        if heavy:
+            k[r.choice(pos, pos // 100, replace=False)] *= heavy
+        qn = (1 + 0.1 * r.standard_normal(s.D)).astype(np.float32)
+        kn = (1 + 0.1 * r.standard_normal(s.D)).astype(np.float32)
+        rq, rk, rv = oracle.qk_norm_rope(qg, k[pos:], v[pos:], qn, kn, pos, s.R, s.theta, s.eps)
+        kc, vc = k.copy(), v.copy()
+        kc[pos:], vc[pos:] = rk[pos:], rv[pos:]
+        full = oracle.attention(rq, kc, vc, pos, qg)
+        half = oracle.attention(rq, kc.astype(np.float16).astype(np.float32), vc.astype(np.float16).astype(np.float32),
+                                pos, qg)
+        d = np.abs(full - half)
+        rel = float(np.linalg.norm(full - half) / np.linalg.norm(full))
+        print(f"fp16 vs fp32 cache (keys x{heavy or 1}): max-abs {d.max():.2e}, rel-l2 {rel:.2e}, "
+              f"max |out| {np.abs(full).max():.2f}")
+        assert rel < rel_max and d.max() < scaled_max * np.abs(full).max()
+        assert d.max() > 1e-6
