@@ -139,8 +139,9 @@ struct QsaSelectArgs {
     const float* gamma;   // [ID] the indexer query norm's gamma (applied as is)
     const float* rope;
     const float* pooled;  // [>= (pos+n)/CR][ID]
-    float* scores;        // workspace [n][stride], stride >= (pos+n)/CR
+    float* scores;        // workspace [n][stride], stride >= (pos+n)/CR and a multiple of 4
     int* cnt;             // [n] arrival counters, zero between launches
+    unsigned* hist;       // [n][hcopies][2048] first-digit counts of the scores, zero between launches
     unsigned* mask;       // [n][mask_words] block bitmask, or NULL
     unsigned* kbits;      // [n][kb_words] key visibility bits, or NULL
     const void* ik;       // with raw: the tokens' raw indexer keys [n][ID] (in_dtype), appended by the launch
@@ -148,8 +149,11 @@ struct QsaSelectArgs {
     int mask_words, kb_words, stride;
     int pos, n, IH, ID, CR, top, R;
     float eps;
+    int hcopies;          // histogram copies a token (n * hcopies <= kQsaHistTokens)
 };
 hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s);
+// First-digit histograms (2,048 bins) a select launch may use: a token takes 1 to 8 copies
+constexpr int kQsaHistTokens = 1024;
 size_t qsa_select_lds(int IH, int ID);
 int qsa_mask_lds_words();  // complete blocks a select launch can hold: 32 x this
 

@@ -60,6 +60,10 @@ __device__ __forceinline__ unsigned wave_isum(unsigned x) {
     return s32[0] + s32[1];
 }
 
+// v_writelane_b32: `src` (uniform) into lane `lane` of `old` (the LLVM intrinsic, which this compiler offers
+// no builtin for)
+__device__ unsigned writelane(unsigned src, unsigned lane, unsigned old) __asm("llvm.amdgcn.writelane.i32");
+
 __device__ __forceinline__ unsigned wave_min(unsigned x) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) x = min(x, (unsigned)__shfl_xor((int)x, o, 64));
@@ -90,28 +94,42 @@ __device__ __forceinline__ void rope_row(const float* x, float* y, const float* 
 }
 
 // Key bits [32 w, 32 w + 32) of a token with nblk complete blocks of `cr` keys and block mask m: key j is
-// visible when block j / cr has its bit set or lies at or past nblk (the tail). One division per word, the
-// block of each following key by counting.
+// visible when block j / cr has its bit set or lies at or past nblk (the tail). A power of two below 32: the
+// word holds 32 / cr whole blocks of one mask word, whose bits are spread over cr bits each by shift-and-mask
+// steps and a multiply; 32 and more: one block; otherwise one division per word, the block of each following
+// key by counting.
 __device__ __forceinline__ unsigned key_word(const unsigned* m, int w, int cr, int nblk) {
     const int nmwc = (nblk + 31) >> 5;
     if ((cr & (cr - 1)) == 0) {
-        // a power of two: the word lies in one block (cr >= 32) or holds 32 / cr whole blocks of one mask word
         const int lc = __builtin_ctz((unsigned)cr);
         if (cr >= 32) {
             const int blk = (32 * w) >> lc;
             const unsigned mw = (blk >> 5) < nmwc ? m[blk >> 5] : 0u;
             return blk >= nblk || ((mw >> (blk & 31)) & 1u) ? 0xFFFFFFFFu : 0u;
         }
-        const int nb = 32 >> lc, blk0 = w * nb;
-        const unsigned mw = (blk0 >> 5) < nmwc ? m[blk0 >> 5] : 0u, ones = (1u << cr) - 1u;
-        unsigned bits = 0u;
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            if (i < nb) {
-                const int blk = blk0 + i;
-                bits |= blk >= nblk || ((mw >> (blk & 31)) & 1u) ? ones << (i * cr) : 0u;
-            }
-        return bits;
+        const int nb = 32 >> lc, blk0 = w * nb, tail = nblk * cr - 32 * w;  // keys of the word before the tail
+        unsigned x = (blk0 >> 5) < nmwc ? m[blk0 >> 5] : 0u;
+        if (nb < 32) x = (x >> (blk0 & 31)) & ((1u << nb) - 1u);
+        switch (lc) {  // bit i to bits [cr i, cr i + cr)
+            case 1:
+                x = (x | (x << 8)) & 0x00FF00FFu;
+                x = (x | (x << 4)) & 0x0F0F0F0Fu;
+                x = (x | (x << 2)) & 0x33333333u;
+                x = ((x | (x << 1)) & 0x55555555u) * 3u;
+                break;
+            case 2:
+                x = (x | (x << 12)) & 0x000F000Fu;
+                x = (x | (x << 6)) & 0x03030303u;
+                x = ((x | (x << 3)) & 0x11111111u) * 15u;
+                break;
+            case 3:
+                x = (x | (x << 14)) & 0x00030003u;
+                x = ((x | (x << 7)) & 0x01010101u) * 255u;
+                break;
+            case 4: x = ((x & 1u) | ((x & 2u) << 15)) * 65535u; break;
+            default: break;  // cr 1: the mask word itself
+        }
+        return tail <= 0 ? 0xFFFFFFFFu : (tail >= 32 ? x : x | (0xFFFFFFFFu << tail));
     }
     int blk = (32 * w) / cr, r = 32 * w - blk * cr;
     // the 32 keys lie in at most 32 consecutive blocks: two mask words, read once (only words that hold
@@ -206,158 +224,31 @@ __device__ __forceinline__ int block_excl_scan(int x, int* s_tot) {
     return base + inc - x;
 }
 
-// The exact top-`top` of token t's nblk block scores (by score, then the lower block id: the scores are >= +0,
-// so their bit patterns order like the values), by the last workgroup to arrive; writes the token's mask
-// row and key bits. Thread tid owns the blocks [per tid, per tid + per). KR > 0: per = KR and the thread
-// holds their keys in registers (nblk <= KR * 1,024; one load per four keys); KR == 0: per is a multiple of
-// 32 and the keys are read from memory at each use (device-coherent loads).
-//
-// The threshold key is found most significant digit first, 11 bits a pass (at most three passes, fewer when
-// the smallest and largest keys share their top bits or the digit's bin holds exactly the keys still
-// needed): the keys that match the digits found so far are counted per next digit in an LDS histogram
-// (2,048 bins, LDS atomic adds), and a scan over the bins from the top, two bins a thread, finds the digit
-// where the count of larger keys reaches the number still needed.
+// Sum over the workgroup's threads, in every thread (one barrier; `s_tot` holds 16 words).
+__device__ __forceinline__ int block_sum(int x, int* s_tot) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    x = (int)wave_isum((unsigned)x);
+    if (lane == 0) s_tot[wave] = x;
+    __syncthreads();
+    return (int)wave_isum(lane < kQsaThreads / 64 ? (unsigned)s_tot[lane] : 0u);
+}
+
+// ---- the selection proper: exact top-`top` of a token's nblk block scores, by (score desc, block id asc) ---
+// The scores are >= +0, so their bit patterns order like the values. The threshold's first radix digit,
+// bits [30:20], comes from the token's histogram `gh` (2,048 bins), which the scoring workgroups filled
+// with global atomic adds; the keys of that digit's bin (the candidates, a few hundred among 65,536 blocks
+// of random scores) are compacted into LDS and resolved there, so that a pass over every key (each VALU op
+// of which costs the one CU 1,024 cycles at 65,536 blocks) happens only to load them, to compact the
+// candidates and to build the mask. A bin of more than kQsaCand keys (bulk exact ties) takes the fallback:
+// radix passes over every key.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kQsaCand = 2048;  // candidates compacted into LDS
+constexpr int kQsaHistCopies = 8;  // at most, a token's first-digit histogram copies
 
-template <int KR, bool COH>
-__device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
-                                              unsigned* s_mask, int* s_misc, int* s_scan, unsigned* s_hist) {
-    constexpr int AUX = COH ? kScDevice : 0;  // device-coherent loads in the scoring launch itself
-    constexpr int NB = 2048;  // bins of a pass
-    static_assert(NB == 2 * kQsaThreads, "two bins a thread");
-    static_assert(KR == 0 || KR == 8 || KR == 16 || KR == 32 || KR == 64, "keys a thread");
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int per = KR > 0 ? KR : ((nblk + kQsaThreads - 1) / kQsaThreads + 31) & ~31;
-    const int lo = min(nblk, tid * per), hi = min(nblk, lo + per);
-    auto load = [&](int b) -> unsigned { return __builtin_amdgcn_raw_buffer_load_b32(rs, b * 4, 0, AUX); };
-    unsigned kr[KR > 0 ? KR : 1];
-    unsigned kmin = 0xFFFFFFFFu, kmax = 0u;
-    if constexpr (KR > 0) {
-        // every load issued before any is used. A block past nblk holds the key ~0u: scores are >= +0, so no
-        // real key has bit 31 and that key never matches a prefix, equals the threshold or counts in the
-        // maximum (no per-key range test, whose lane masks would stay live through every pass)
-#pragma unroll
-        for (int i = 0; i < KR; i += 4) {
-            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (tid * KR + i) * 4, 0, AUX));
-            kr[i] = v[0], kr[i + 1] = v[1], kr[i + 2] = v[2], kr[i + 3] = v[3];
-        }
-        const int nv = hi - lo;  // this thread's blocks below nblk
-#pragma unroll
-        for (int i = 0; i < KR; i++) {
-            kr[i] = i < nv ? kr[i] : 0xFFFFFFFFu;
-            kmin = min(kmin, kr[i]), kmax = max(kmax, kr[i] >> 31 ? 0u : kr[i]);
-        }
-    } else {
-        for (int b = lo; b < hi; b++) {
-            const unsigned k = load(b);
-            kmin = min(kmin, k), kmax = max(kmax, k);
-        }
-    }
-    s_hist[2 * tid] = 0u, s_hist[2 * tid + 1] = 0u;  // the first pass's bins
-    kmin = wave_min(kmin), kmax = wave_max(kmax);
-    if (lane == 0) s_scan[wave] = (int)kmin, s_scan[16 + wave] = (int)kmax;
-    __syncthreads();
-    {
-        const unsigned m0 = lane < 16 ? (unsigned)s_scan[lane] : 0xFFFFFFFFu;
-        const unsigned m1 = lane < 16 ? (unsigned)s_scan[16 + lane] : 0u;
-        kmin = wave_min(m0), kmax = wave_max(m1);  // every wave, the same reduction
-    }
-    const int nmw = (nblk + 31) >> 5;  // mask words holding complete blocks
-
-    // the bits above the highest one where the smallest and largest keys differ are every key's
-    const int hb = kmin == kmax ? -1 : 31 - __builtin_clz(kmin ^ kmax);
-    unsigned prefix = hb < 0 ? kmin : (hb == 31 ? 0u : kmin & ~((2u << hb) - 1u));
-    unsigned fmask = 0xFFFFFFFFu;  // the bits of a key the final comparison looks at
-    int need = a.top;  // keys still to take among those matching the prefix
-    for (int hb_ = hb, pass = 0; hb_ >= 0; pass++) {
-        const int shift = max(hb_ - 10, 0), width = hb_ - shift + 1;
-        const unsigned pmask = hb_ == 31 ? 0u : ~((2u << hb_) - 1u);  // the digits found so far
-        const unsigned dmask = (1u << width) - 1u;
-        unsigned* h = s_hist + (pass & 1) * NB;
-        auto count = [&](unsigned k) {
-            if ((k & pmask) == prefix)
-                __hip_atomic_fetch_add(&h[(k >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        };
-        if constexpr (KR > 0) {
-#pragma unroll
-            for (int i = 0; i < KR; i++) count(kr[i]);
-        } else {
-            for (int b = lo; b < hi; b++) count(load(b));
-        }
-        __syncthreads();
-        // the next pass's bins (last read two passes ago, before this pass's first barrier)
-        s_hist[((pass + 1) & 1) * NB + 2 * tid] = 0u, s_hist[((pass + 1) & 1) * NB + 2 * tid + 1] = 0u;
-        // thread tid: digits d1 = 2^width - 1 - 2 tid and d1 - 1 (from the top); the keys with a larger digit
-        // are the exclusive scan of the pair counts
-        const int d1 = (int)dmask - 2 * tid, d0 = d1 - 1;
-        const int c1 = d1 >= 0 ? (int)h[d1] : 0, c0 = d0 >= 0 ? (int)h[d0] : 0;
-        const int larger = block_excl_scan(c1 + c0, s_scan + 32);
-        if (larger < need && larger + c1 + c0 >= need) {  // exactly one thread
-            const bool in1 = larger + c1 >= need;
-            s_misc[0] = in1 ? d1 : d0;
-            s_misc[1] = in1 ? larger : larger + c1;
-            s_misc[2] = in1 ? c1 : c0;
-        }
-        __syncthreads();
-        prefix |= (unsigned)s_misc[0] << shift;
-        need -= s_misc[1];
-        hb_ = shift - 1;
-        if (s_misc[2] == need && hb_ >= 0) {
-            // every key matching the digits so far is taken: the lower bits need not be resolved
-            fmask = ~((2u << hb_) - 1u);
-            break;
-        }
-    }
-    // prefix (under fmask): the top-th largest key; all keys above it are taken, and the first `need` equal
-    // to it (in block order): the equal keys of the earlier threads' blocks are an exclusive scan
-    int eq = 0;
-    if constexpr (KR > 0) {
-#pragma unroll
-        for (int i = 0; i < KR; i++) eq += (kr[i] & fmask) == prefix;
-    } else {
-        for (int b = lo; b < hi; b++) eq += (load(b) & fmask) == prefix;
-    }
-    int taken = block_excl_scan(eq, s_scan + 32);
-    auto selected = [&](unsigned k) {
-        k &= fmask;
-        bool sel = k > prefix;
-        if (k == prefix) sel = taken++ < need;
-        return sel;
-    };
-    if constexpr (KR == 8 || KR == 16) {
-        unsigned bits = 0u;
-#pragma unroll
-        for (int i = 0; i < KR; i++) bits |= (unsigned)selected(kr[i]) << i;
-        bits &= hi - lo >= KR ? (1u << KR) - 1u : (1u << (hi - lo)) - 1u;  // no bits past nblk
-        // the word of blocks [32 (tid / q), + 32), q = 32 / KR threads: their parts OR-ed across the group
-        constexpr int Q = 32 / KR;
-        unsigned wv = bits << (KR * (tid & (Q - 1)));
-        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-        if constexpr (Q == 4) wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
-        if ((tid & (Q - 1)) == 0 && tid / Q < nmw) s_mask[tid / Q] = wv;
-    } else if constexpr (KR > 0) {
-#pragma unroll
-        for (int w = 0; w < KR / 32; w++) {
-            unsigned bits = 0u;
-#pragma unroll
-            for (int i = 0; i < 32; i++) bits |= (unsigned)selected(kr[32 * w + i]) << i;
-            const int nvw = hi - lo - 32 * w;  // this word's blocks below nblk
-            bits &= nvw >= 32 ? 0xFFFFFFFFu : (nvw > 0 ? (1u << nvw) - 1u : 0u);
-            if (tid * (KR / 32) + w < nmw) s_mask[tid * (KR / 32) + w] = bits;
-        }
-    } else {
-        // lo is a multiple of 32 whenever lo < hi, so the words [lo/32, ceil(hi/32)) are this thread's alone
-        for (int w = lo >> 5; lo < hi && w < (hi + 31) >> 5; w++) {
-            unsigned bits = 0u;
-            for (int i = 0; i < 32; i++) {
-                const int b = 32 * w + i;
-                if (b < hi && selected(load(b))) bits |= 1u << i;
-            }
-            s_mask[w] = bits;
-        }
-    }
-    __syncthreads();
-    const int kb_words = a.kb_words;
+// The token's mask row and key bits from the selection in LDS.
+__device__ __forceinline__ void write_rows(const QsaSelectArgs& a, int t, int nblk, const unsigned* s_mask) {
+    const int tid = threadIdx.x, nmw = (nblk + 31) >> 5, kb_words = a.kb_words;
     if (a.mask)
         for (int w = tid; w < a.mask_words; w += kQsaThreads) a.mask[(size_t)t * a.mask_words + w] = w < nmw ? s_mask[w] : 0u;
     if (a.kbits)
@@ -365,10 +256,420 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
             a.kbits[(size_t)t * kb_words + w] = key_word(s_mask, w, a.CR, nblk);
 }
 
+// Of the candidates ck[] (blocks cb[]; 16 segments of kQsaCand / 16 places, segment w holding n[w]), which
+// share the bits above bit 20 (`prefix`), the `need` largest by (key, then the lower block) are taken: T is the
+// smallest taken key, and of the keys equal to T those of blocks <= id_end (every one when id_end is ~0u).
+// Two 10-bit digit passes over the keys from the top, then, when T has more ties than places, two 9-bit
+// passes over the tied keys' blocks from the smallest (block ids < 2^18). LDS histograms of 1,024 bins (four,
+// zero on entry), thread tid scanning one.
+__device__ __forceinline__ void resolve_candidates(const unsigned* ck, const unsigned* cb, const int* n, int need,
+                                                   unsigned prefix, unsigned* s_hist, int* s_misc, int* s_scan,
+                                                   unsigned& T, unsigned& id_end) {
+    constexpr int W = kQsaCand / (kQsaThreads / 64);
+    static_assert(kQsaCand == 2 * kQsaThreads, "two places a thread");
+    const int tid = threadIdx.x;
+    // this thread's two places, tid and tid + 1,024, when filled
+    const bool v0 = (tid % W) < n[tid / W], v1 = ((tid + kQsaThreads) % W) < n[(tid + kQsaThreads) / W];
+    for (int pass = 0; pass < 2; pass++) {
+        const int shift = pass == 0 ? 10 : 0;
+        const unsigned pmask = pass == 0 ? 0xFFF00000u : 0xFFFFFC00u;  // the bits found so far
+        unsigned* h = s_hist + pass * 1024;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const unsigned k = ck[tid + r * kQsaThreads];
+            if ((r ? v1 : v0) && (k & pmask) == prefix)
+                __hip_atomic_fetch_add(&h[(k >> shift) & 1023u], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __syncthreads();
+        const int c = (int)h[1023 - tid];
+        const int larger = block_excl_scan(c, s_scan + 32);
+        if (larger < need && larger + c >= need) s_misc[3] = 1023 - tid, s_misc[4] = larger, s_misc[5] = c;
+        __syncthreads();
+        prefix |= (unsigned)s_misc[3] << shift;
+        need -= s_misc[4];
+    }
+    T = prefix;
+    id_end = 0xFFFFFFFFu;
+    if (s_misc[5] > need) {  // more keys equal T than places
+        unsigned idp = 0u;
+        for (int pass = 0; pass < 2; pass++) {
+            const int shift = pass == 0 ? 9 : 0;
+            const unsigned pm = pass == 0 ? 0u : ~511u;
+            unsigned* h = s_hist + 2048 + pass * 1024;
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int i = tid + r * kQsaThreads;
+                if ((r ? v1 : v0) && ck[i] == T && (cb[i] & pm) == idp)
+                    __hip_atomic_fetch_add(&h[(cb[i] >> shift) & 511u], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            __syncthreads();
+            const int c = tid < 512 ? (int)h[tid] : 0;
+            const int smaller = block_excl_scan(c, s_scan + 32);
+            if (smaller < need && smaller + c >= need) s_misc[6] = tid, s_misc[7] = smaller;
+            __syncthreads();
+            idp |= (unsigned)s_misc[6] << shift;
+            need -= s_misc[7];
+        }
+        id_end = idp;
+    }
+}
 
-// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [64 c, 64 c + 64) of token t; the last of
-// the token's workgroups to arrive selects. A token that selects nothing has its rows written by workgroup
-// (0, t).
+// The fallback: the threshold's remaining digits by passes over every key, 11 bits a pass (bits [19:9], then
+// [8:0]; none when the whole bin is taken, fewer when a digit's bin holds exactly the keys still needed),
+// the matching keys counted per digit in an LDS histogram (2,048 bins, zero on entry) and the bins scanned
+// from the top, two a thread. The blocks are dealt in chunks of 4,096: thread tid takes blocks 4 tid ..
+// 4 tid + 3 of each, one 16-byte load a chunk; KR > 0: their keys stay in registers, KR == 0: they are read
+// from memory at each use. Ties at the threshold are taken in block order (the need-th smallest tied block
+// by two passes over the block ids). Writes the mask into s_mask.
+template <int KR, bool COH>
+__device__ __forceinline__ void select_fallback(__amdgpu_buffer_rsrc_t rs, int nblk, unsigned prefix, int need,
+                                                int cnt, unsigned* s_mask, int* s_misc, int* s_scan,
+                                                unsigned* s_hist) {
+    constexpr int AUX = COH ? kScDevice : 0;  // device-coherent loads in the scoring launch itself
+    constexpr int NB = 2048;                  // bins of a pass
+    constexpr int CHK = 4 * kQsaThreads;      // blocks of a chunk
+    constexpr int NCK = KR / 4;               // chunks held in registers
+    static_assert(NB == 2 * kQsaThreads, "two bins a thread");
+    const int tid = threadIdx.x;
+    const int nch = KR > 0 ? NCK : (nblk + CHK - 1) / CHK;
+    // The row holds ~key, and 0 past nblk (written by the scoring, or outside the buffer's range): the key
+    // ~word is then ~0u there, whose bit 31 no real key has, so it never matches a digit prefix or equals the
+    // threshold (the host pads each score row to a multiple of four blocks: no load crosses the buffer's end).
+    auto ld4 = [&](int j) -> u32x4 {
+        return ~__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (j * CHK + 4 * tid) * 4, 0, AUX));
+    };
+    u32x4 kr[NCK > 0 ? NCK : 1];
+    if constexpr (KR > 0) {
+#pragma unroll
+        for (int j = 0; j < NCK; j++) kr[j] = ld4(j);
+    }
+    // f(key, block) over this thread's keys
+    auto each = [&](auto&& f) {
+        if constexpr (KR > 0) {
+#pragma unroll
+            for (int j = 0; j < NCK; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) f(kr[j][r], j * CHK + 4 * tid + r);
+        } else {
+            for (int j = 0; j < nch; j++) {
+                const u32x4 v = ld4(j);
+#pragma unroll
+                for (int r = 0; r < 4; r++) f(v[r], j * CHK + 4 * tid + r);
+            }
+        }
+    };
+    unsigned fmask = 0xFFF00000u;  // the bits of a key the final comparison looks at
+    if (cnt != need) {  // else the whole bin is taken
+        fmask = 0xFFFFFFFFu;
+        for (int hb_ = 19, pass = 0; hb_ >= 0; pass++) {
+            const int shift = max(hb_ - 10, 0), width = hb_ - shift + 1;
+            const unsigned pmask = ~((2u << hb_) - 1u);  // the digits found so far
+            const unsigned dmask = (1u << width) - 1u;
+            unsigned* h = s_hist + (pass & 1) * NB;
+            each([&](unsigned k, int) {
+                if ((k & pmask) == prefix)
+                    __hip_atomic_fetch_add(&h[(k >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            });
+            __syncthreads();
+            // the next pass's bins (last read two passes ago, before this pass's first barrier)
+            s_hist[((pass + 1) & 1) * NB + 2 * tid] = 0u, s_hist[((pass + 1) & 1) * NB + 2 * tid + 1] = 0u;
+            // thread tid: digits d1 = 2^width - 1 - 2 tid and d1 - 1 (from the top); the keys with a larger
+            // digit are the exclusive scan of the pair counts
+            const int d1 = (int)dmask - 2 * tid, d0 = d1 - 1;
+            const int c1 = d1 >= 0 ? (int)h[d1] : 0, c0 = d0 >= 0 ? (int)h[d0] : 0;
+            const int larger = block_excl_scan(c1 + c0, s_scan + 32);
+            if (larger < need && larger + c1 + c0 >= need) {  // exactly one thread
+                const bool in1 = larger + c1 >= need;
+                s_misc[0] = in1 ? d1 : d0;
+                s_misc[1] = in1 ? larger : larger + c1;
+                s_misc[2] = in1 ? c1 : c0;
+            }
+            __syncthreads();
+            prefix |= (unsigned)s_misc[0] << shift;
+            need -= s_misc[1];
+            hb_ = shift - 1;
+            if (s_misc[2] == need && hb_ >= 0) {
+                // every key matching the digits so far is taken: the lower bits need not be resolved
+                fmask = ~((2u << hb_) - 1u);
+                break;
+            }
+        }
+    }
+    // prefix (under fmask): the top-th largest key; every key above it is taken, and the first `need` keys
+    // equal to it in block order. The held keys keep only the compared bits (bit 31, set on the blocks past
+    // nblk, among them), and the comparisons below are not carried from the count to the marking: both would
+    // hold a second copy of every key.
+    if constexpr (KR > 0) {
+#pragma unroll
+        for (int j = 0; j < NCK; j++) kr[j] &= fmask;
+    }
+    int eq = 0;
+    each([&](unsigned k, int) { eq += (k & fmask) == prefix; });
+    unsigned id_end = 0xFFFFFFFFu;  // equal keys of blocks <= id_end are taken
+    if (block_sum(eq, s_scan) > need) {
+        // the need-th smallest block among the equal keys (every read of the bins ended before the last
+        // barrier)
+        s_hist[2 * tid] = 0u, s_hist[2 * tid + 1] = 0u, s_hist[NB + 2 * tid] = 0u, s_hist[NB + 2 * tid + 1] = 0u;
+        __syncthreads();
+        unsigned idp = 0u;
+        int need2 = need;
+        for (int pass = 0; pass < 2; pass++) {
+            const int shift = pass == 0 ? 7 : 0;
+            const unsigned pm = pass == 0 ? 0u : ~127u;  // the id bits found so far
+            unsigned* h = s_hist + pass * NB;
+            each([&](unsigned k, int b) {
+                if ((k & fmask) == prefix && ((unsigned)b & pm) == idp)
+                    __hip_atomic_fetch_add(&h[((unsigned)b >> shift) & 2047u], 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            });
+            __syncthreads();
+            const int c0 = (int)h[2 * tid], c1 = (int)h[2 * tid + 1];  // ascending digits
+            const int smaller = block_excl_scan(c0 + c1, s_scan + 32);
+            if (smaller < need2 && smaller + c0 + c1 >= need2) {  // exactly one thread
+                const bool in0 = smaller + c0 >= need2;
+                s_misc[4] = in0 ? 2 * tid : 2 * tid + 1;
+                s_misc[5] = in0 ? smaller : smaller + c0;
+            }
+            __syncthreads();
+            idp |= (unsigned)s_misc[4] << shift;
+            need2 -= s_misc[5];
+        }
+        id_end = idp;
+    }
+    asm volatile("" : "+v"(prefix));
+    // the mask: a chunk's four bits of each thread, OR-ed over eight lanes into the word of blocks
+    // [32 (tid / 8), + 32) of the chunk
+    const int nmw = (nblk + 31) >> 5;
+    auto mark = [&](u32x4 v, int j) {
+        unsigned bits = 0u;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const unsigned k = v[r] & fmask, b = (unsigned)(j * CHK + 4 * tid + r);
+            const bool sel = (v[r] >> 31) == 0u && (k > prefix || (k == prefix && b <= id_end));
+            bits |= (unsigned)sel << r;
+        }
+        unsigned wv = bits << (4 * (tid & 7));
+        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+        wv |= (unsigned)__builtin_amdgcn_mov_dpp((int)wv, 0x141, 0xF, 0xF, false);  // row_half_mirror
+        const int w = j * (CHK / 32) + (tid >> 3);
+        if ((tid & 7) == 0 && w < nmw) s_mask[w] = wv;
+    };
+    if constexpr (KR > 0) {
+#pragma unroll
+        for (int j = 0; j < NCK; j++) mark(kr[j], j);
+    } else {
+        for (int j = 0; j < nch; j++) mark(ld4(j), j);
+    }
+}
+
+// The selection of token t by one workgroup (the row `rs` holds ~score per block and 0 past nblk; the
+// token's first-digit histogram is `nh` copies of 2,048 bins at gh, summed here and cleared for the next
+// launch); writes the token's mask row and key bits. Thread tid takes blocks 1,024 j + tid (KR > 0: KR of
+// them held in registers, nblk <= KR * 1,024; KR == 0: read from memory at each use), so that each wave's
+// ballot over one of them is two mask words. A stored word L orders opposite to its key, and as a signed
+// value every L of a block (bit 31 set) lies below the 0 past nblk: key > T is (int) L < (int) ~T.
+template <int KR, bool COH>
+__device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
+                                              unsigned* s_mask, int* s_misc, int* s_scan, unsigned* s_hist,
+                                              unsigned* s_ck, unsigned* gh, int nh) {
+    constexpr int AUX = COH ? kScDevice : 0;  // device-coherent loads in the scoring launch itself
+    static_assert(KR == 0 || KR == 8 || KR == 16 || KR == 32 || KR == 64, "keys a thread");
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nch = KR > 0 ? KR : (nblk + kQsaThreads - 1) / kQsaThreads;
+    unsigned* s_cb = s_ck + kQsaCand;
+    // the first digit's counts of the bins this thread scans, 2,047 - 2 tid and the one below: one 8-byte
+    // device-coherent load a copy, all issued first (copies past nh lie outside the resource: they read 0)
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(gh, (short)0, nh * 2048 * 4, 0x00020000);
+    u32x2 gv[kQsaHistCopies];
+#pragma unroll
+    for (int i = 0; i < kQsaHistCopies; i++)
+        gv[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rh, (2048 * i + 2046 - 2 * tid) * 4, 0,
+                                                                              kScDevice));
+    auto ld = [&](int j) -> unsigned { return __builtin_amdgcn_raw_buffer_load_b32(rs, (j * kQsaThreads + tid) * 4, 0, AUX); };
+    unsigned kr[KR > 0 ? KR : 1];
+    if constexpr (KR > 0) {
+#pragma unroll
+        for (int j = 0; j < KR; j++) kr[j] = ld(j);  // every load issued before any is used
+    }
+    // the later passes' LDS bins start at zero
+#pragma unroll
+    for (int i = 0; i < 4; i++) s_hist[tid + i * kQsaThreads] = 0u;
+    unsigned g1 = 0u, g0 = 0u;
+#pragma unroll
+    for (int i = 0; i < kQsaHistCopies; i++) g0 += gv[i][0], g1 += gv[i][1];
+    // the first digit: the bins scanned from the top, two a thread
+    const int larger = block_excl_scan((int)(g1 + g0), s_scan + 32);
+    if (larger < a.top && larger + (int)(g1 + g0) >= a.top) {  // exactly one thread
+        const bool in1 = larger + (int)g1 >= a.top;
+        s_misc[0] = in1 ? 2047 - 2 * tid : 2046 - 2 * tid;
+        s_misc[1] = in1 ? larger : larger + (int)g1;
+        s_misc[2] = (int)(in1 ? g1 : g0);
+    }
+    __syncthreads();
+    // the bins start at zero for the next launch (their counts were used above)
+#pragma unroll
+    for (int i = 0; i < kQsaHistCopies; i++)
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, rh, (2048 * i + 2046 - 2 * tid) * 4, 0, kScDevice);
+    const unsigned d1 = (unsigned)s_misc[0];
+    const int need = a.top - s_misc[1], cnt = s_misc[2];  // to take from the bin, of cnt
+    if (cnt > kQsaCand) {
+        select_fallback<KR, COH>(rs, nblk, d1 << 20, need, cnt, s_mask, s_misc, s_scan, s_hist);
+    } else {
+        auto word = [&](int j) -> unsigned {
+            if constexpr (KR > 0) return kr[j];
+            else return ld(j);
+        };
+        // the candidates (key bits [30:20] == d1, i.e. L bits [31:20] == 0xFFF - d1; 0 past nblk never is)
+        // into LDS: wave w fills places [w kQsaW, + kQsaW) in order (per chunk a ballot, each candidate's place
+        // the count of the lanes below it); a wave with more candidates than places sends the whole selection
+        // to the fallback
+        constexpr int kQsaW = kQsaCand / (kQsaThreads / 64);
+        const unsigned dL = 0xFFFu - d1;
+        int nw = 0;  // the wave's candidates so far (uniform)
+        auto compact = [&](int j) {
+            const unsigned L = word(j);
+            const bool c = (L >> 20) == dL;
+            const unsigned long long bal = __ballot(c);
+            if (bal) {
+                const int at = nw + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+                if (c && at < kQsaW) s_ck[wave * kQsaW + at] = ~L, s_cb[wave * kQsaW + at] = (unsigned)(j * kQsaThreads + tid);
+                nw += (int)__popcll(bal);
+            }
+        };
+        if constexpr (KR > 0) {
+#pragma unroll
+            for (int j = 0; j < KR; j++) compact(j);
+        } else {
+            for (int j = 0; j < nch; j++) compact(j);
+        }
+        if (lane == 0) s_scan[wave] = nw;
+        __syncthreads();
+        const int nwl = lane < kQsaThreads / 64 ? s_scan[lane] : 0;
+        if (wave_max((unsigned)nwl) > (unsigned)kQsaW) {  // uniform: every wave reads the same counts
+            select_fallback<KR, COH>(rs, nblk, d1 << 20, need, cnt, s_mask, s_misc, s_scan, s_hist);
+            __syncthreads();
+            write_rows(a, t, nblk, s_mask);
+            return;
+        }
+        unsigned T, id_end;
+        resolve_candidates(s_ck, s_cb, s_scan, need, d1 << 20, s_hist, s_misc, s_scan, T, id_end);
+        // the mask: per wave and chunk, the ballot of the taken blocks is mask words 32 j + 2 wave (+1),
+        // gathered into the lanes of one register per 32 chunks and stored together. A tied key is taken when
+        // its block 1,024 j + tid <= id_end (uniform operands: no block id is held per key).
+        const int nT = (int)~__builtin_amdgcn_readfirstlane(T);
+        const int ide = (int)__builtin_amdgcn_readfirstlane(id_end);
+        // the ballot of chunk j into lanes 2 jj, 2 jj + 1 of acc
+        auto take = [&](unsigned long long bal, unsigned acc, int jj) -> unsigned {
+            return writelane((unsigned)(bal >> 32), 2 * jj + 1, writelane((unsigned)bal, 2 * jj, acc));
+        };
+        auto put = [&](int jb, unsigned acc) {
+            if (lane < 2 * min(32, nch - jb)) s_mask[32 * (jb + (lane >> 1)) + 2 * wave + (lane & 1)] = acc;
+        };
+        auto marks = [&](auto&& sel) {
+            if constexpr (KR > 0) {
+#pragma unroll
+                for (int jb = 0; jb < KR; jb += 32) {
+                    unsigned acc = 0u;
+#pragma unroll
+                    for (int jj = 0; jj < (KR < 32 ? KR : 32); jj++) acc = take(__ballot(sel(jb + jj)), acc, jj);
+                    put(jb, acc);
+                }
+            } else {
+                for (int jb = 0; jb < nch; jb += 32) {
+                    unsigned acc = 0u;
+                    for (int jj = 0; jj < 32 && jb + jj < nch; jj++) acc = take(__ballot(sel(jb + jj)), acc, jj);
+                    put(jb, acc);
+                }
+            }
+        };
+        if (id_end == 0xFFFFFFFFu)  // every key equal to T is taken
+            marks([&](int j) { return (int)word(j) <= nT; });
+        else
+            marks([&](int j) {
+                const int L = (int)word(j);
+                return L < nT || (L == nT && tid <= ide - j * kQsaThreads);
+            });
+    }
+    __syncthreads();
+    write_rows(a, t, nblk, s_mask);
+}
+
+// The scores of blocks [bc0, bc1) of token t at position p: sum over the heads of relu(q_h . key), stored
+// device-coherently into the token's score row as ~bits, and each score's first radix digit (bits [30:20])
+// counted in the LDS histogram `hist`. 16 lanes a pooled key (coalesced rows), DL = ID / 16 consecutive dims a lane,
+// RB rounds of 64 keys; the keys are loaded first, so that their latency hides behind the query heads'
+// prologue (RMS norm with the gamma as stored, rope to p).
+template <int IN_DT, int DL, int RB>
+__device__ __forceinline__ void score_chunk(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int p, int bc0,
+                                            int bc1, float* s_q, float* s_t, unsigned* hist) {
+    constexpr int ID = 16 * DL, G = kQsaThreads / 16;  // dims; keys a round
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = tid >> 4, sub = tid & 15;
+    float kv[RB][DL];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        // past the chunk: a valid row, its score not stored
+        const float* pk = a.pooled + (size_t)min(bc0 + rr * G + grp, bc1 - 1) * ID + sub * DL;
+#pragma unroll
+        for (int i = 0; i < DL; i += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
+            kv[rr][i] = v[0], kv[rr][i + 1] = v[1], kv[rr][i + 2] = v[2], kv[rr][i + 3] = v[3];
+        }
+    }
+    // the query heads: wave w takes heads w, w + 16, ...
+    for (int h = wave; h < a.IH; h += kQsaThreads / 64) {
+        float x[ID / 64], ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < ID / 64; k++) {
+            x[k] = load_in<IN_DT>(a.iq, ((size_t)t * a.IH + h) * ID + lane + 64 * k);
+            ss += x[k] * x[k];
+        }
+        ss = wave_sum(ss);
+        const float r = 1.0f / sqrtf(ss / (float)ID + a.eps);
+#pragma unroll
+        for (int k = 0; k < ID / 64; k++) s_t[h * ID + lane + 64 * k] = x[k] * r * a.gamma[lane + 64 * k];
+    }
+    __syncthreads();
+    for (int i = tid; i < a.IH * ID; i += kQsaThreads) {
+        const int h = i / ID;
+        rope_row(s_t + h * ID, s_q + h * ID, a.rope, p, a.R, ID, i - h * ID, ID);
+    }
+    __syncthreads();
+    float sc[RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) sc[rr] = 0.f;
+    for (int h = 0; h < a.IH; h++) {
+        float q[DL];
+#pragma unroll
+        for (int i = 0; i < DL; i += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(s_q + h * ID + sub * DL + i);
+            q[i] = v[0], q[i + 1] = v[1], q[i + 2] = v[2], q[i + 3] = v[3];
+        }
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            float dp = 0.f;
+#pragma unroll
+            for (int i = 0; i < DL; i++) dp = __builtin_fmaf(q[i], kv[rr][i], dp);
+            dp = sum16(dp);
+            sc[rr] += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const int b = bc0 + rr * G + grp;
+        if (sub == 0 && b < bc1) {
+            __builtin_amdgcn_raw_buffer_store_b32(~__float_as_uint(sc[rr]), rs, b * 4, 0, kScDevice);
+            // bits [30:20] (a score is >= +0: bit 31 is clear)
+            __hip_atomic_fetch_add(&hist[__float_as_uint(sc[rr]) >> 20], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+}
+
+// Grid (chunks, n), 1,024 threads: workgroup (c, t) scores blocks [CH c, CH c + CH) of token t and adds the
+// counts of its scores' first radix digit into the token's histogram; the last of the token's workgroups to
+// arrive selects. A token that selects nothing has its rows written by workgroup (0, t).
 // MODE 0: score, then the last workgroup of each token selects (device-coherent score reads). For many
 // blocks (64 keys a thread and more) the two run as two launches instead: MODE 1 scores only, MODE 2 (one
 // workgroup a token) selects, reading the scores with plain loads (the launch boundary makes them visible):
@@ -379,16 +680,18 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
 template <int IN_DT, int KR, int MODE, int CH = kQsaChunk>
 __global__ __launch_bounds__(kQsaThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_qsa_select(QsaSelectArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    unsigned* s_mask = reinterpret_cast<unsigned*>(smem);  // [kQsaMaskLds] the token's selection
+    unsigned* s_mask = reinterpret_cast<unsigned*>(smem);  // [kQsaMaskLds] the token's selection; scoring: the
+                                                           // first-digit counts [2,048]
     int* s_misc = reinterpret_cast<int*>(s_mask + kQsaMaskLds);  // [16]
     int* s_tot = s_misc + 16;                               // [16] spare
-    int* s_scan = s_tot + 16;                               // [48]: per-wave minima, maxima, sums
+    int* s_scan = s_tot + 16;                               // [48]: per-wave sums
     unsigned char* work = reinterpret_cast<unsigned char*>(s_scan + 48);
     float* s_q = reinterpret_cast<float*>(work);            // scoring: [IH][ID] normed, rotated query heads
     float* s_t = s_q + a.IH * a.ID;                         // scoring: [IH][ID] the normed heads before rotation
-    unsigned* s_hist = reinterpret_cast<unsigned*>(work);   // select: [2 passes][2,048] digit counts
+    unsigned* s_hist = reinterpret_cast<unsigned*>(work);   // select: [4,096] digit counts
+    unsigned* s_ck = s_hist + 4096;                         // select: [2][kQsaCand] candidate keys, blocks
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x;
     const int c = blockIdx.x, t = blockIdx.y;
     const int p = a.pos + t, nblk = (p + 1) / a.CR, ID = a.ID;
     const int kb_words = a.kb_words;
@@ -407,65 +710,33 @@ __global__ __launch_bounds__(kQsaThreads) __attribute__((amdgpu_waves_per_eu(4, 
     if (c >= ct) return;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)t * a.stride, (short)0,
                                                                         a.stride * 4, 0x00020000);
+    unsigned* gh = a.hist + (size_t)t * a.hcopies * 2048;  // the token's histogram copies
     if constexpr (MODE == 2) {
-        select_blocks<KR, false>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist);
+        select_blocks<KR, false>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist, s_ck, gh, a.hcopies);
         return;
     }
+    s_mask[tid] = 0u, s_mask[tid + kQsaThreads] = 0u;  // the chunk's first-digit counts
+    if (c == ct - 1)  // the row past nblk reads 0 (its words up to the row's end, a multiple of four)
+        for (int b = nblk + tid; b < a.stride; b += kQsaThreads)
+            __builtin_amdgcn_raw_buffer_store_b32(0u, rs, b * 4, 0, kScDevice);
 
-    // this chunk's pooled keys, 16 lanes a key (RB rounds of 64 keys), DL = ID / 16 consecutive dims a lane:
-    // loaded first, so that their latency hides behind the query heads' prologue
     constexpr int RB = CH / (kQsaThreads / 16);
     static_assert(RB * (kQsaThreads / 16) == CH, "whole rounds of one key per 16-lane group");
-    const int grp = tid >> 4, sub = tid & 15, DL = ID >> 4;
     const int bc0 = c * CH, bc1 = min(nblk, bc0 + CH);
-    float kv[RB][16];
-#pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-        const float* pk = a.pooled + (size_t)min(bc0 + rr * (kQsaThreads / 16) + grp, bc1 - 1) * ID + sub * DL;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4)
-            if (i < DL) {  // DL <= 16: the host keeps ID <= 256 (past the chunk: a valid row, score not stored)
-                const f32x4 v = *reinterpret_cast<const f32x4*>(pk + i);
-                kv[rr][i] = v[0], kv[rr][i + 1] = v[1], kv[rr][i + 2] = v[2], kv[rr][i + 3] = v[3];
-            }
+    switch (ID) {  // the host keeps ID a multiple of 64, <= 256
+        case 64: score_chunk<IN_DT, 4, RB>(a, rs, t, p, bc0, bc1, s_q, s_t, s_mask); break;
+        case 128: score_chunk<IN_DT, 8, RB>(a, rs, t, p, bc0, bc1, s_q, s_t, s_mask); break;
+        case 192: score_chunk<IN_DT, 12, RB>(a, rs, t, p, bc0, bc1, s_q, s_t, s_mask); break;
+        default: score_chunk<IN_DT, 16, RB>(a, rs, t, p, bc0, bc1, s_q, s_t, s_mask); break;
     }
-    // the query heads: RMS-normed (gamma as stored), rotated to p; wave w takes heads w, w + 16, ...
-    for (int h = wave; h < a.IH; h += kQsaThreads / 64) {
-        float ss = 0.f;
-        for (int d = lane; d < ID; d += 64) {
-            const float x = load_in<IN_DT>(a.iq, ((size_t)t * a.IH + h) * ID + d);
-            s_t[h * ID + d] = x;
-            ss += x * x;
-        }
-        ss = wave_sum(ss);
-        const float r = 1.0f / sqrtf(ss / (float)ID + a.eps);
-        for (int d = lane; d < ID; d += 64) s_t[h * ID + d] = s_t[h * ID + d] * r * a.gamma[d];
-    }
+    // the chunk's counts into one of the token's histogram copies (workgroups in turn: fewer adds meet at
+    // one address), which the selecting workgroup sums and clears
     __syncthreads();
-    for (int i = tid; i < a.IH * ID; i += kQsaThreads) {
-        const int h = i / ID;
-        rope_row(s_t + h * ID, s_q + h * ID, a.rope, p, a.R, ID, i - h * ID, ID);
-    }
-    __syncthreads();
-
-    // the chunk's scores: sum over the heads of relu(q_h . key), the dot products summed over each 16-lane row
-#pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-        const int b = bc0 + rr * (kQsaThreads / 16) + grp;
-        float sc = 0.f;
-        for (int h = 0; h < a.IH; h++) {
-            const float* qh = s_q + h * ID + sub * DL;
-            float dp = 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                if (i < DL) dp = __builtin_fmaf(qh[i], kv[rr][i], dp);
-            dp = sum16(dp);
-            sc += dp > 0.f ? dp : 0.f;  // relu; -0 and NaN contribute +0, so every score is >= +0
-        }
-        if (sub == 0 && b < bc1) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc), rs, b * 4, 0, kScDevice);
-    }
+    unsigned* gc = gh + (size_t)(c % a.hcopies) * 2048;
+    for (int i = tid; i < 2048; i += kQsaThreads)
+        if (const unsigned v = s_mask[i]) __hip_atomic_fetch_add(gc + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (MODE == 1) return;
-    // arrive: the stores are acknowledged (device-coherent) before the counter moves
+    // arrive: the score stores and histogram adds are acknowledged (device-coherent) before the counter moves
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -477,7 +748,7 @@ __global__ __launch_bounds__(kQsaThreads) __attribute__((amdgpu_waves_per_eu(4, 
     if (s_misc[0] != ct - 1) return;
 
     // ---- the last workgroup of token t: exact top-`top` by (score desc, block id asc) ---------------
-    select_blocks<KR, true>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist);  // the host sizes KR for the call's last token
+    select_blocks<KR, true>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist, s_ck, gh, a.hcopies);  // KR: the last token's
 }
 
 // ---- key bits from a block mask (shaders/attention.comp:35-43) -------------------------------------------
@@ -488,7 +759,7 @@ __global__ __launch_bounds__(256) void k_qsa_key_bits(QsaKeyBitsArgs a) {
 }
 
 size_t qsa_select_lds(int IH, int ID) {
-    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)2 * 2048 * 4);
+    const size_t work = std::max((size_t)2 * IH * ID * 4, (size_t)(4096 + 2 * kQsaCand) * 4);
     return (size_t)(kQsaMaskLds + 32 + 48) * 4 + work;
 }
 
@@ -553,6 +824,9 @@ static hipError_t launch_select_dt(const QsaSelectArgs& a, int kr, size_t shm, d
 }
 
 hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s) {
+    if (a.hcopies < 1 || a.hcopies > kQsaHistCopies || a.n * a.hcopies > kQsaHistTokens || a.hist == nullptr ||
+        a.stride % 4)
+        return hipErrorInvalidValue;
     const size_t shm = qsa_select_lds(a.IH, a.ID);
     const int nmax = (a.pos + a.n) / a.CR;
     const dim3 grid((nmax + kQsaChunk - 1) / kQsaChunk > 0 ? (nmax + kQsaChunk - 1) / kQsaChunk : 1, a.n);

@@ -36,6 +36,8 @@ struct qwattn_ctx {
     int pf_slots_per_head = 0;   // prefill: split slots per KV head in pf_part / pf_cnt
     float* qsa_scores = nullptr; // QSA select: block scores of the tokens of one launch (kQsaScoreBytes)
     int* qsa_cnt = nullptr;      // QSA select: per-token arrival counters [max_tokens], zero between launches
+    unsigned* qsa_hist = nullptr; // QSA select: first-digit histograms [qsa_hist_n][2048], zero between launches
+    int qsa_hist_n = 0;           // histograms in qsa_hist: a select launch holds that many tokens x copies
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
     int last_splits = 0;         // split count of the last qwattn_attend_partial / qwattn_decode_partial
     int last_n = 0;
@@ -245,6 +247,8 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     const int qt_max = qw::pf_query_tiles(cfg->max_tokens, NH / NKV);
     c->pf_slots_per_head = std::max(1, std::max(qt_max / 2, std::min(qt_max, c->n_cu / (2 * NKV))));
     const size_t pf_slots = (size_t)NKV * c->pf_slots_per_head * 4;
+    c->qsa_hist_n = std::min(cfg->max_tokens, qw::kQsaHistTokens);
+    const size_t hist_tokens = (size_t)c->qsa_hist_n;
     bool ok = hipMalloc(&c->pf_part, sizeof(float) * 2 * pf_slots * qw::pf_part_floats(D)) == hipSuccess &&
               hipMalloc(&c->pf_cnt, sizeof(int) * pf_slots) == hipSuccess &&
               hipMalloc(&c->inv_freq, sizeof(float) * std::max(1, R / 2)) == hipSuccess &&
@@ -256,6 +260,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->q32, sizeof(float) * qn) == hipSuccess && hipMalloc(&c->q16, 2 * qn) == hipSuccess &&
               hipMalloc(&c->qsa_scores, kQsaScoreBytes) == hipSuccess &&
               hipMalloc(&c->qsa_cnt, sizeof(int) * cfg->max_tokens) == hipSuccess &&
+              hipMalloc(&c->qsa_hist, sizeof(unsigned) * 2048 * hist_tokens) == hipSuccess &&
               hipHostMalloc(&c->wait_err_host, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
               hipHostGetDevicePointer((void**)&c->wait_err_dev, c->wait_err_host, 0) == hipSuccess;
     if (!ok) {
@@ -270,6 +275,7 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
         hipMemset(c->part_ml, 0, sizeof(float) * part * 2) != hipSuccess ||
         hipMemset(c->pf_cnt, 0, sizeof(int) * pf_slots) != hipSuccess ||
         hipMemset(c->qsa_cnt, 0, sizeof(int) * cfg->max_tokens) != hipSuccess ||
+        hipMemset(c->qsa_hist, 0, sizeof(unsigned) * 2048 * hist_tokens) != hipSuccess ||
         hipMemset(c->ep, 0, sizeof(unsigned long long) * NKV) != hipSuccess ||
         hipMemset(c->rec, 0, sizeof(float) * 4 * part) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         qwattn_destroy(c);
@@ -285,7 +291,8 @@ int qwattn_destroy(qwattn_ctx* c) {
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
     for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ep, (void*)c->rec,
-                    (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt, (void*)c->qsa_scores, (void*)c->qsa_cnt})
+                    (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt, (void*)c->qsa_scores, (void*)c->qsa_cnt,
+                    (void*)c->qsa_hist})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
@@ -475,6 +482,10 @@ int qwattn_qk_norm_rope_append(qwattn_ctx* c, void* stream, const void* qg, cons
 // QSA key bits of a call (NULL: dense): checks the row width and raises the split count until no workgroup
 // has more tiles than its kernel holds key words for (kQsaTiles: the loader-wave kernel, at most 8 query rows
 // per KV head; kQsaChunkTiles: the 16-row-slice kernel)
+// Histogram copies a token of a select launch of n tokens takes: up to 8 (the scoring workgroups add their
+// counts into the copies in turn), within the context's histograms.
+static int qsa_hist_copies(const qwattn_ctx* c, int n) { return std::max(1, std::min(8, c->qsa_hist_n / std::max(1, n))); }
+
 static int qsa_args(qwattn_ctx* c, const char* fn, const uint32_t* kbits, int kb_words, int pos, int n, Split* sp,
                     qw::DecodeArgs* a) {
     if (!kbits) return QWATTN_OK;
@@ -933,16 +944,17 @@ int qwattn_qsa_select(qwattn_ctx* c, void* stream, const void* iq, int in_dtype,
         return fail(c, QWATTN_EINVAL, "qwattn_qsa_select: kb_words %d < %d keys / 32", kb_words, pos + n);
     if (int rc = take_wait_error(c)) return rc;
     DeviceGuard dg(c->device);
-    const int stride = std::max(1, nmax);
-    const int per = (int)std::max<size_t>(1, kQsaScoreBytes / ((size_t)stride * sizeof(float)));
+    const int stride = (std::max(1, nmax) + 3) & ~3;  // score rows padded to whole 16-byte loads
+    const int per = (int)std::min<size_t>(c->qsa_hist_n,
+                                          std::max<size_t>(1, kQsaScoreBytes / ((size_t)stride * sizeof(float))));
     for (int t0 = 0; t0 < n; t0 += per) {
         const int nt = std::min(per, n - t0);
         qw::QsaSelectArgs a{(const char*)iq + (size_t)t0 * idx_heads * idx_dim * (in_dtype == QWATTN_F32 ? 4 : 2),
-                            q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt,
+                            q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, c->qsa_hist,
                             mask ? mask + (size_t)t0 * mask_words : nullptr,
                             key_bits ? key_bits + (size_t)t0 * kb_words : nullptr, nullptr, nullptr, mask_words,
                             kb_words, stride, pos + t0, nt, idx_heads, idx_dim, cr, budget / cr, g.rope_dim,
-                            g.rms_eps};
+                            g.rms_eps, qsa_hist_copies(c, nt)};
         HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
     }
     return QWATTN_OK;
@@ -957,7 +969,9 @@ int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq
         return fail(c, QWATTN_ERANGE, "qwattn_qsa_index: positions [%d, %d) beyond the capacity %d (max_ctx %d)", pos,
                     pos + n, cap, c->cfg.max_ctx);
     const int nmax = (pos + n) / std::max(cr, 1);
-    const int per = (int)std::max<size_t>(1, kQsaScoreBytes / ((size_t)std::max(1, nmax) * sizeof(float)));
+    const int stride = (std::max(1, nmax) + 3) & ~3;  // score rows padded to whole 16-byte loads
+    const int per = (int)std::min<size_t>(c->qsa_hist_n,
+                                          std::max<size_t>(1, kQsaScoreBytes / ((size_t)stride * sizeof(float))));
     if (cr < 2 || nmax != pos / cr || n > per) {
         // a block completes (or the tokens take several select launches): the pooling launch, then the select
         if (int rc = qwattn_qsa_pool(c, stream, ik, in_dtype, k_gamma, idx_dim, cr, raw, pooled, cap, pos, n)) return rc;
@@ -986,9 +1000,9 @@ int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq
         return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: kb_words %d < %d keys / 32", kb_words, pos + n);
     if (int rc = take_wait_error(c)) return rc;
     DeviceGuard dg(c->device);
-    qw::QsaSelectArgs a{iq, q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, mask, key_bits, ik, raw, mask_words,
-                        kb_words, std::max(1, nmax), pos, n, idx_heads, idx_dim, cr, budget / cr, g.rope_dim,
-                        g.rms_eps};
+    qw::QsaSelectArgs a{iq, q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, c->qsa_hist, mask, key_bits, ik,
+                        raw, mask_words, kb_words, stride, pos, n, idx_heads, idx_dim, cr, budget / cr,
+                        g.rope_dim, g.rms_eps, qsa_hist_copies(c, n)};
     HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
     return QWATTN_OK;
 }

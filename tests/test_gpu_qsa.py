@@ -5,7 +5,9 @@ Indexer: the pooled block keys agree with the oracle's to fp32 rounding (rtol 1e
 oracle's exactly, except where the oracle's own scores put the budget boundary within float rounding of a
 tie (|score - threshold| <= 1e-5 * (1 + threshold)): there a block may swap with its near-equal neighbour,
 and the test checks that only such blocks differ. Zero scores (all heads' dots negative) tie exactly on
-both sides and fall back to the lower block ids, which the comparison covers.
+both sides and fall back to the lower block ids: the cases whose threshold is 0 allow no swap (zero
+queries) or at most two (a near-zero dot whose sign rounding flips), where a wrong tie order would swap
+thousands.
 """
 import numpy as np
 import pytest
@@ -78,7 +80,21 @@ CASES = {
     "cr4_256k": (QsaShape(1, 64, 4, 1024, 64), 262152, [(0, 262144, 0), (262144, 1, 1), (262145, 2, 1)], "f32"),
     # zero indexer queries: every score is 0, the lowest block ids win (no histogram pass at all)
     "zeros": (QsaShape(2, 128, 4, 256, 64), 8200, [(0, 8000, 0), (8000, 2, 1), (8002, 1, 1)], "f32"),
+    # the same past 32,768 blocks (scoring launch + selection launch)
+    "zeros_cr2_64k": (QsaShape(2, 64, 2, 512, 64), 65560, [(0, 65544, 0), (65544, 2, 1)], "f32"),
+    # one indexer head: about half the blocks score exactly 0 (a negative dot), and the budget reaches into
+    # them, so the threshold is 0 and only part of its ties are taken, lowest block ids first; in the one-launch
+    # select, the two-launch select and the one that reads the scores from memory
+    "halfzero_cr4_8k": (QsaShape(1, 64, 4, 4 * 1500, 64), 8200, [(0, 8000, 0), (8000, 2, 1)], "f32"),
+    "halfzero_cr2_64k": (QsaShape(1, 64, 2, 2 * 24000, 64), 65560, [(0, 65544, 0), (65544, 2, 1)], "f32"),
+    "halfzero_long_cr2": (QsaShape(1, 64, 2, 2 * 70000, 64), 262144, [(0, 262000, 0), (262000, 2, 1)], "f32"),
+    # raw keys repeating every `period` blocks and queries zero on the rotated dims: every score value recurs
+    # on many blocks, exactly, so the threshold's ties are cut by block id among the compacted candidates
+    "ties_cr4_8k": (QsaShape(2, 128, 4, 4 * 300, 64), 8200, [(0, 8000, 0), (8000, 2, 1), (8002, 1, 1)], "f32"),
+    "ties_cr2_64k": (QsaShape(1, 128, 2, 2 * 5000, 64), 65560, [(0, 65544, 0), (65544, 2, 1)], "f32"),
+    "ties_long_cr2": (QsaShape(1, 128, 2, 2 * 9000, 64), 262144, [(0, 262000, 0), (262000, 2, 1)], "f32"),
 }
+TIE_PERIOD = {"ties_cr4_8k": 37, "ties_cr2_64k": 101, "ties_long_cr2": 1009}  # blocks
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -99,8 +115,12 @@ def _indexer_case(qw, oracle, name, qs, max_ctx, calls, dt):
     import oracle as orc
     tot = sum(c[1] for c in calls)
     iq, ik, qg, kg = qsa_inputs(41, tot, qs)
-    if name == "zeros":
+    if name.startswith("zeros"):
         iq[:] = 0.0
+    if name in TIE_PERIOD:
+        rows = TIE_PERIOD[name] * qs.CR
+        ik = np.ascontiguousarray(np.tile(ik[:rows], (-(-len(ik) // rows), 1))[:len(ik)])
+        iq[..., :qs.R] = 0.0
     if dt == "bf16":  # the oracle reads the same bf16-rounded values
         iq = torch.from_numpy(iq).bfloat16().float().numpy()
         ik = torch.from_numpy(ik).bfloat16().float().numpy()
@@ -135,6 +155,10 @@ def _indexer_case(qw, oracle, name, qs, max_ctx, calls, dt):
             swaps = assert_selection(got, want, scores, qs, pos, n, f"{name} pos={pos}")
             print(f"qsa {name} pos={pos} n={n}: {swaps} near-tie swap(s) of {n * qs.top} selected blocks",
                   flush=True)
+            if name.startswith(("zeros", "ties")):  # exact ties on both sides: block order alone decides
+                assert swaps == 0
+            if name.startswith("halfzero"):  # thousands of exact zeros at the threshold: at most a sign flip or two
+                assert swaps <= 2
             # the key bits follow the GPU's own selection by the reference's visibility rule
             assert np.array_equal(host(kbits).view(np.uint32), orc.qsa_key_bits(got, pos, n, qs.CR))
         row += n
