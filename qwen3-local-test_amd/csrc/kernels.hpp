@@ -142,6 +142,8 @@ struct QsaSelectArgs {
     float* scores;        // workspace [n][stride], stride >= (pos+n)/CR and a multiple of 4
     int* cnt;             // [n] arrival counters, zero between launches
     unsigned* hist;       // [n][hcopies][2048] first-digit counts of the scores, zero between launches
+    unsigned* cand;       // two-launch form: [n][kQsaSelWgMax][2][kQsaCandWg] candidates handed to the last
+    int* cand_n;          //   workgroup, [n][kQsaSelWgMax] their counts
     unsigned* mask;       // [n][mask_words] block bitmask, or NULL
     unsigned* kbits;      // [n][kb_words] key visibility bits, or NULL
     const void* ik;       // with raw: the tokens' raw indexer keys [n][ID] (in_dtype), appended by the launch
@@ -154,6 +156,11 @@ struct QsaSelectArgs {
 hipError_t launch_qsa_select(const QsaSelectArgs& a, int in_dtype, hipStream_t s);
 // First-digit histograms (2,048 bins) a select launch may use: a token takes 1 to 8 copies
 constexpr int kQsaHistTokens = 1024;
+// The two-launch form (more than 32,768 complete blocks): selection workgroups of kQsaSelBlocks blocks, each
+// handing over at most kQsaCandWg candidates, at most kQsaSelWgMax a token (kQsaMaskLds * 32 blocks), for at
+// most kQsaCandTokens tokens a launch
+constexpr int kQsaSelBlocks = 4096, kQsaCandWg = 256, kQsaSelWgMax = 36, kQsaCandTokens = 32;
+int qsa_select_tokens(int nmax);  // tokens a select launch may hold at nmax complete blocks
 size_t qsa_select_lds(int IH, int ID);
 int qsa_mask_lds_words();  // complete blocks a select launch can hold: 32 x this
 

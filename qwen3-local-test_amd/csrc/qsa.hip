@@ -256,20 +256,17 @@ __device__ __forceinline__ void write_rows(const QsaSelectArgs& a, int t, int nb
             a.kbits[(size_t)t * kb_words + w] = key_word(s_mask, w, a.CR, nblk);
 }
 
-// Of the candidates ck[] (blocks cb[]; 16 segments of kQsaCand / 16 places, segment w holding n[w]), which
-// share the bits above bit 20 (`prefix`), the `need` largest by (key, then the lower block) are taken: T is the
-// smallest taken key, and of the keys equal to T those of blocks <= id_end (every one when id_end is ~0u).
-// Two 10-bit digit passes over the keys from the top, then, when T has more ties than places, two 9-bit
-// passes over the tied keys' blocks from the smallest (block ids < 2^18). LDS histograms of 1,024 bins (four,
-// zero on entry), thread tid scanning one.
-__device__ __forceinline__ void resolve_candidates(const unsigned* ck, const unsigned* cb, const int* n, int need,
+// Of the candidates ck[] (blocks cb[]; places tid and tid + 1,024 filled when v0, v1), which share the bits
+// above bit 20 (`prefix`), the `need` largest by (key, then the lower block) are taken: T is the smallest
+// taken key, and of the keys equal to T those of blocks <= id_end (every one when id_end is ~0u). Two 10-bit
+// digit passes over the keys from the top, then, when T has more ties than places, two 9-bit passes over the
+// tied keys' blocks from the smallest (block ids < 2^18). LDS histograms of 1,024 bins (four, zero on entry),
+// thread tid scanning one.
+__device__ __forceinline__ void resolve_candidates(const unsigned* ck, const unsigned* cb, bool v0, bool v1, int need,
                                                    unsigned prefix, unsigned* s_hist, int* s_misc, int* s_scan,
                                                    unsigned& T, unsigned& id_end) {
-    constexpr int W = kQsaCand / (kQsaThreads / 64);
     static_assert(kQsaCand == 2 * kQsaThreads, "two places a thread");
     const int tid = threadIdx.x;
-    // this thread's two places, tid and tid + 1,024, when filled
-    const bool v0 = (tid % W) < n[tid / W], v1 = ((tid + kQsaThreads) % W) < n[(tid + kQsaThreads) / W];
     for (int pass = 0; pass < 2; pass++) {
         const int shift = pass == 0 ? 10 : 0;
         const unsigned pmask = pass == 0 ? 0xFFF00000u : 0xFFFFFC00u;  // the bits found so far
@@ -463,6 +460,44 @@ __device__ __forceinline__ void select_fallback(__amdgpu_buffer_rsrc_t rs, int n
     }
 }
 
+// The token's first-digit histogram (nh copies of 2,048 bins at gh): thread tid's bins 2,047 - 2 tid and the
+// one below, summed over the copies (one 8-byte device-coherent load a copy, issued at construction; copies
+// past nh lie outside the resource and read 0).
+struct FirstDigit {
+    __amdgpu_buffer_rsrc_t rh;
+    u32x2 gv[kQsaHistCopies];
+    __device__ __forceinline__ FirstDigit(unsigned* gh, int nh) {
+        rh = __builtin_amdgcn_make_buffer_rsrc(gh, (short)0, nh * 2048 * 4, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < kQsaHistCopies; i++)
+            gv[i] = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rh, (2048 * i + 2046 - 2 * (int)threadIdx.x) * 4, 0, kScDevice));
+    }
+    // the bin of the top-th largest key, scanned from the top two bins a thread: s_misc[0] the digit, [1] the
+    // keys of larger digits, [2] the bin's keys (every thread reads them after the barrier)
+    __device__ __forceinline__ void scan(int top, int* s_misc, int* s_scan) const {
+        const int tid = threadIdx.x;
+        unsigned g1 = 0u, g0 = 0u;
+#pragma unroll
+        for (int i = 0; i < kQsaHistCopies; i++) g0 += gv[i][0], g1 += gv[i][1];
+        const int larger = block_excl_scan((int)(g1 + g0), s_scan + 32);
+        if (larger < top && larger + (int)(g1 + g0) >= top) {  // exactly one thread
+            const bool in1 = larger + (int)g1 >= top;
+            s_misc[0] = in1 ? 2047 - 2 * tid : 2046 - 2 * tid;
+            s_misc[1] = in1 ? larger : larger + (int)g1;
+            s_misc[2] = (int)(in1 ? g1 : g0);
+        }
+        __syncthreads();
+    }
+    // zero for the next launch (after every reader has its counts)
+    __device__ __forceinline__ void clear() const {
+#pragma unroll
+        for (int i = 0; i < kQsaHistCopies; i++)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, rh, (2048 * i + 2046 - 2 * (int)threadIdx.x) * 4, 0,
+                                                  kScDevice);
+    }
+};
+
 // The selection of token t by one workgroup (the row `rs` holds ~score per block and 0 past nblk; the
 // token's first-digit histogram is `nh` copies of 2,048 bins at gh, summed here and cleared for the next
 // launch); writes the token's mask row and key bits. Thread tid takes blocks 1,024 j + tid (KR > 0: KR of
@@ -478,14 +513,7 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nch = KR > 0 ? KR : (nblk + kQsaThreads - 1) / kQsaThreads;
     unsigned* s_cb = s_ck + kQsaCand;
-    // the first digit's counts of the bins this thread scans, 2,047 - 2 tid and the one below: one 8-byte
-    // device-coherent load a copy, all issued first (copies past nh lie outside the resource: they read 0)
-    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(gh, (short)0, nh * 2048 * 4, 0x00020000);
-    u32x2 gv[kQsaHistCopies];
-#pragma unroll
-    for (int i = 0; i < kQsaHistCopies; i++)
-        gv[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rh, (2048 * i + 2046 - 2 * tid) * 4, 0,
-                                                                              kScDevice));
+    const FirstDigit fd(gh, nh);
     auto ld = [&](int j) -> unsigned { return __builtin_amdgcn_raw_buffer_load_b32(rs, (j * kQsaThreads + tid) * 4, 0, AUX); };
     unsigned kr[KR > 0 ? KR : 1];
     if constexpr (KR > 0) {
@@ -495,22 +523,8 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     // the later passes' LDS bins start at zero
 #pragma unroll
     for (int i = 0; i < 4; i++) s_hist[tid + i * kQsaThreads] = 0u;
-    unsigned g1 = 0u, g0 = 0u;
-#pragma unroll
-    for (int i = 0; i < kQsaHistCopies; i++) g0 += gv[i][0], g1 += gv[i][1];
-    // the first digit: the bins scanned from the top, two a thread
-    const int larger = block_excl_scan((int)(g1 + g0), s_scan + 32);
-    if (larger < a.top && larger + (int)(g1 + g0) >= a.top) {  // exactly one thread
-        const bool in1 = larger + (int)g1 >= a.top;
-        s_misc[0] = in1 ? 2047 - 2 * tid : 2046 - 2 * tid;
-        s_misc[1] = in1 ? larger : larger + (int)g1;
-        s_misc[2] = (int)(in1 ? g1 : g0);
-    }
-    __syncthreads();
-    // the bins start at zero for the next launch (their counts were used above)
-#pragma unroll
-    for (int i = 0; i < kQsaHistCopies; i++)
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, rh, (2048 * i + 2046 - 2 * tid) * 4, 0, kScDevice);
+    fd.scan(a.top, s_misc, s_scan);
+    fd.clear();
     const unsigned d1 = (unsigned)s_misc[0];
     const int need = a.top - s_misc[1], cnt = s_misc[2];  // to take from the bin, of cnt
     if (cnt > kQsaCand) {
@@ -554,7 +568,10 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
             return;
         }
         unsigned T, id_end;
-        resolve_candidates(s_ck, s_cb, s_scan, need, d1 << 20, s_hist, s_misc, s_scan, T, id_end);
+        const int* nwv = s_scan;  // wave w's candidates fill places [w kQsaW, + nwv[w])
+        resolve_candidates(s_ck, s_cb, (tid % kQsaW) < nwv[tid / kQsaW],
+                           ((tid + kQsaThreads) % kQsaW) < nwv[(tid + kQsaThreads) / kQsaW], need, d1 << 20, s_hist,
+                           s_misc, s_scan, T, id_end);
         // the mask: per wave and chunk, the ballot of the taken blocks is mask words 32 j + 2 wave (+1),
         // gathered into the lanes of one register per 32 chunks and stored together. A tied key is taken when
         // its block 1,024 j + tid <= id_end (uniform operands: no block id is held per key).
@@ -594,6 +611,142 @@ __device__ __forceinline__ void select_blocks(const QsaSelectArgs& a, __amdgpu_b
     }
     __syncthreads();
     write_rows(a, t, nblk, s_mask);
+}
+
+// The two-launch form's selection, spread: workgroup (g, t) takes blocks [4,096 g, + 4,096) of token t
+// (thread tid: blocks 4,096 g + 1,024 j + tid, j < 4). Every workgroup finds the threshold's first digit from
+// the histogram itself, writes its part of the mask row and key bits with the blocks above that digit taken
+// (device-coherent stores), and hands the digit's keys (the candidates) to its places in the token's
+// candidate area; the last to arrive resolves the candidates and ORs the taken ones' bits in (device-scope
+// atomics, after every part is stored). A workgroup with more candidates than its places, or more candidates
+// in all than LDS holds, sends the token to the one-workgroup selection over every key.
+__device__ __forceinline__ void select_spread(const QsaSelectArgs& a, __amdgpu_buffer_rsrc_t rs, int t, int nblk,
+                                              int g, unsigned* s_mask, int* s_misc, int* s_scan, unsigned* s_hist,
+                                              unsigned* s_ck, unsigned* gh) {
+    constexpr int J = kQsaSelBlocks / kQsaThreads;  // keys a thread
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int gt = (nblk + kQsaSelBlocks - 1) / kQsaSelBlocks;  // the token's workgroups
+    const FirstDigit fd(gh, a.hcopies);
+    unsigned L[J];
+#pragma unroll
+    for (int j = 0; j < J; j++)
+        L[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (g * kQsaSelBlocks + j * kQsaThreads + tid) * 4, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) s_hist[tid + i * kQsaThreads] = 0u;  // the last workgroup's bins
+    fd.scan(a.top, s_misc, s_scan);
+    const unsigned d1 = (unsigned)s_misc[0], dL = 0xFFFu - d1;
+    const int need = a.top - s_misc[1], cnt = s_misc[2];
+    // taken outright: key digit above d1, i.e. L bits [31:20] below 0xFFF - d1 (as signed values, so that the
+    // 0 past nblk is not); per chunk the wave's ballot is mask words 128 g + 32 j + 2 wave (+1). Candidates:
+    // L bits [31:20] == 0xFFF - d1, counted per wave
+    unsigned long long cbal[J];
+    int nw = 0;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const unsigned long long above = __ballot((int)L[j] < (int)(dL << 20));
+        if (lane < 2) s_mask[128 * g + 32 * j + 2 * wave + lane] = lane ? (unsigned)(above >> 32) : (unsigned)above;
+        cbal[j] = __ballot((L[j] >> 20) == dL);
+        nw += (int)__popcll(cbal[j]);
+    }
+    if (lane == 0) s_scan[wave] = nw;
+    __syncthreads();
+    int at = 0, tot = 0;  // this wave's first place; the workgroup's candidates
+    for (int w = 0; w < kQsaThreads / 64; w++) {
+        const int c = s_scan[w];
+        at += w < wave ? c : 0;
+        tot += c;
+    }
+    unsigned* ck = a.cand + ((size_t)t * kQsaSelWgMax + g) * 2 * kQsaCandWg;  // [keys][blocks]
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const unsigned long long bal = cbal[j];
+        const int pos = at + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+        if (((bal >> lane) & 1ull) && pos < kQsaCandWg) {
+            __hip_atomic_store(ck + pos, ~L[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ck + kQsaCandWg + pos, (unsigned)(g * kQsaSelBlocks + j * kQsaThreads + tid),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        at += (int)__popcll(bal);
+    }
+    if (tid == 0) __hip_atomic_store(a.cand_n + (size_t)t * kQsaSelWgMax + g, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // this workgroup's words of the mask row and key bits (the last one's run to the rows' ends); the key words
+    // of blocks [4,096 g, + 4,096) read only this workgroup's mask words (4,096 CR keys are whole words)
+    const int nmw = (nblk + 31) >> 5, last = g == gt - 1;
+    if (a.mask) {
+        const int w1 = last ? a.mask_words : min(a.mask_words, 128 * (g + 1));
+        for (int w = 128 * g + tid; w < w1; w += kQsaThreads)
+            __hip_atomic_store(a.mask + (size_t)t * a.mask_words + w, w < nmw ? s_mask[w] : 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (a.kbits) {
+        const int k0 = 128 * g * a.CR, k1 = last ? a.kb_words : min(a.kb_words, k0 + 128 * a.CR);
+        for (int w = k0 + tid; w < k1; w += kQsaThreads)
+            __hip_atomic_store(a.kbits + (size_t)t * a.kb_words + w, key_word(s_mask, w, a.CR, nblk), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // arrive: every store acknowledged before the counter moves
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(a.cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_misc[8] = old;
+        if (old == gt - 1) __hip_atomic_store(a.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (s_misc[8] != gt - 1) return;
+
+    // ---- the last workgroup: every part is stored; the candidates into LDS, in workgroup order -------------
+    int* s_cn = reinterpret_cast<int*>(s_mask);  // [gt + 1] the workgroups' first places
+    const int cg = tid < gt ? __hip_atomic_load(a.cand_n + (size_t)t * kQsaSelWgMax + tid, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0;
+    const int over = __syncthreads_or(cg > kQsaCandWg);
+    const int first = block_excl_scan(cg, s_scan + 32);
+    if (tid < gt) s_cn[tid] = first;
+    if (tid == gt - 1) s_cn[gt] = first + cg;
+    __syncthreads();
+    const int total = s_cn[gt];
+    if (over || total != cnt || total > kQsaCand) {
+        select_blocks<0, false>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist, s_ck, gh, a.hcopies);
+        return;
+    }
+    unsigned* s_cb = s_ck + kQsaCand;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = tid + r * kQsaThreads;
+        if (i < total) {
+            int gg = 0;
+            while (s_cn[gg + 1] <= i) gg++;
+            const unsigned* src = a.cand + ((size_t)t * kQsaSelWgMax + gg) * 2 * kQsaCandWg + (i - s_cn[gg]);
+            s_ck[i] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_cb[i] = __hip_atomic_load(src + kQsaCandWg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    fd.clear();  // every workgroup read its counts before arriving
+    __syncthreads();
+    unsigned T, id_end;
+    resolve_candidates(s_ck, s_cb, tid < total, tid + kQsaThreads < total, need, d1 << 20, s_hist, s_misc, s_scan, T,
+                       id_end);
+    // the taken candidates' bits into the stored rows
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = tid + r * kQsaThreads;
+        if (i >= total) continue;
+        const unsigned k = s_ck[i], b = s_cb[i];
+        if (!(k > T || (k == T && b <= id_end))) continue;
+        if (a.mask)
+            __hip_atomic_fetch_or(a.mask + (size_t)t * a.mask_words + (b >> 5), 1u << (b & 31), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        if (a.kbits) {
+            const int k0 = (int)b * a.CR, k1 = k0 + a.CR;  // the block's keys
+            for (int w = k0 >> 5; w <= (k1 - 1) >> 5 && w < a.kb_words; w++) {
+                const int lo = max(k0, 32 * w) - 32 * w, hi = min(k1, 32 * w + 32) - 32 * w;
+                const unsigned bits = (hi == 32 ? 0xFFFFFFFFu : (1u << hi) - 1u) & ~((1u << lo) - 1u);
+                __hip_atomic_fetch_or(a.kbits + (size_t)t * a.kb_words + w, bits, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
 }
 
 // The scores of blocks [bc0, bc1) of token t at position p: sum over the heads of relu(q_h . key), stored
@@ -712,7 +865,7 @@ __global__ __launch_bounds__(kQsaThreads) __attribute__((amdgpu_waves_per_eu(4, 
                                                                         a.stride * 4, 0x00020000);
     unsigned* gh = a.hist + (size_t)t * a.hcopies * 2048;  // the token's histogram copies
     if constexpr (MODE == 2) {
-        select_blocks<KR, false>(a, rs, t, nblk, s_mask, s_misc, s_scan, s_hist, s_ck, gh, a.hcopies);
+        select_spread(a, rs, t, nblk, c, s_mask, s_misc, s_scan, s_hist, s_ck, gh);
         return;
     }
     s_mask[tid] = 0u, s_mask[tid + kQsaThreads] = 0u;  // the chunk's first-digit counts
@@ -780,6 +933,11 @@ static int select_kr(int nmax) {
     return 0;
 }
 
+int qsa_select_tokens(int nmax) {
+    const int kr = select_kr(nmax);
+    return kr >= 64 || kr == 0 ? kQsaCandTokens : 1 << 30;  // the two-launch form hands candidates over
+}
+
 // Largest indexer width the host accepts (heads x dims); the select's dynamic LDS grows with it.
 constexpr int kQsaMaxHeadDims = 8192;
 
@@ -810,15 +968,15 @@ static hipError_t launch_select_dt(const QsaSelectArgs& a, int kr, size_t shm, d
         case 16: return launch_select_kr<IN_DT, 16, 0>(a, shm, grid, s);
         case 32: return launch_select_kr<IN_DT, 32, 0>(a, shm, grid, s);
         default: {
-            // many blocks: scoring (256 blocks a workgroup), then a select launch of one workgroup a token
-            // (which does not append)
+            // many blocks: scoring (256 blocks a workgroup), then the spread selection launch (4,096 blocks a
+            // workgroup; it does not append)
             constexpr int CH1 = 4 * kQsaChunk;
             const int nmax = (a.pos + a.n) / a.CR;
+            if (a.n > kQsaCandTokens || a.cand == nullptr || a.cand_n == nullptr) return hipErrorInvalidValue;
             if (hipError_t e = launch_select_kr<IN_DT, 8, 1, CH1>(a, shm, dim3((nmax + CH1 - 1) / CH1, grid.y), s)) return e;
             QsaSelectArgs b = a;
             b.raw = nullptr;
-            const dim3 g1(1, grid.y);
-            return kr == 64 ? launch_select_kr<IN_DT, 64, 2>(b, shm, g1, s) : launch_select_kr<IN_DT, 0, 2>(b, shm, g1, s);
+            return launch_select_kr<IN_DT, 0, 2, kQsaSelBlocks>(b, shm, dim3((nmax + kQsaSelBlocks - 1) / kQsaSelBlocks, grid.y), s);
         }
     }
 }

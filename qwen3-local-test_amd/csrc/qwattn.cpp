@@ -38,6 +38,8 @@ struct qwattn_ctx {
     int* qsa_cnt = nullptr;      // QSA select: per-token arrival counters [max_tokens], zero between launches
     unsigned* qsa_hist = nullptr; // QSA select: first-digit histograms [qsa_hist_n][2048], zero between launches
     int qsa_hist_n = 0;           // histograms in qsa_hist: a select launch holds that many tokens x copies
+    unsigned* qsa_cand = nullptr; // QSA select, two-launch form: candidates handed to the last workgroup
+    int* qsa_cand_n = nullptr;    //   and their counts (qw::kQsaCandTokens tokens)
     int split_rows = 0;          // rows the split kernel handles: 32 * NKV (n * G <= 32)
     int last_splits = 0;         // split count of the last qwattn_attend_partial / qwattn_decode_partial
     int last_n = 0;
@@ -261,6 +263,9 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
               hipMalloc(&c->qsa_scores, kQsaScoreBytes) == hipSuccess &&
               hipMalloc(&c->qsa_cnt, sizeof(int) * cfg->max_tokens) == hipSuccess &&
               hipMalloc(&c->qsa_hist, sizeof(unsigned) * 2048 * hist_tokens) == hipSuccess &&
+              hipMalloc(&c->qsa_cand, sizeof(unsigned) * qw::kQsaCandTokens * qw::kQsaSelWgMax * 2 * qw::kQsaCandWg) ==
+                  hipSuccess &&
+              hipMalloc(&c->qsa_cand_n, sizeof(int) * qw::kQsaCandTokens * qw::kQsaSelWgMax) == hipSuccess &&
               hipHostMalloc(&c->wait_err_host, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
               hipHostGetDevicePointer((void**)&c->wait_err_dev, c->wait_err_host, 0) == hipSuccess;
     if (!ok) {
@@ -292,7 +297,7 @@ int qwattn_destroy(qwattn_ctx* c) {
     (void)hipDeviceSynchronize();
     for (void* p : {(void*)c->inv_freq, (void*)c->rope, (void*)c->part_o, (void*)c->part_ml, (void*)c->ep, (void*)c->rec,
                     (void*)c->q32, c->q16, (void*)c->pf_part, (void*)c->pf_cnt, (void*)c->qsa_scores, (void*)c->qsa_cnt,
-                    (void*)c->qsa_hist})
+                    (void*)c->qsa_hist, (void*)c->qsa_cand, (void*)c->qsa_cand_n})
         if (p) (void)hipFree(p);
     for (auto* p : c->kc) (void)hipFree(p);
     for (auto* p : c->vc) (void)hipFree(p);
@@ -945,13 +950,13 @@ int qwattn_qsa_select(qwattn_ctx* c, void* stream, const void* iq, int in_dtype,
     if (int rc = take_wait_error(c)) return rc;
     DeviceGuard dg(c->device);
     const int stride = (std::max(1, nmax) + 3) & ~3;  // score rows padded to whole 16-byte loads
-    const int per = (int)std::min<size_t>(c->qsa_hist_n,
+    const int per = (int)std::min<size_t>(std::min(c->qsa_hist_n, qw::qsa_select_tokens(nmax)),
                                           std::max<size_t>(1, kQsaScoreBytes / ((size_t)stride * sizeof(float))));
     for (int t0 = 0; t0 < n; t0 += per) {
         const int nt = std::min(per, n - t0);
         qw::QsaSelectArgs a{(const char*)iq + (size_t)t0 * idx_heads * idx_dim * (in_dtype == QWATTN_F32 ? 4 : 2),
-                            q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, c->qsa_hist,
-                            mask ? mask + (size_t)t0 * mask_words : nullptr,
+                            q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, c->qsa_hist, c->qsa_cand,
+                            c->qsa_cand_n, mask ? mask + (size_t)t0 * mask_words : nullptr,
                             key_bits ? key_bits + (size_t)t0 * kb_words : nullptr, nullptr, nullptr, mask_words,
                             kb_words, stride, pos + t0, nt, idx_heads, idx_dim, cr, budget / cr, g.rope_dim,
                             g.rms_eps, qsa_hist_copies(c, nt)};
@@ -970,7 +975,7 @@ int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq
                     pos + n, cap, c->cfg.max_ctx);
     const int nmax = (pos + n) / std::max(cr, 1);
     const int stride = (std::max(1, nmax) + 3) & ~3;  // score rows padded to whole 16-byte loads
-    const int per = (int)std::min<size_t>(c->qsa_hist_n,
+    const int per = (int)std::min<size_t>(std::min(c->qsa_hist_n, qw::qsa_select_tokens(nmax)),
                                           std::max<size_t>(1, kQsaScoreBytes / ((size_t)stride * sizeof(float))));
     if (cr < 2 || nmax != pos / cr || n > per) {
         // a block completes (or the tokens take several select launches): the pooling launch, then the select
@@ -1000,9 +1005,9 @@ int qwattn_qsa_index(qwattn_ctx* c, void* stream, const void* ik, const void* iq
         return fail(c, QWATTN_EINVAL, "qwattn_qsa_index: kb_words %d < %d keys / 32", kb_words, pos + n);
     if (int rc = take_wait_error(c)) return rc;
     DeviceGuard dg(c->device);
-    qw::QsaSelectArgs a{iq, q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, c->qsa_hist, mask, key_bits, ik,
-                        raw, mask_words, kb_words, stride, pos, n, idx_heads, idx_dim, cr, budget / cr,
-                        g.rope_dim, g.rms_eps, qsa_hist_copies(c, n)};
+    qw::QsaSelectArgs a{iq, q_gamma, c->rope, pooled, c->qsa_scores, c->qsa_cnt, c->qsa_hist, c->qsa_cand,
+                        c->qsa_cand_n, mask, key_bits, ik, raw, mask_words, kb_words, stride, pos, n, idx_heads,
+                        idx_dim, cr, budget / cr, g.rope_dim, g.rms_eps, qsa_hist_copies(c, n)};
     HIP_TRY(c, qw::launch_qsa_select(a, in_dtype, (hipStream_t)stream));
     return QWATTN_OK;
 }
