@@ -80,21 +80,26 @@ CASES = {
     "cr4_256k": (QsaShape(1, 64, 4, 1024, 64), 262152, [(0, 262144, 0), (262144, 1, 1), (262145, 2, 1)], "f32"),
     # zero indexer queries: every score is 0, the lowest block ids win (no histogram pass at all)
     "zeros": (QsaShape(2, 128, 4, 256, 64), 8200, [(0, 8000, 0), (8000, 2, 1), (8002, 1, 1)], "f32"),
-    # the same past 32,768 blocks (scoring launch + selection launch)
+    # the same at 1,000 blocks (scoring and selection in one launch) and past 32,768 (a scoring launch, then
+    # the spread selection launch)
+    "zeros_cr8": (QsaShape(2, 128, 8, 8 * 64, 64), 8200, [(0, 8000, 0), (8000, 2, 1)], "f32"),
     "zeros_cr2_64k": (QsaShape(2, 64, 2, 512, 64), 65560, [(0, 65544, 0), (65544, 2, 1)], "f32"),
     # one indexer head: about half the blocks score exactly 0 (a negative dot), and the budget reaches into
-    # them, so the threshold is 0 and only part of its ties are taken, lowest block ids first; in the one-launch
-    # select, the two-launch select and the one that reads the scores from memory
+    # them, so the threshold is 0 and only part of its ties are taken, lowest block ids first; in the
+    # one-workgroup select, the one-launch select, the two-launch select and the one that reads the scores
+    # from memory
+    "halfzero_cr8": (QsaShape(1, 64, 8, 8 * 600, 64), 8200, [(0, 8000, 0), (8000, 2, 1)], "f32"),
     "halfzero_cr4_8k": (QsaShape(1, 64, 4, 4 * 1500, 64), 8200, [(0, 8000, 0), (8000, 2, 1)], "f32"),
     "halfzero_cr2_64k": (QsaShape(1, 64, 2, 2 * 24000, 64), 65560, [(0, 65544, 0), (65544, 2, 1)], "f32"),
     "halfzero_long_cr2": (QsaShape(1, 64, 2, 2 * 70000, 64), 262144, [(0, 262000, 0), (262000, 2, 1)], "f32"),
     # raw keys repeating every `period` blocks and queries zero on the rotated dims: every score value recurs
     # on many blocks, exactly, so the threshold's ties are cut by block id among the compacted candidates
+    "ties_cr8": (QsaShape(2, 128, 8, 8 * 100, 64), 8200, [(0, 8000, 0), (8000, 2, 1)], "f32"),
     "ties_cr4_8k": (QsaShape(2, 128, 4, 4 * 300, 64), 8200, [(0, 8000, 0), (8000, 2, 1), (8002, 1, 1)], "f32"),
     "ties_cr2_64k": (QsaShape(1, 128, 2, 2 * 5000, 64), 65560, [(0, 65544, 0), (65544, 2, 1)], "f32"),
     "ties_long_cr2": (QsaShape(1, 128, 2, 2 * 9000, 64), 262144, [(0, 262000, 0), (262000, 2, 1)], "f32"),
 }
-TIE_PERIOD = {"ties_cr4_8k": 37, "ties_cr2_64k": 101, "ties_long_cr2": 1009}  # blocks
+TIE_PERIOD = {"ties_cr8": 37, "ties_cr4_8k": 37, "ties_cr2_64k": 101, "ties_long_cr2": 1009}  # blocks
 
 
 @pytest.mark.parametrize("name", list(CASES))
