@@ -105,9 +105,13 @@ class Workload:
         self.kn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.split = n * (NH // NKV) <= 32 and n <= 8
         # decode (up to 8 query rows per KV head): the combine runs inside the attend launch (its combining
-        # workgroups, one per output row, on at most half the CUs)
-        self.one_launch = (self.split and n * (NH // NKV) <= 8
-                           and 2 * n * NH <= torch.cuda.get_device_properties(0).multi_processor_count)
+        # workgroups, one per output row, on at most half the CUs); verify (more rows, 16-row slices): the
+        # slices' last chunks combine, in the same launch, when a slice has at least as many chunks as rows
+        # (the automatic split count gives 64 at 32K)
+        rows = n * (NH // NKV)
+        self.one_launch = self.split and (
+            (rows <= 8 and 2 * n * NH <= torch.cuda.get_device_properties(0).multi_processor_count)
+            or (rows > 8 and (n_split == 0 or n_split >= min(rows, 16))))
         # prefill: the kernel normalizes the query rows itself (the layer entry point's path for this
         # rope width), so no query buffer
         self.q = None
@@ -441,7 +445,11 @@ def run_workload(wl, steps, warmup, graph):
                   "splits": wl.used, "visible_keys": vis, "streamed_tile_keys": tile_keys,
                   "indexer": f"{wl.IH} heads x {wl.ID} dims, blocks of {wl.CR}, budget {wl.BUDGET}"})
     elif wl.split:
-        if wl.one_launch:
+        if wl.one_launch and wl.n * (NH // NKV) > 8:
+            r.update({"kernel": "k_decode (fused norm+rope+append+split attend, the 16-row slices' last chunks "
+                                "combining: one launch)",
+                      "us_main_each_event": statistics.mean(k_first), "splits": wl.used})
+        elif wl.one_launch:
             r.update({"kernel": "k_decode_ld (fused norm+rope+append+split attend+combine, one launch)",
                       "us_main_each_event": statistics.mean(k_first), "splits": wl.used})
         else:

@@ -178,17 +178,18 @@ int qwattn_decode_partial(qwattn_ctx* ctx, void* stream, const void* qg, const v
 
 /* All three of the reference's decode dispatches (src/qwen4_vk.cpp:968-992: qk_norm_rope,
  * attention, attn_combine): qwattn_decode_partial followed, inside the same kernel, by the log-sum-exp
- * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. Combining workgroups, one per
- * output row and first in the grid, merge the split partials as their records (in the context, tagged
- * with a per-launch epoch) arrive; nothing needs clearing between launches, so the call allocates and
- * clears nothing and can be captured into a graph. Calls on one context must not overlap (one stream,
- * or ordered streams). The merge order is fixed, so the output does not depend on which workgroup
- * finishes first. Same limits as qwattn_decode_partial
- * (n <= 8, n * NH/NKV <= 32: decode and MTP verify); one launch for n * NH/NKV <= 8, above that (verify)
- * the attend launch is followed by the combine launch. `n_split` as in qwattn_attend_partial, except that
- * the one-launch form caps a requested count at the automatic one (one streaming workgroup per CU): its
- * partials never leave the launch, and more parts would only add workgroup prologues and partials to
- * merge. *used_splits (may be NULL) returns the count used. */
+ * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. One workgroup per output row
+ * merges the split partials as their records (in the context, tagged with a per-launch epoch) arrive:
+ * for n * NH/NKV <= 8 (decode) combining workgroups first in the grid, above that (MTP verify) the last
+ * chunks of each 16-row slice once their own partials are out (the combine launch follows instead only
+ * when a slice has fewer chunks than rows). Nothing needs clearing between launches, so the call
+ * allocates and clears nothing and can be captured into a graph. Calls on one context must not overlap
+ * (one stream, or ordered streams). The merge order is fixed, so the output does not depend on which
+ * workgroup finishes first. Same limits as qwattn_decode_partial (n <= 8, n * NH/NKV <= 32: decode and
+ * MTP verify). `n_split` as in qwattn_attend_partial, except that for n * NH/NKV <= 8 a requested count
+ * is capped at the automatic one (one streaming workgroup per CU): its partials never leave the launch,
+ * and more parts would only add workgroup prologues and partials to merge. *used_splits (may be NULL)
+ * returns the count used. */
 int qwattn_decode(qwattn_ctx* ctx, void* stream, const void* qg, const void* k, const void* v,
                   int in_dtype, const float* qn, const float* kn, const float* rope, void* kcache,
                   void* vcache, int kv_cap, float* out, int pos, int n, int n_split, int* used_splits);

@@ -318,6 +318,15 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
     const int r0 = blockIdx.z * RMAX;                  // first query row of this slice
     const int rows = min(RMAX, a.n * G - r0);          // query rows of this workgroup
     const int maxlen = a.pos + a.n;
+    // one-launch verify: the partials are combined in this launch by the slice's last `rows` chunks (see
+    // tail_combine below); the head's launch counter for the epoch tag is read now, before this
+    // workgroup stores its records, so its latency hides behind the whole stream
+    const bool one = FUSED && a.out != nullptr;
+    u32x2 ep_raw = {0u, 0u};
+    if constexpr (FUSED) {
+        const __amdgpu_buffer_rsrc_t rep = __builtin_amdgcn_make_buffer_rsrc(one ? a.ep + kvh : a.ep, (short)0, one ? 8 : 0, 0x00020000);
+        ep_raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rep, 0, 0, kScDevice));
+    }
     int kb, ke;
     split_keys(a, z, maxlen, kb, ke);
     const int ntile_wg = (ke - kb + 31) >> 5;
@@ -643,10 +652,18 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         }
         const int t = (r0 + r) / G, h = kvh * G + (r0 + r) % G;
         const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
-        a.part_ml[row * 2] = M;
-        a.part_ml[row * 2 + 1] = L;
+        if (one) {
+            sM[0][r] = M;  // for the record (wave 0 of every row reads its own row's entry back)
+            sL[0][r] = L;
+        } else {
+            a.part_ml[row * 2] = M;
+            a.part_ml[row * 2 + 1] = L;
+        }
     }
     __syncthreads();
+    // one launch: device-coherent stores (they reach the point every XCD reads from once acknowledged),
+    // so the combining workgroups read them without any cache-wide write-back
+    const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(a.part_o, (short)0, 0x7fffffff, 0x00020000);
     for (int idx = tid; idx < rows * (D / 4); idx += 256) {
         const int r = idx / (D / 4), d = (idx % (D / 4)) * 4;
         f32x4 o = *reinterpret_cast<const f32x4*>(&sO[r * C::OSTRIDE + d]) * sF[0][r];
@@ -654,7 +671,33 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
         for (int w = 1; w < 4; w++) o += *reinterpret_cast<const f32x4*>(&sO[(w * RMAX + r) * C::OSTRIDE + d]) * sF[w][r];
         const int t = (r0 + r) / G, h = kvh * G + (r0 + r) % G;
         const size_t row = ((size_t)t * a.NH + h) * a.n_split + z;
-        *reinterpret_cast<f32x4*>(&a.part_o[row * D + d]) = o;
+        if (one) __builtin_amdgcn_raw_buffer_store_b128(o, rpo, (int)((row * D + d) * 4), 0, kScDevice);
+        else *reinterpret_cast<f32x4*>(&a.part_o[row * D + d]) = o;
+    }
+    if constexpr (FUSED) {
+        if (one) {
+            // the records go out once every o store of the workgroup is acknowledged (the wait counts the
+            // wave's memory operations, the barrier joins the four waves): a record with this launch's
+            // tag is the combiner's guarantee that its row's o is visible device-wide
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            if (tid < rows) {
+                const unsigned long long tag = tag_of(ep_raw, kvh);
+                const int t = (r0 + tid) / G, h = kvh * G + (r0 + tid) % G;
+                const int row = (t * a.NH + h) * a.n_split + z;
+                const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(a.rec, (short)0, 0x7fffffff, 0x00020000);
+                __builtin_amdgcn_raw_buffer_store_b128(f32x4{sM[0][tid], sL[0][tid], __uint_as_float((unsigned)tag), __uint_as_float((unsigned)(tag >> 32))},
+                                                       rr, row * 16, 0, kScDevice);
+            }
+            // the slice's last `rows` chunks (the shortest: the first cr chunks are one block longer) then
+            // combine one output row each. They wait only for chunks of their own slice, which come before
+            // them in the grid's dispatch order, so every wait ends whatever the number of free CUs
+            const int zc = z - (a.n_split - rows);
+            if (zc >= 0) {
+                const int t = (r0 + zc) / G, h = kvh * G + (r0 + zc) % G;
+                combine_row<D, IN_DT>(a, s_u, t * a.NH + h);
+            }
+        }
     }
 }
 
@@ -1179,9 +1222,10 @@ static hipError_t launch_lds(K kern, std::atomic<uint64_t>& raised, dim3 grid, s
 template <int D, int FUSED, int IN_DT>
 static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
-    // the in-launch combine: fused (it needs the gate), at most 8 rows (the 16-row kernel has no
-    // registers left for it), one combining workgroup per output row
-    if (a.out != nullptr && (!FUSED || rows > 8 || a.ncomb != a.n * a.NH || !a.ep || !a.rec))
+    // the in-launch combine: fused (it needs the gate); up to 8 rows on one combining workgroup per output
+    // row, more on the last chunks of each 16-row slice (one row each, so a slice needs that many chunks)
+    if (a.out != nullptr && (!FUSED || (rows > 8 && a.n_split < (rows < 16 ? rows : 16)) || a.ncomb != a.n * a.NH ||
+                             !a.ep || !a.rec))
         return hipErrorInvalidValue;
     if (rows <= 8) {
         static std::atomic<uint64_t> raised{0};

@@ -42,11 +42,12 @@ struct DecodeArgs {
     int cq, cr;           // split z holds the 32-key blocks [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr))
     int n_split;
     float eps, q_scale;   // q_scale = log2(e) / sqrt(D)
-    float* out;           // fused decode with n * NH/NKV <= 8 only: the gated output [n][NH][D], combined in
-                          // the same launch (nullptr: partials only, for a separate combine)
+    float* out;           // fused decode: the gated output [n][NH][D], combined in the same launch (nullptr:
+                          // partials only, for a separate combine)
     unsigned long long* ep;  // with out: per KV head, the launch counter the epochs come from (zero at first)
     float* rec;           // with out: [n*NH][n_split][4] split records (m, l, epoch tag, 0)
-    int ncomb;            // with out: combining workgroups, one per output row (n * NH), first in the grid
+    int ncomb;            // with out: output rows (n * NH), each combined by one workgroup (first in the grid
+                          // up to 8 rows, else the last chunks of each 16-row slice)
     int cap;              // capacity (positions) of the caches kc, vc
     int* err;             // a bounded wait that gives up stores its kWait* code here (nullptr: not reported)
     const unsigned* kbits;  // QSA: per-token key visibility bits [n][kb_words] (nullptr: dense attention)

@@ -158,8 +158,17 @@ struct Split {
 // One launch (attend + combine) for n tokens: up to 8 query rows per KV head (the loader-wave kernel),
 // and the combining workgroups (one per output row, waiting for the streaming ones) on at most half the
 // CUs, so the others always have room to run.
+// Up to 8 query rows: the combine runs in the launch on one combining workgroup per output row, first in
+// the grid, unless those would take more than half the CUs.
 bool one_launch(int n_cu, const qwattn_config& g, int n) {
     return n * (g.n_heads / g.n_kv_heads) <= 8 && 2 * n * g.n_heads <= n_cu;
+}
+
+// More rows (the 16-row slices): the combine runs in the launch when every slice has at least as many
+// chunks as rows, its last chunks combining one row each.
+bool tail_launch(const qwattn_config& g, int n, int S) {
+    const int rows = n * (g.n_heads / g.n_kv_heads);
+    return rows > 8 && S >= std::min(rows, 16);
 }
 
 // reserve: CUs left to the combining workgroups of a one-launch call; more than 8 rows go to the decode
@@ -588,13 +597,14 @@ static int decode_impl(qwattn_ctx* c, const char* fn, void* stream, const void* 
     if (n * G > 32 || n > 8)
         return fail(c, QWATTN_EINVAL, "qwattn_decode: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
                     "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
-    // the combine runs inside the attend launch, in one combining workgroup per output row (first in the
-    // grid), unless those would take more than half the CUs: then the combine kernel follows
+    // the combine runs inside the attend launch (one_launch, tail_launch); otherwise the combine kernel
+    // follows
     const int ncomb = n * g.n_heads;
-    const bool one = one_launch(c->n_cu, g, n);
-    Split sp = pick_split(c, pos + n, n, n_split, one ? ncomb : 0, one);
+    const bool small = one_launch(c->n_cu, g, n);
+    Split sp = pick_split(c, pos + n, n, n_split, small ? ncomb : 0, small);
     qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
     if ((rc = qsa_args(c, fn, kbits, kb_words, pos, n, &sp, &a))) return rc;
+    const bool one = small || tail_launch(g, n, sp.S);
     const int used = sp.S;
     DeviceGuard dg(c->device);
     if (one) a.out = out, a.ep = c->ep, a.rec = c->rec, a.ncomb = ncomb;
@@ -874,8 +884,9 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
     int n_cu = 0;
     if (int rc = scratch_base(device, &base, &n_cu)) return rc;
     const int ncomb = n * g.n_heads;
-    const bool one = one_launch(n_cu, g, n);
-    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, one ? ncomb : 0, one);
+    const bool small = one_launch(n_cu, g, n);
+    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, small ? ncomb : 0, small);
+    const bool one = small || tail_launch(g, n, sp.S);
     const size_t parts = (size_t)ncomb * sp.S;  // split partial rows
     const size_t rec_b = align256(parts * 16), ml_b = align256(parts * 8), o_b = align256(parts * g.head_dim * 4);
     if (kScratchData + rec_b + ml_b + o_b > kScratchBytes)

@@ -307,9 +307,13 @@ ONE_LAUNCH = CASES_FUSED + [
     (TINY_GGUF, 61, 4, 0, "f32"),       # automatic splits of one block each: the new rows straddle two chunks
     (TINY, 63, 2, 0, "bf16"),           # the same with one new row in each chunk
     (QWEN3_NEXT, 16383, 1, 64, "f32"),  # 64 splits of 8 blocks, the new row opening the last block
-    # 9 to 32 rows (qwattn_decode's 16-row-slice kernel and combine kernel): partly filled slices, 8 new
+    # 9 to 32 rows (qwattn_decode's 16-row-slice kernel; the combine on the slices' last chunks when a
+    # slice has at least as many chunks as rows, else the combine kernel): partly filled slices, 8 new
     # rows, one split holding every tile, splits of a single tile that holds new rows
     (TINY, 500, 3, 0, "f32"),           # 12 rows: the second group half full, two idle waves
+    (QWEN3_NEXT, 32768, 4, 0, "bf16"),  # 32 rows in two slices, 64 chunks each
+    (QWEN3_NEXT, 3000, 3, 16, "f32"),   # 24 rows: a full and a half slice, 16 chunks (every chunk of the
+                                        # first slice combines a row)
     (TINY_GGUF, 100, 5, 0, "bf16"),     # 10 rows at D = 256, G = 2
     (D128, 2000, 8, 0, "bf16"),         # 32 rows, 8 new rows across a block boundary
     (QWEN3_NEXT, 5000, 4, 1, "f32"),    # one split: 157 tiles through one ring
@@ -339,16 +343,18 @@ def test_decode_one_launch_parity(qw, oracle, s, pos, n, n_split, dtype):
 
 def test_decode_one_launch_equals_two_launches(qw):
     """The in-launch combine merges what qwattn_combine merges: over a run of calls on one context with
-    changing token counts (decode n=1 on the loader-wave kernel, verify n=4 on two 16-row slices and the
-    combine kernel) and split counts (fewer splits than combine units, one split, many; the two-launch call
-    is given the first call's count), each output matches decode_partial + combine to fp32 rounding (the
-    two merges visit the splits in different orders).
+    changing token counts (decode n=1 on the loader-wave kernel, verify n=4 on two 16-row slices, combined
+    by the slices' last chunks with 16 chunks or more, else by the combine kernel) and split counts (fewer
+    splits than combine units, one split, many; the two-launch call is given the first call's count), each
+    output matches decode_partial + combine to fp32 rounding (the two merges visit the splits in different
+    orders).
     The one-launch calls use the context's ready flags with changing split counts: a flag left by one
     call that passed for a later call's epoch would let its combiners merge stale partials."""
     s, pos = QWEN3_NEXT, 3000
     cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, 4, "f32", 77)
     ctx = make_ctx(qw, s, max_ctx=cap)
-    for n, n_split in [(1, 3), (4, 0), (1, 0), (4, 1), (1, 1), (4, 7), (1, 93), (4, 93), (1, 0), (2, 2)]:
+    for n, n_split in [(1, 3), (4, 0), (1, 0), (4, 1), (1, 1), (4, 7), (1, 93), (4, 93), (1, 0), (2, 2), (4, 16),
+                       (3, 16), (4, 0)]:
         print(f"one-launch vs two-launch n={n} splits={n_split}", flush=True)
         out = torch.full((n, s.NH, s.D), float("nan"), device=DEV)
         used = ctx.decode(qg_d, k_d, v_d, qn_d, kn_d, ctx.rope_table(), kc, vc, cap, out, pos, n, n_split)
@@ -360,11 +366,12 @@ def test_decode_one_launch_equals_two_launches(qw):
         assert np.abs(host(out) - host(out2)).max() <= 2e-6, f"splits={used}"
 
 
-def test_decode_one_launch_graph_replays(qw):
-    """Captured into a HIP graph, the one-launch decode gives the eager result on every replay, with
-    eager work and synchronizations in between (each launch advances its own epoch inside the kernel;
-    nothing is cleared by a memset node)."""
-    s, pos, n = QWEN3_NEXT, 8190, 1
+@pytest.mark.parametrize("n", [1, 4])
+def test_decode_one_launch_graph_replays(qw, n):
+    """Captured into a HIP graph, the one-launch decode (n = 1: combining workgroups; n = 4: the slices'
+    last chunks combine) gives the eager result on every replay, with eager work and synchronizations in
+    between (each launch advances its own epoch inside the kernel; nothing is cleared by a memset node)."""
+    s, pos = QWEN3_NEXT, 8190
     cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 91)
     ctx = make_ctx(qw, s, max_ctx=cap)
     rope = ctx.rope_table()
@@ -440,13 +447,14 @@ def test_decode_256k_peaked_keys(qw, oracle):
         assert_parity(o, ref, f"256K {name}")
 
 
-def test_decode_wait_timeout_is_reported(qw):
+@pytest.mark.parametrize("n", [1, 4])
+def test_decode_wait_timeout_is_reported(qw, n):
     """A bounded in-kernel wait that gives up is an error, not silently wrong output: with the test hook
-    skewing the epoch the in-launch combine waits for, no split's ready flag ever matches, the poller
-    gives up after 64 polls, every kernel still ends, and the context reports QWATTN_ETIMEOUT once
-    (through qwattn_sync_status, or the next call). With the hook off, the context computes correctly
-    again."""
-    s, pos, n = QWEN3_NEXT, 3000, 1
+    skewing the epoch the in-launch combine waits for (n = 1: combining workgroups; n = 4: the slices'
+    last chunks), no split's ready flag ever matches, the poller gives up after 64 polls, every kernel
+    still ends, and the context reports QWATTN_ETIMEOUT once (through qwattn_sync_status, or the next
+    call). With the hook off, the context computes correctly again."""
+    s, pos = QWEN3_NEXT, 3000
     cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 123)
     ctx = make_ctx(qw, s, max_ctx=cap)
     rope = ctx.rope_table()

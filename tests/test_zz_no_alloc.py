@@ -1,7 +1,7 @@
 """qwattn_decode_noalloc (no context, library-static scratch) computes exactly what qwattn_decode
 computes: the same kernels, split counts and merge order, so the outputs and the appended cache rows are
 bit-identical. Two calls in a row, the second with a smaller input; the one-launch path (n = 1) and the
-verify path (n = 4: the 16-row-slice kernel and the combine kernel) both run."""
+verify path (n = 4: the 16-row-slice kernel, its slices' last chunks combining) both run."""
 import numpy as np
 import pytest
 import torch
