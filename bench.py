@@ -104,14 +104,11 @@ class Workload:
         self.qn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.kn = 0.1 * torch.randn(D, device="cuda", generator=g)
         self.split = n * (NH // NKV) <= 32 and n <= 8
-        # decode (up to 8 query rows per KV head): the combine runs inside the attend launch (its combining
-        # workgroups, one per output row, on at most half the CUs); verify (more rows, 16-row slices): the
-        # slices' last chunks combine, in the same launch, when a slice has at least as many chunks as rows
-        # (the automatic split count gives 64 at 32K)
+        # decode and verify: the combine runs inside the attend launch, on the last chunks of each KV head
+        # (up to 8 query rows) or 16-row slice, when each has at least as many chunks as rows (the
+        # automatic split count gives 128 at 32K for decode, 64 for the verify's slices)
         rows = n * (NH // NKV)
-        self.one_launch = self.split and (
-            (rows <= 8 and 2 * n * NH <= torch.cuda.get_device_properties(0).multi_processor_count)
-            or (rows > 8 and (n_split == 0 or n_split >= min(rows, 16))))
+        self.one_launch = self.split and (n_split == 0 or n_split >= min(rows, 16))
         # prefill: the kernel normalizes the query rows itself (the layer entry point's path for this
         # rope width), so no query buffer
         self.q = None
@@ -450,7 +447,8 @@ def run_workload(wl, steps, warmup, graph):
                                 "combining: one launch)",
                       "us_main_each_event": statistics.mean(k_first), "splits": wl.used})
         elif wl.one_launch:
-            r.update({"kernel": "k_decode_ld (fused norm+rope+append+split attend+combine, one launch)",
+            r.update({"kernel": "k_decode_ld (fused norm+rope+append+split attend, the KV heads' last chunks "
+                                "combining: one launch)",
                       "us_main_each_event": statistics.mean(k_first), "splits": wl.used})
         else:
             r.update({"kernel": "k_decode (fused norm+rope+append+split attend)",
@@ -694,8 +692,8 @@ def main():
     }
     if head:
         line["roofline"] = {"bound": "hbm",
-                            "kernel": f"k_decode_ld<256,1,0> (one launch: {NH} combining + {head['splits']}x{NKV} "
-                                      "streaming workgroups)",
+                            "kernel": f"k_decode_ld<256,1,0> (one launch: {head['splits']}x{NKV} streaming "
+                                      f"workgroups, the last {NH // NKV} of each KV head combining one row each)",
                             "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                             "frac": round(head["frac_hbm_kernel"], 4),

@@ -178,11 +178,11 @@ int qwattn_decode_partial(qwattn_ctx* ctx, void* stream, const void* qg, const v
 
 /* All three of the reference's decode dispatches (src/qwen4_vk.cpp:968-992: qk_norm_rope,
  * attention, attn_combine): qwattn_decode_partial followed, inside the same kernel, by the log-sum-exp
- * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. One workgroup per output row
- * merges the split partials as their records (in the context, tagged with a per-launch epoch) arrive:
- * for n * NH/NKV <= 8 (decode) combining workgroups first in the grid, above that (MTP verify) the last
- * chunks of each 16-row slice once their own partials are out (the combine launch follows instead only
- * when a slice has fewer chunks than rows). Nothing needs clearing between launches, so the call
+ * combine and the sigmoid gate of qwattn_combine, writing out[n][NH][D]. One workgroup per output row,
+ * one of the last chunks of its KV head (n * NH/NKV <= 8: decode) or 16-row slice (above: MTP verify) once
+ * its own partials are out, merges the split partials as their records (in the context, tagged with a
+ * per-launch epoch) arrive; the combine launch follows instead only when a head or slice has fewer chunks
+ * than rows. Nothing needs clearing between launches, so the call
  * allocates and clears nothing and can be captured into a graph. Calls on one context must not overlap
  * (one stream, or ordered streams). The merge order is fixed, so the output does not depend on which
  * workgroup finishes first. Same limits as qwattn_decode_partial (n <= 8, n * NH/NKV <= 32: decode and

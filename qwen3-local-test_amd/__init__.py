@@ -275,7 +275,8 @@ class Attention:
         return used.value
 
     def decode(self, qg, k, v, qn, kn, rope, kcache, vcache, kv_cap, out, pos, n, n_split=0, stream=None):
-        """Norm + rope + append + split-KV attend + combine and gate in one launch (n * NH/NKV <= 8);
+        """Norm + rope + append + split-KV attend + combine and gate in one launch (n <= 8, n * NH/NKV <= 32;
+        the combine kernel follows only when a KV head or 16-row slice gets fewer splits than rows);
         returns the split count."""
         used = ctypes.c_int()
         self._check(self.lib.qwattn_decode(

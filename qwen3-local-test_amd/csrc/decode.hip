@@ -180,9 +180,10 @@ __device__ __forceinline__ void merge_batch(float& M, float& L, f32x4& O, const 
     M = mx;
 }
 
-// In-launch log-sum-exp combine of the one-launch decode (attn_combine.comp:13-29): the workgroups
-// first in the grid, one per output row (t, h), each merge that row's split partials while the others
-// stream K/V. A streaming workgroup stores its rows' unnormalized o[D] (device-coherent stores), waits
+// In-launch log-sum-exp combine of the one-launch decode (attn_combine.comp:13-29): one workgroup per
+// output row (t, h), one of the last chunks of its KV head or 16-row slice once its own partials are out,
+// merges that row's split partials as they arrive. A streaming workgroup stores its rows' unnormalized
+// o[D] (device-coherent stores), waits
 // for them to be acknowledged, then stores each row's record (m, l, 64-bit tag): a record carrying this
 // launch's tag guarantees the row's o is visible. The combining workgroup takes the splits in windows of
 // kCombSlots: wave w owns the kCombGroup splits [wb + 32 w, wb + 32 w + 32) of window wb, lane j < 32
@@ -193,8 +194,8 @@ __device__ __forceinline__ void merge_batch(float& M, float& L, f32x4& O, const 
 // then meet in LDS and merge into the running (M, L, O) in group order — a fixed order, so the result
 // does not depend on which split arrives first. Splits with l = 0 are skipped. The epoch: see
 // kEpochStep. Every wait is bounded (a.spin_max polling rounds); a combiner that gives up reports
-// kWaitCombineFlags and merges whatever its registers hold. Combiners wait only for streaming
-// workgroups, which never wait, and the host keeps them at half the CUs or below, so every wait ends.
+// kWaitCombineFlags and merges whatever its registers hold. At most one combiner per output row waits
+// (8 per KV head, 16 per slice), so every wait ends while more CUs than that are free to the launch.
 template <int D, int IN_DT>
 __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* smem, int r) {
     constexpr int NS = kCombSlots, GS = kCombGroup, DL = D / 64;
@@ -690,8 +691,8 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
                                                        rr, row * 16, 0, kScDevice);
             }
             // the slice's last `rows` chunks (the shortest: the first cr chunks are one block longer) then
-            // combine one output row each. They wait only for chunks of their own slice, which come before
-            // them in the grid's dispatch order, so every wait ends whatever the number of free CUs
+            // combine one output row each. A combiner waits for the other chunks of its slice; at most 16
+            // per slice wait, so every wait ends while more CUs than waiting combiners are free to the launch
             const int zc = z - (a.n_split - rows);
             if (zc >= 0) {
                 const int t = (r0 + zc) / G, h = kvh * G + (r0 + zc) % G;
@@ -742,16 +743,10 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = lane & 15, g = lane >> 4;
-    // one-launch decode: the first a.ncomb workgroups of the grid combine, one output row each
+    // one-launch decode: each KV head's last chunks combine one output row each once their own partials
+    // are out (the end of this kernel)
     const bool one = FUSED && a.out != nullptr;
-    if constexpr (FUSED) {
-        if (one && (int)blockIdx.x < a.ncomb) {
-            combine_row<D, IN_DT>(a, smem, blockIdx.x);
-            return;
-        }
-    }
-    const int sidx = blockIdx.x - (one ? a.ncomb : 0);
-    const int kvh = sidx / a.n_split, z = sidx - kvh * a.n_split;
+    const int kvh = blockIdx.x / a.n_split, z = blockIdx.x - kvh * a.n_split;
     const int G = a.NH / a.NKV;
     const int rows = min(RMAX, a.n * G);
     const int maxlen = a.pos + a.n;
@@ -1191,6 +1186,16 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             __builtin_amdgcn_raw_buffer_store_b128(f32x4{m_run, l_run, __uint_as_float((unsigned)tag), __uint_as_float((unsigned)(tag >> 32))},
                                                    rr, row * 16, 0, kScDevice);
         }
+        if constexpr (FUSED) {
+            // the head's last `rows` chunks then combine one output row each (the ring is dead: the merge
+            // above was its last use). A combiner waits for the other chunks of its head; at most 8 per head
+            // wait, so every wait ends while more than 8 x NKV CUs are free to the launch
+            const int zc = z - (S - rows);
+            if (zc >= 0) {
+                __syncthreads();
+                combine_row<D, IN_DT>(a, smem, (zc / G) * a.NH + kvh * G + zc % G);
+            }
+        }
     }
 }
 
@@ -1222,15 +1227,13 @@ static hipError_t launch_lds(K kern, std::atomic<uint64_t>& raised, dim3 grid, s
 template <int D, int FUSED, int IN_DT>
 static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
-    // the in-launch combine: fused (it needs the gate); up to 8 rows on one combining workgroup per output
-    // row, more on the last chunks of each 16-row slice (one row each, so a slice needs that many chunks)
-    if (a.out != nullptr && (!FUSED || (rows > 8 && a.n_split < (rows < 16 ? rows : 16)) || a.ncomb != a.n * a.NH ||
-                             !a.ep || !a.rec))
+    // the in-launch combine: fused (it needs the gate), on the last chunks of each KV head (up to 8 rows)
+    // or 16-row slice, one output row each, so a head / slice needs that many chunks
+    if (a.out != nullptr && (!FUSED || a.n_split < (rows < 16 ? rows : 16) || a.ncomb != a.n * a.NH || !a.ep || !a.rec))
         return hipErrorInvalidValue;
     if (rows <= 8) {
         static std::atomic<uint64_t> raised{0};
-        const int ncomb = a.out != nullptr ? a.ncomb : 0;
-        const dim3 grid(ncomb + a.n_split * a.NKV);
+        const dim3 grid(a.n_split * a.NKV);
         if (a.kbits) {
             static std::atomic<uint64_t> raised_q{0};
             return launch_lds(k_decode_ld<D, FUSED, IN_DT, 1>, raised_q, grid, decode_ld_lds<D, 1>(), a, s);

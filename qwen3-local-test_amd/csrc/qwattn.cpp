@@ -146,46 +146,36 @@ int check_call(qwattn_ctx* c, int pos, int n, int kv_cap) {
 // [z*cq + min(z, cr), (z+1)*cq + min(z+1, cr)) with cq = nb / S, cr = nb % S (the first cr chunks one block
 // longer). A requested count n_split > 0 is used as given (the reference's 64, src/qwen4_vk.cpp:974-978,
 // or 1,024 at 256K), capped at max_splits and at nb: a part holds at least one block. n_split = 0 picks
-// one workgroup per CU: (CUs - `reserve`, the one-launch decode's combining workgroups) / (NKV x the
-// decode kernel's 16-row slices) parts. `fill_cap` (the one-launch decode, whose partials never leave the
-// launch) also caps a requested count at that number: more parts than streaming workgroups that fit
-// the CUs at once only add workgroup prologues and partials to merge, and the output is the same up to
-// fp32 rounding.
+// one workgroup per CU: CUs / (NKV x the decode kernel's 16-row slices) parts. `fill_cap` (the
+// one-launch decode up to 8 rows, whose partials never leave the launch) also caps a requested count at
+// that number: more parts than streaming workgroups that fit the CUs at once only add workgroup
+// prologues and partials to merge, and the output is the same up to fp32 rounding.
 struct Split {
     int S, cq, cr;
 };
 
-// One launch (attend + combine) for n tokens: up to 8 query rows per KV head (the loader-wave kernel),
-// and the combining workgroups (one per output row, waiting for the streaming ones) on at most half the
-// CUs, so the others always have room to run.
-// Up to 8 query rows: the combine runs in the launch on one combining workgroup per output row, first in
-// the grid, unless those would take more than half the CUs.
-bool one_launch(int n_cu, const qwattn_config& g, int n) {
-    return n * (g.n_heads / g.n_kv_heads) <= 8 && 2 * n * g.n_heads <= n_cu;
-}
-
-// More rows (the 16-row slices): the combine runs in the launch when every slice has at least as many
-// chunks as rows, its last chunks combining one row each.
+// The one-launch decode combines in the launch on the last chunks of each KV head (up to 8 query rows)
+// or 16-row slice (more rows), one output row each, once their own partials are out: every CU streams
+// (1,024 blocks at 32K split evenly over 128 chunks a head). This needs at least as many chunks as rows
+// per head / slice; otherwise the combine kernel follows.
 bool tail_launch(const qwattn_config& g, int n, int S) {
     const int rows = n * (g.n_heads / g.n_kv_heads);
-    return rows > 8 && S >= std::min(rows, 16);
+    return S >= std::min(rows, 16);
 }
 
-// reserve: CUs left to the combining workgroups of a one-launch call; more than 8 rows go to the decode
-// kernel's 16-row slices (grid.z)
-Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, int reserve = 0,
-                 bool fill_cap = false) {
+// more than 8 rows go to the decode kernel's 16-row slices (grid.z)
+Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, bool fill_cap = false) {
     const int nb = (maxlen + 31) / 32;
     const int rows = n * (g.n_heads / g.n_kv_heads);
     const int slices = rows <= 8 ? 1 : (rows + 15) / 16;
-    const int fill = std::max(1, (n_cu - reserve) / (g.n_kv_heads * slices));
+    const int fill = std::max(1, n_cu / (g.n_kv_heads * slices));
     int S = n_split > 0 ? (fill_cap ? std::min(n_split, fill) : n_split) : fill;
     S = std::max(1, std::min({S, g.max_splits, nb}));
     return Split{S, nb / S, nb % S};
 }
 
-Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, int reserve = 0, bool fill_cap = false) {
-    return pick_split(c->n_cu, c->cfg, maxlen, n, n_split, reserve, fill_cap);
+Split pick_split(const qwattn_ctx* c, int maxlen, int n, int n_split, bool fill_cap = false) {
+    return pick_split(c->n_cu, c->cfg, maxlen, n, n_split, fill_cap);
 }
 
 // Arguments of the decode kernels: shape and split (partials and wait settings: decode_args below).
@@ -597,14 +587,14 @@ static int decode_impl(qwattn_ctx* c, const char* fn, void* stream, const void* 
     if (n * G > 32 || n > 8)
         return fail(c, QWATTN_EINVAL, "qwattn_decode: n = %d tokens (n * NH/NKV = %d) exceeds the fused decode "
                     "kernel (n <= 8 and n * NH/NKV <= 32)", n, n * G);
-    // the combine runs inside the attend launch (one_launch, tail_launch); otherwise the combine kernel
-    // follows
+    // the combine runs inside the attend launch (tail_launch); otherwise the combine kernel follows. Up to 8
+    // rows a requested split count is capped at one streaming workgroup per CU: its partials never leave
+    // the launch, and more parts would only add workgroup prologues and partials to merge
     const int ncomb = n * g.n_heads;
-    const bool small = one_launch(c->n_cu, g, n);
-    Split sp = pick_split(c, pos + n, n, n_split, small ? ncomb : 0, small);
+    Split sp = pick_split(c, pos + n, n, n_split, n * G <= 8);
     qw::DecodeArgs a = decode_args(c, qg, k, v, qn, kn, rope ? rope : c->rope, kcache, vcache, kv_cap, pos, n, sp);
     if ((rc = qsa_args(c, fn, kbits, kb_words, pos, n, &sp, &a))) return rc;
-    const bool one = small || tail_launch(g, n, sp.S);
+    const bool one = tail_launch(g, n, sp.S);
     const int used = sp.S;
     DeviceGuard dg(c->device);
     if (one) a.out = out, a.ep = c->ep, a.rec = c->rec, a.ncomb = ncomb;
@@ -884,9 +874,8 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
     int n_cu = 0;
     if (int rc = scratch_base(device, &base, &n_cu)) return rc;
     const int ncomb = n * g.n_heads;
-    const bool small = one_launch(n_cu, g, n);
-    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, small ? ncomb : 0, small);
-    const bool one = small || tail_launch(g, n, sp.S);
+    const Split sp = pick_split(n_cu, g, pos + n, n, n_split, n * G <= 8);
+    const bool one = tail_launch(g, n, sp.S);
     const size_t parts = (size_t)ncomb * sp.S;  // split partial rows
     const size_t rec_b = align256(parts * 16), ml_b = align256(parts * 8), o_b = align256(parts * g.head_dim * 4);
     if (kScratchData + rec_b + ml_b + o_b > kScratchBytes)

@@ -368,9 +368,10 @@ def test_decode_one_launch_equals_two_launches(qw):
 
 @pytest.mark.parametrize("n", [1, 4])
 def test_decode_one_launch_graph_replays(qw, n):
-    """Captured into a HIP graph, the one-launch decode (n = 1: combining workgroups; n = 4: the slices'
-    last chunks combine) gives the eager result on every replay, with eager work and synchronizations in
-    between (each launch advances its own epoch inside the kernel; nothing is cleared by a memset node)."""
+    """Captured into a HIP graph, the one-launch decode (n = 1: the KV heads' last chunks combine; n = 4:
+    the 16-row slices' last chunks) gives the eager result on every replay, with eager work and
+    synchronizations in between (each launch advances its own epoch inside the kernel; nothing is cleared
+    by a memset node)."""
     s, pos = QWEN3_NEXT, 8190
     cap, _, _, qg_d, k_d, v_d, qn_d, kn_d, kc, vc = _fused_setup(qw, s, pos, n, "f32", 91)
     ctx = make_ctx(qw, s, max_ctx=cap)
@@ -450,8 +451,8 @@ def test_decode_256k_peaked_keys(qw, oracle):
 @pytest.mark.parametrize("n", [1, 4])
 def test_decode_wait_timeout_is_reported(qw, n):
     """A bounded in-kernel wait that gives up is an error, not silently wrong output: with the test hook
-    skewing the epoch the in-launch combine waits for (n = 1: combining workgroups; n = 4: the slices'
-    last chunks), no split's ready flag ever matches, the poller gives up after 64 polls, every kernel
+    skewing the epoch the in-launch combine waits for (n = 1: the KV heads' last chunks; n = 4: the 16-row
+    slices' last chunks), no split's ready flag ever matches, the poller gives up after 64 polls, every kernel
     still ends, and the context reports QWATTN_ETIMEOUT once (through qwattn_sync_status, or the next
     call). With the hook off, the context computes correctly again."""
     s, pos = QWEN3_NEXT, 3000
