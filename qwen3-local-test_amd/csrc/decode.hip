@@ -181,51 +181,56 @@ __device__ __forceinline__ void merge_batch(float& M, float& L, f32x4& O, const 
 }
 
 // In-launch log-sum-exp combine of the one-launch decode (attn_combine.comp:13-29): one workgroup per
-// output row (t, h), one of the last chunks of its KV head or 16-row slice once its own partials are out,
-// merges that row's split partials as they arrive. A streaming workgroup stores its rows' unnormalized
-// o[D] (device-coherent stores), waits
-// for them to be acknowledged, then stores each row's record (m, l, 64-bit tag): a record carrying this
-// launch's tag guarantees the row's o is visible. The combining workgroup takes the splits in windows of
-// kCombSlots: wave w owns the kCombGroup splits [wb + 32 w, wb + 32 w + 32) of window wb, lane j < 32
-// polling split wb + 32 w + j's record (one 16-byte device-coherent load per round); each split that
-// has arrived has its o row loaded straight into the wave's registers (one coalesced load, D/64 dims a
-// lane). Once its group is complete the wave takes the group's max and weights (wave reductions, the
-// weights broadcast through LDS) and its weighted sum over all D dims; the window's four group results
-// then meet in LDS and merge into the running (M, L, O) in group order — a fixed order, so the result
-// does not depend on which split arrives first. Splits with l = 0 are skipped. The epoch: see
+// (output row (t, h), slice of DW = D / nds dims), one of the last chunks of its KV head or 16-row slice
+// once its own partials are out, merges that row's split partials over its dims as they arrive. A
+// streaming workgroup stores its rows' unnormalized o[D] (device-coherent stores), waits for them to be
+// acknowledged, then stores each row's record (m, l, 64-bit tag): a record carrying this launch's tag
+// guarantees the row's o is visible. The combiner takes the splits in windows of kCombSlots: wave w owns
+// the kCombGroup splits [wb + 32 w, wb + 32 w + 32) of window wb, lane j < 32 polling split wb + 32 w + j's
+// record (one 16-byte device-coherent load per round); each split that has arrived has its DW dims loaded
+// straight into the wave's registers, 16 bytes a lane: lane group g (LPP = DW / 4 lanes) holds splits
+// g NL .. g NL + NL - 1 of the wave's 32. Once its group is complete the wave takes the group's max and
+// weights (wave reductions, the weights broadcast through LDS), its weighted sum per lane and then across
+// the lane groups; the window's four group results meet in LDS and merge into the running (M, L, O) in
+// group order — a fixed order, so the result does not depend on which split arrives first. Splits with
+// l = 0 are skipped. Slicing the dims (nds = 4 at decode: 32 combiners of a KV head's 128 chunks) divides
+// what one combiner loads (128 splits x DW x 4 bytes) and sums, the tail of the launch. The epoch: see
 // kEpochStep. Every wait is bounded (a.spin_max polling rounds); a combiner that gives up reports
-// kWaitCombineFlags and merges whatever its registers hold. At most one combiner per output row waits
-// (8 per KV head, 16 per slice), so every wait ends while more CUs than that are free to the launch.
-template <int D, int IN_DT>
-__device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* smem, int r) {
-    constexpr int NS = kCombSlots, GS = kCombGroup, DL = D / 64;
+// kWaitCombineFlags and merges whatever its registers hold. The host keeps the combiners at half of each
+// KV head's (slice's) chunks or fewer, so every wait ends while more CUs than that are free to the launch.
+template <int D, int IN_DT, int DW>
+__device__ __forceinline__ void combine_slice(const DecodeArgs& a, unsigned char* smem, int r, int ds) {
+    constexpr int NS = kCombSlots, GS = kCombGroup;
+    constexpr int LPP = DW / 4, PPL = 64 / LPP, NL = GS / PPL;  // lanes a split, splits a load, loads a wave
     static_assert(NS == 4 * GS && GS == 32, "one group of 32 splits per wave and window");
-    typedef float fDL __attribute__((ext_vector_type(DL)));
-    float* s_go = reinterpret_cast<float*>(smem);  // [4][D] the window's group sums
-    float* s_gm = s_go + 4 * D;                     // [4] group maxima (log2 units)
+    static_assert(DW % 16 == 0 && DW <= 256 && DW <= D, "16 to 256 dims a combiner, 4 a lane");
+    float* s_go = reinterpret_cast<float*>(smem);  // [4][DW] the window's group sums
+    float* s_gm = s_go + 4 * DW;                    // [4] group maxima (log2 units)
     float* s_gl = s_gm + 4;                         // [4] group sums of l
     float* s_w = s_gl + 4;                          // [4][GS] each group's weights
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int lg = lane / LPP, d4 = (lane % LPP) * 4;  // lane group, first of the lane's 4 dims in the slice
     const int S = a.n_split, G = a.NH / a.NKV;
     const int t = r / a.NH, h = r % a.NH, kvh = h / G;
+    const int d0 = ds * DW;
     const unsigned long long cnt = __hip_atomic_load(a.ep + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // this launch's record tag (see rec_tag), skewed by the test hook
     const unsigned long long want = rec_tag(cnt / kEpochStep + 1u + (unsigned long long)(long long)a.epoch_skew, kvh);
-    const float gate = tid < D ? load_in<IN_DT>(a.q, ((size_t)t * a.NH + h) * 2 * D + D + tid) : 0.f;
+    const float gate = tid < DW ? load_in<IN_DT>(a.q, ((size_t)t * a.NH + h) * 2 * D + D + d0 + tid) : 0.f;
     const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(a.rec + (size_t)r * S * 4, (short)0, S * 16, 0x00020000);
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + (size_t)r * S * D, (short)0, S * D * 4, 0x00020000);
     int spins = 0;
     bool gave_up = false;
-    float M = kNegInf, L = 0.f, O = 0.f;  // thread tid < D: running state of dim tid
+    float M = kNegInf, L = 0.f, O = 0.f;  // thread tid < DW: running state of dim d0 + tid
     for (int wb = 0; wb < S; wb += NS) {
         const int z0 = wb + wave * GS;                 // this wave's first split (wave-uniform)
         const int nz = max(0, min(GS, S - z0));        // its splits in this window
         const int z = z0 + lane;
         bool pend = lane < nz;                         // lane j: split z0 + j not arrived yet
         float mj = kNegInf, lj = 0.f;
-        fDL ov[GS];  // splits past S stay zero (weight 0 too), so the group sum needs no per-split guard
+        f32x4 ov[NL];  // splits past S stay zero (weight 0 too), so the group sum needs no per-split guard
 #pragma unroll
-        for (int j = 0; j < GS; j++) ov[j] = fDL{};
+        for (int k = 0; k < NL; k++) ov[k] = f32x4{};
         while (__ballot(pend) != 0) {
             const f32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(rrec, (pend ? z : 0) * 16, 0, kScDevice);
             const bool last = ++spins > a.spin_max;
@@ -235,16 +240,11 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
             if (got) mj = rv[0], lj = rv[1];
             pend = pend && !got;
             const unsigned long long b = __ballot(got);
-            // each arrived split's o row: one coalesced load into its register slot (a uniform branch per
-            // split keeps the register index static)
+            // each arrived split's dims: lane group lg loads split lg NL + k into register slot k (static)
 #pragma unroll
-            for (int j = 0; j < GS; j++) {
-                if ((b >> j) & 1) {
-                    const int off = ((z0 + j) * D + lane * DL) * 4;
-                    if constexpr (DL == 4) ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, kScDevice);
-                    else if constexpr (DL == 2) ov[j] = __builtin_bit_cast(fDL, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, kScDevice));
-                    else ov[j] = __builtin_bit_cast(fDL, __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, kScDevice));
-                }
+            for (int k = 0; k < NL; k++) {
+                const int j = lg * NL + k;
+                if ((b >> j) & 1) ov[k] = __builtin_amdgcn_raw_buffer_load_b128(ro, ((z0 + j) * D + d0 + d4) * 4, 0, kScDevice);
             }
             if (b == 0) __builtin_amdgcn_s_sleep(1);
         }
@@ -254,25 +254,35 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
         const bool use = lane < nz && lj > 0.f;
         const float mg = max32(use ? mj : kNegInf);
         const float w = use ? exp2_fast(mj - mg) : 0.f;
-        const float lg = sum32(lj * w);
+        const float lsum = sum32(lj * w);
         // the weights to every lane through LDS (broadcast reads): lane j < 32 holds split z0 + j's
         if (lane < GS) s_w[wave * GS + lane] = w;
-        float wv[GS];
+        float wv[NL];
 #pragma unroll
-        for (int j = 0; j < GS; j += 4) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(&s_w[wave * GS + j]);
-            wv[j] = x[0], wv[j + 1] = x[1], wv[j + 2] = x[2], wv[j + 3] = x[3];
+        for (int k = 0; k < NL; k += 4) {
+            if constexpr (NL >= 4) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(&s_w[wave * GS + lg * NL + k]);
+                wv[k] = x[0], wv[k + 1] = x[1], wv[k + 2] = x[2], wv[k + 3] = x[3];
+            } else {
+#pragma unroll
+                for (int u = 0; u < NL; u++) wv[u] = s_w[wave * GS + lg * NL + u];
+            }
         }
-        fDL og = {};
+        f32x4 og = {};
 #pragma unroll
-        for (int j = 0; j < GS; j++) og += ov[j] * wv[j];
-        *reinterpret_cast<fDL*>(&s_go[wave * D + lane * DL]) = og;
+        for (int k = 0; k < NL; k++) og += ov[k] * wv[k];
+        // the lane groups' sums (a fixed butterfly: the same order whatever arrived when)
+#pragma unroll
+        for (int sh = LPP; sh < 64; sh <<= 1)
+#pragma unroll
+            for (int e = 0; e < 4; e++) og[e] += __shfl_xor(og[e], sh, 64);
+        if (lane < LPP) *reinterpret_cast<f32x4*>(&s_go[wave * DW + d4]) = og;
         if (lane == 0) {
             s_gm[wave] = mg;
-            s_gl[wave] = lg;
+            s_gl[wave] = lsum;
         }
         __syncthreads();
-        if (tid < D) {
+        if (tid < DW) {
 #pragma unroll
             for (int gi = 0; gi < 4; gi++) {  // the window's groups in order
                 const float gl = s_gl[gi];
@@ -280,20 +290,30 @@ __device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* 
                     const float gm = s_gm[gi], mn = fmaxf(M, gm);
                     const float cf = L > 0.f ? exp2_fast(M - mn) : 0.f, cg = exp2_fast(gm - mn);
                     L = L * cf + gl * cg;
-                    O = O * cf + s_go[gi * D + tid] * cg;
+                    O = O * cf + s_go[gi * DW + tid] * cg;
                     M = mn;
                 }
             }
         }
         __syncthreads();  // s_go is rewritten by the next window
     }
-    if (tid < D) a.out[((size_t)t * a.NH + h) * D + tid] = (L > 0.f ? O / L : 0.f) * sigmoid(gate);
+    if (tid < DW) a.out[((size_t)t * a.NH + h) * D + d0 + tid] = (L > 0.f ? O / L : 0.f) * sigmoid(gate);
     if (__ballot(gave_up) != 0 && lane == 0) report_wait(a, kWaitCombineFlags);
     if (tid == 0) {  // this combiner is done: its share of the head's epoch step (see kEpochStep)
-        const unsigned m = (unsigned)(a.ncomb / a.NKV), j = (unsigned)(t * G + h % G);  // j-th of the head's m
+        const unsigned m = (unsigned)(a.ncomb / a.NKV * a.nds), j = (unsigned)((t * G + h % G) * a.nds + ds);
         __hip_atomic_fetch_add(a.ep + kvh, (unsigned long long)((j + 1) * kEpochStep / m - j * kEpochStep / m),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// The combiner of output row r, dims slice ds of a.nds (1, 2, 4 or 8: host-checked)
+template <int D, int IN_DT>
+__device__ __forceinline__ void combine_row(const DecodeArgs& a, unsigned char* smem, int r, int ds) {
+    if constexpr (D / 8 >= 16)
+        if (a.nds == 8) return combine_slice<D, IN_DT, D / 8>(a, smem, r, ds);
+    if (a.nds == 4) combine_slice<D, IN_DT, D / 4>(a, smem, r, ds);
+    else if (a.nds == 2) combine_slice<D, IN_DT, D / 2>(a, smem, r, ds);
+    else combine_slice<D, IN_DT, D>(a, smem, r, ds);
 }
 
 template <int D, int FUSED, int IN_DT, int QSA>
@@ -693,10 +713,10 @@ __global__ __launch_bounds__(256, 1) void k_decode(DecodeArgs a) {
             // the slice's last `rows` chunks (the shortest: the first cr chunks are one block longer) then
             // combine one output row each. A combiner waits for the other chunks of its slice; at most 16
             // per slice wait, so every wait ends while more CUs than waiting combiners are free to the launch
-            const int zc = z - (a.n_split - rows);
+            const int zc = z - (a.n_split - rows * a.nds);
             if (zc >= 0) {
-                const int t = (r0 + zc) / G, h = kvh * G + (r0 + zc) % G;
-                combine_row<D, IN_DT>(a, s_u, t * a.NH + h);
+                const int rl = r0 + zc % rows, t = rl / G, h = kvh * G + rl % G;
+                combine_row<D, IN_DT>(a, s_u, t * a.NH + h, zc / rows);
             }
         }
     }
@@ -1190,10 +1210,11 @@ __global__ __launch_bounds__(256, 1) void k_decode_ld(DecodeArgs a) {
             // the head's last `rows` chunks then combine one output row each (the ring is dead: the merge
             // above was its last use). A combiner waits for the other chunks of its head; at most 8 per head
             // wait, so every wait ends while more than 8 x NKV CUs are free to the launch
-            const int zc = z - (S - rows);
+            const int zc = z - (S - rows * a.nds);
             if (zc >= 0) {
                 __syncthreads();
-                combine_row<D, IN_DT>(a, smem, (zc / G) * a.NH + kvh * G + zc % G);
+                const int rl = zc % rows;
+                combine_row<D, IN_DT>(a, smem, (rl / G) * a.NH + kvh * G + rl % G, zc / rows);
             }
         }
     }
@@ -1229,7 +1250,9 @@ static hipError_t launch_mode(const DecodeArgs& a, hipStream_t s) {
     const int rows = a.n * (a.NH / a.NKV);
     // the in-launch combine: fused (it needs the gate), on the last chunks of each KV head (up to 8 rows)
     // or 16-row slice, one output row each, so a head / slice needs that many chunks
-    if (a.out != nullptr && (!FUSED || a.n_split < (rows < 16 ? rows : 16) || a.ncomb != a.n * a.NH || !a.ep || !a.rec))
+    if (a.out != nullptr && (!FUSED || (a.nds != 1 && a.nds != 2 && a.nds != 4 && a.nds != 8) || D / a.nds < 16 ||
+                             a.n_split < (rows < 16 ? rows : 16) * a.nds ||
+                             a.ncomb != a.n * a.NH || !a.ep || !a.rec))
         return hipErrorInvalidValue;
     if (rows <= 8) {
         static std::atomic<uint64_t> raised{0};

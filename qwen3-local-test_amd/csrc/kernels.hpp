@@ -46,8 +46,9 @@ struct DecodeArgs {
                           // partials only, for a separate combine)
     unsigned long long* ep;  // with out: per KV head, the launch counter the epochs come from (zero at first)
     float* rec;           // with out: [n*NH][n_split][4] split records (m, l, epoch tag, 0)
-    int ncomb;            // with out: output rows (n * NH), each combined by one of the last chunks of its
-                          // KV head (up to 8 rows) or 16-row slice
+    int ncomb;            // with out: output rows (n * NH), each combined by nds of the last chunks of its
+                          // KV head (up to 8 rows) or 16-row slice, one slice of D / nds dims each
+    int nds;              // with out: 1, 2, 4 or 8 (D / nds >= 16)
     int cap;              // capacity (positions) of the caches kc, vc
     int* err;             // a bounded wait that gives up stores its kWait* code here (nullptr: not reported)
     const unsigned* kbits;  // QSA: per-token key visibility bits [n][kb_words] (nullptr: dense attention)

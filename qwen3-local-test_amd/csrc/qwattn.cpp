@@ -163,6 +163,16 @@ bool tail_launch(const qwattn_config& g, int n, int S) {
     return S >= std::min(rows, 16);
 }
 
+// Dim slices per output row of that combine: the most of 4, 2, 1 that keeps the combiners at half of a
+// head's (slice's) chunks or fewer (4 at decode: 32 of 128 chunks; 2 at the 4-token verify: 32 of 64);
+// each combiner then loads and sums D / slices dims of every split.
+int combine_slices(const qwattn_config& g, int n, int S) {
+    const int rows = std::min(n * (g.n_heads / g.n_kv_heads), 16);
+    for (int k : {4, 2})
+        if (k > 0 && 2 * rows * k <= S && g.head_dim / k >= 16) return k;
+    return 1;
+}
+
 // more than 8 rows go to the decode kernel's 16-row slices (grid.z)
 Split pick_split(int n_cu, const qwattn_config& g, int maxlen, int n, int n_split, bool fill_cap = false) {
     const int nb = (maxlen + 31) / 32;
@@ -597,7 +607,7 @@ static int decode_impl(qwattn_ctx* c, const char* fn, void* stream, const void* 
     const bool one = tail_launch(g, n, sp.S);
     const int used = sp.S;
     DeviceGuard dg(c->device);
-    if (one) a.out = out, a.ep = c->ep, a.rec = c->rec, a.ncomb = ncomb;
+    if (one) a.out = out, a.ep = c->ep, a.rec = c->rec, a.ncomb = ncomb, a.nds = combine_slices(g, n, sp.S);
     HIP_TRY(c, qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream));
     if (!one) {
         qw::CombineArgs ca{c->part_o, c->part_ml, qg, out, n, g.n_heads, used};
@@ -887,7 +897,7 @@ int qwattn_decode_noalloc(int device, void* stream, const qwattn_config* cfg, co
     a.part_ml = reinterpret_cast<float*>(base + kScratchData + rec_b);
     a.part_o = reinterpret_cast<float*>(base + kScratchData + rec_b + ml_b);
     a.err = wait_status;
-    if (one) a.out = out, a.ep = reinterpret_cast<unsigned long long*>(base), a.ncomb = ncomb;
+    if (one) a.out = out, a.ep = reinterpret_cast<unsigned long long*>(base), a.ncomb = ncomb, a.nds = combine_slices(g, n, sp.S);
     else a.rec = nullptr;
     hipError_t e = qw::launch_decode(a, g.head_dim, true, in_dtype, (hipStream_t)stream);
     if (e == hipSuccess && !one) {

@@ -318,6 +318,9 @@ ONE_LAUNCH = CASES_FUSED + [
     (D128, 2000, 8, 0, "bf16"),         # 32 rows, 8 new rows across a block boundary
     (QWEN3_NEXT, 5000, 4, 1, "f32"),    # one split: 157 tiles through one ring
     (QWEN3_NEXT, 40, 2, 0, "bf16"),     # 16 rows, two splits of one tile each
+    # the in-launch combine's dim slices: 4 per row of 16 dims (D = 64), 2 of 128 (D = 256, 32 splits)
+    (TINY, 4000, 1, 0, "f32"),
+    (QWEN3_NEXT, 9000, 1, 32, "bf16"),
 ]
 
 
