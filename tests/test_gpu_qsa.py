@@ -162,8 +162,10 @@ def _indexer_case(qw, oracle, name, qs, max_ctx, calls, dt):
                   flush=True)
             if name.startswith(("zeros", "ties")):  # exact ties on both sides: block order alone decides
                 assert swaps == 0
-            if name.startswith("halfzero"):  # thousands of exact zeros at the threshold: at most a sign flip or two
-                assert swaps <= 2
+            # thousands of exact zeros at the threshold (halfzero): at most a sign flip or two; random scores: a
+            # near-tie at the budget boundary is rare (a few blocks lie within 1e-5 of it at 65,536 blocks), so
+            # more than two swaps in a call would be a wrong selection, not rounding
+            assert swaps <= 2, f"{name} pos={pos}: {swaps} near-tie swaps"
             # the key bits follow the GPU's own selection by the reference's visibility rule
             assert np.array_equal(host(kbits).view(np.uint32), orc.qsa_key_bits(got, pos, n, qs.CR))
         row += n
