@@ -64,12 +64,6 @@ __device__ __forceinline__ unsigned wave_isum(unsigned x) {
 // no builtin for)
 __device__ unsigned writelane(unsigned src, unsigned lane, unsigned old) __asm("llvm.amdgcn.writelane.i32");
 
-__device__ __forceinline__ unsigned wave_min(unsigned x) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x = min(x, (unsigned)__shfl_xor((int)x, o, 64));
-    return x;
-}
-
 __device__ __forceinline__ unsigned wave_max(unsigned x) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) x = max(x, (unsigned)__shfl_xor((int)x, o, 64));
