@@ -7,8 +7,9 @@
 // scalar FMAs); this kernel is new design:
 //  - GQA packing: a workgroup owns 128 query rows = 128/G consecutive tokens x the G heads of one KV
 //    head, so each K/V tile staged in LDS feeds all of them; 4 waves x 32 rows.
-//  - S^T[32 keys x 32 rows] = K Q^T and O^T[D x 32 rows] += V^T P^T on v_mfma_f32_32x32x16_f16 (the
-//    shape that reaches ~2 PFLOP/s on gfx950; 16x16x32 reaches half of that) with fp32 accumulators.
+//  - S^T[32 keys x 32 rows] = K Q^T and O^T[D x 32 rows] += V^T P^T on v_mfma_f32_32x32x16_f16 with fp32
+//    accumulators: 32 query rows a wave, so each K/V fragment read from LDS feeds twice the work a
+//    16x16x32 instruction would (both shapes issue at the same FLOP rate on gfx950).
 //    A 64-key tile is two cache blocks; the QK^T product runs as four independent accumulation chains
 //    (block x even/odd k-step) and P.V as D/32 chains, so the matrix pipe never waits on one result.
 //  - Tiles are copied verbatim from the blocked cache (common.hpp) into LDS: 16 contiguous bytes per
