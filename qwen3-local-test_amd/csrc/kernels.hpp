@@ -94,8 +94,8 @@ struct PrefillArgs {
     int pos, n, NH, NKV;
     float q_scale;
     int cap;              // capacity (positions) of the caches kc, vc
-    float* part;          // [NKV][slots][2 halves][4 waves][pf_part_floats(D)]: partials of split query tiles
-    int* cnt;             // [NKV][slots][4 waves] arrival counters, zero between launches
+    float* part;          // [NKV][slots][2 halves][kPfWaves][pf_part_floats(D)]: partials of split query tiles
+    int* cnt;             // [NKV][slots][kPfWaves] arrival counters, zero between launches
     int slots;            // split tiles per KV head: pf_split_slots(n_qt, split_all)
     int split_all;        // 0: short and long tiles paired; 1: every tile's keys split over two workgroups
     // queries normalized in the kernel (q == NULL): RMSNorm weights, rope table [>= pos+n][R/2][2], R
@@ -114,8 +114,10 @@ __host__ __device__ constexpr bool pf_fused_rope_ok(int R, int D) {
 }
 // Split slots per KV head of a launch with n_qt query tiles per KV head.
 __host__ __device__ constexpr int pf_split_slots(int n_qt, int split_all) { return split_all ? n_qt : n_qt / 2; }
-// Floats of one wave's prefill partial: 64 lanes x (D/2 accumulator values + max and sum).
-__host__ __device__ constexpr int pf_part_floats(int D) { return 64 * (D / 2 + 2); }
+// Waves of a prefill workgroup (16 query rows each).
+constexpr int kPfWaves = 8;
+// Floats of one wave's prefill partial: 64 lanes x (D/4 accumulator values + max and sum).
+__host__ __device__ constexpr int pf_part_floats(int D) { return 64 * (D / 4 + 2); }
 // Query tiles of an n-token prefill with GQA group G (128 query rows per tile).
 __host__ __device__ constexpr int pf_query_tiles(int n, int G) { return (n + 128 / G - 1) / (128 / G); }
 hipError_t launch_prefill(const PrefillArgs& a, int D, int q_dtype, int in_dtype, hipStream_t s);

@@ -6,17 +6,18 @@
 // times sigmoid(gate). The reference has no matrix-core attention (every workgroup streams K/V with
 // scalar FMAs); this kernel is new design:
 //  - GQA packing: a workgroup owns 128 query rows = 128/G consecutive tokens x the G heads of one KV
-//    head, so each K/V tile staged in LDS feeds all of them; 4 waves x 32 rows.
-//  - S^T[32 keys x 32 rows] = K Q^T and O^T[D x 32 rows] += V^T P^T on v_mfma_f32_32x32x16_f16 with fp32
-//    accumulators: 32 query rows a wave, so each K/V fragment read from LDS feeds twice the work a
-//    16x16x32 instruction would (both shapes issue at the same FLOP rate on gfx950).
-//    A 64-key tile is two cache blocks; the QK^T product runs as four independent accumulation chains
-//    (block x even/odd k-step) and P.V as D/32 chains, so the matrix pipe never waits on one result.
+//    head, so each K/V tile staged in LDS feeds all of them; 8 waves x 16 rows, two waves a SIMD (a wave
+//    holds its rows' Q^T, D/4 registers a lane, and their whole output, D/4 more, so two fit the 256
+//    registers a wave has at that occupancy; both waves of a SIMD interleave their matrix instructions,
+//    LDS reads and softmax).
+//  - S^T[16 keys x 16 rows] = K Q^T and O^T[16 dims x 16 rows] += V^T P^T on v_mfma_f32_16x16x32_f16 with
+//    fp32 accumulators (the same FLOP rate as the 32x32x16 shape on gfx950). A 64-key tile is two cache
+//    blocks; QK^T runs as four independent accumulation chains (block x key set), P.V as D/16.
 //  - Tiles are copied verbatim from the blocked cache (common.hpp) into LDS: 16 contiguous bytes per
 //    lane from global memory, the same bytes lane-linearly into LDS. In that layout every operand
-//    fragment read is 8-lane groups over 128 contiguous bytes, so LDS reads are bank-conflict free, and
-//    the P^T operand of P.V is exactly the register order the QK^T product leaves (S rows map to keys
-//    with bits 2 and 3 swapped), so no shuffles sit between the two products.
+//    fragment is one contiguous kilobyte read lane-linearly (bank-conflict free), and the P^T operand of
+//    P.V is exactly the register order the QK^T product leaves (a lane's scores are keys 8 g .. 8 g + 7 of
+//    each block), so no shuffles sit between the two products.
 //  - Global -> LDS staging is double buffered with direct-to-LDS buffer loads (no registers; range
 //    checked, so blocks past the last written position load zeros) and one barrier per tile; V rows past
 //    the last position are zeroed in LDS, so stale or unwritten cache memory never reaches the sum.
@@ -42,11 +43,11 @@ constexpr int PF_KT = 64;     // keys per LDS tile (two cache blocks)
 
 template <int D>
 struct PfCfg {
-    static constexpr int NKS = D / 16;                  // QK k-steps (32x32x16)
-    static constexpr int NDT = D / 32;                  // P.V dim tiles
+    static constexpr int NKS = D / 32;                  // QK k-steps (16x16x32)
+    static constexpr int NDT = D / 16;                  // P.V dim tiles
     static constexpr int BLKE = kBlk * D;               // elements of one (block, head) part
     static constexpr int TILEE = 2 * BLKE;              // elements of a 64-key tile (K or V)
-    static constexpr int LOADS = TILEE * 2 / (4 * 1024);  // 1 KB direct loads per wave per tile (K or V)
+    static constexpr int LOADS = TILEE * 2 / (kPfWaves * 1024);  // 1 KB direct loads per wave per tile (K or V)
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -73,78 +74,102 @@ constexpr int slot_nth(int n, bool pv, int u) {
 
 }  // namespace
 
-// The raw query values of a lane (8 per k-step: one 16-byte load of bf16, two of fp32) and, for R <= 64,
-// its rope (cos, sin) pairs, loaded first and used only in pf_query_fused: every vector load of the
-// prologue is then issued before the first K tiles' copies, so none of them waits behind the copies
-// (vector loads complete in issue order), and the math runs while the copies fly.
-constexpr int kPfRopeEarly = 2;  // k-steps of (cos, sin) loaded with the query (R <= 64)
+// The raw query values of lane (c, g) — row c of its wave's 16, dims 32 kk + 8 g + j (j < 8) of every
+// 32-dim k-step kk: one 16-byte load of bf16 or two of fp32 a k-step — and, for 64 <= R <= 32 kPfRopeEarly
+// * 2, the rope (cos, sin) pairs of its first k-steps, loaded first and used only in pf_query_fused: every
+// vector load of the prologue is then issued before the first K tiles' copies, so none of them waits
+// behind the copies (vector loads complete in issue order), and the math runs while the copies fly.
+constexpr int kPfRopeEarly = 1;  // k-steps of (cos, sin) loaded with the query (R = 64)
 template <int D, int IN_DT>
 struct PfQRaw {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    typename std::conditional<IN_DT == 0, f32x4, u32x4>::type v[D / 16][IN_DT == 0 ? 2 : 1];
+    typename std::conditional<IN_DT == 0, f32x4, u32x4_t>::type v[D / 32][IN_DT == 0 ? 2 : 1];
     f32x4 cs[kPfRopeEarly][4];
-    __device__ __forceinline__ void load(const PrefillArgs& a, int t, int h, int half) {
-        if (a.R > 0 && a.R <= 32 * kPfRopeEarly) {
-            const float* cs_row = a.rope + (size_t)(a.pos + t) * a.R + 16 * half;
+    __device__ __forceinline__ void load(const PrefillArgs& a, int t, int h, int g) {
+        if (a.R == 64) {
+            const float* cs_row = a.rope + (size_t)(a.pos + t) * a.R + 16 * g;
 #pragma unroll
-            for (int ks = 0; ks < kPfRopeEarly; ks++)
-                if (32 * ks < a.R)
-#pragma unroll
-                    for (int k = 0; k < 4; k++) cs[ks][k] = *reinterpret_cast<const f32x4*>(cs_row + 32 * ks + 4 * k);
+            for (int k = 0; k < 4; k++) cs[0][k] = *reinterpret_cast<const f32x4*>(cs_row + 4 * k);
         }
-        const size_t off = ((size_t)t * a.NH + h) * 2 * D + 8 * half;
+        const size_t off = ((size_t)t * a.NH + h) * 2 * D + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ks++) {
+        for (int kk = 0; kk < D / 32; kk++) {
             if constexpr (IN_DT == 0) {
-                const float* p = static_cast<const float*>(a.qg) + off + 16 * ks;
-                v[ks][0] = *reinterpret_cast<const f32x4*>(p);
-                v[ks][1] = *reinterpret_cast<const f32x4*>(p + 4);
+                const float* p = static_cast<const float*>(a.qg) + off + 32 * kk;
+                v[kk][0] = *reinterpret_cast<const f32x4*>(p);
+                v[kk][1] = *reinterpret_cast<const f32x4*>(p + 4);
             } else {
-                v[ks][0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qg) + off + 16 * ks);
+                v[kk][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(a.qg) + off + 32 * kk);
             }
         }
     }
-    __device__ __forceinline__ float at(int ks, int j) const {
-        if constexpr (IN_DT == 0) return v[ks][j >> 2][j & 3];
-        else return __uint_as_float((j & 1) ? v[ks][0][j >> 1] & 0xffff0000u : v[ks][0][j >> 1] << 16);
+    __device__ __forceinline__ float at(int kk, int j) const {
+        if constexpr (IN_DT == 0) return v[kk][j >> 2][j & 3];
+        else return __uint_as_float((j & 1) ? v[kk][0][j >> 1] & 0xffff0000u : v[kk][0][j >> 1] << 16);
     }
 };
 
 // The Q^T operand of query row (t, h) from the raw projection output: the query half of qg normalized,
 // rotated and scaled in registers — the steps of the norm kernel (norm_rope.hip) for a query row, so a
 // layer's prefill needs no query buffer: y = x * rsqrt(mean(x^2) + eps) * (1 + qn), rotate-half RoPE
-// on dims [0, R) with the (cos, sin) of position pos + t, then fp16(y * q_scale). Lane (col, half) holds
-// dims 16 ks + 8 half + j of the row and its partner lane (col, 1 - half) the other half of every k-step,
-// so the mean of squares is one lane swap, and the rotate-half partner of dim d < R/2 is dim d + R/2 =
-// k-step ks + OFF of the same lane, OFF = R/32 (a template argument, so both operands are static
-// registers). Each k-step (or rotate-half pair) goes from the raw registers to the operand directly;
-// rs = rsqrt term * q_scale folds the score scale into the row factor (0 for a row past the chunk).
+// on dims [0, R) with the (cos, sin) of position pos + t, then fp16(y * q_scale). The four lanes (c, g) of
+// a row hold its dims 32 kk + 8 g + j, so the mean of squares is two lane swaps. The rotate-half partner
+// of dim d < R/2 is d + R/2: k-step kk + OFF of the same lane for R >= 64 (OFF = R/64), the lane 32 away
+// for R = 32 (OFF = -1: dims 0-15 in lanes g < 2, their partners in lanes g + 2). rs = rsqrt term *
+// q_scale folds the score scale into the row factor (0 for a row past the chunk).
 template <int D, int IN_DT, int OFF>
-__device__ __forceinline__ void pf_query_finish(const PrefillArgs& a, const PfQRaw<D, IN_DT>& raw, const float* sW,
-                                                float rs, int t, int half, f16x8 (&qop)[D / 16]) {
-    constexpr int NKS = D / 16;
-    const float* cs_row = a.rope + (size_t)(a.pos + t) * a.R + 16 * half;
-    auto y = [&](int ks, float (&o)[8]) __attribute__((always_inline)) {  // normalized, weighted
-        const f32x4 w0 = *reinterpret_cast<const f32x4*>(sW + 16 * ks + 8 * half);
-        const f32x4 w1 = *reinterpret_cast<const f32x4*>(sW + 16 * ks + 8 * half + 4);
+__device__ __forceinline__ void pf_query_finish(const PrefillArgs& a, PfQRaw<D, IN_DT> raw, const float* sW,
+                                                float rs, int t, int g, int lane, f16x8 (&qop)[D / 32]) {
+    constexpr int NKS = D / 32;
+    const float* cs_row = a.rope + (size_t)(a.pos + t) * a.R + 16 * g;
+    // opaque per rope width: the widened raw values and the products raw * rs would otherwise be
+    // hoisted above the caller's branch on R as common expressions, all of them live at once
+    asm volatile("" : "+v"(rs));
 #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = raw.at(ks, j) * rs * (j < 4 ? w0[j] : w1[j - 4]);
+    for (int kk = 0; kk < NKS; kk++)
+#pragma unroll
+        for (int k = 0; k < (IN_DT == 0 ? 2 : 1); k++) asm volatile("" : "+v"(raw.v[kk][k]));
+    auto y = [&](int kk, float (&o)[8]) __attribute__((always_inline)) {  // normalized, weighted
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(sW + 32 * kk + 8 * g);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(sW + 32 * kk + 8 * g + 4);
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = raw.at(kk, j) * rs * (j < 4 ? w0[j] : w1[j - 4]);
     };
-    auto put = [&](int ks, const float (&o)[8]) __attribute__((always_inline)) {
+    auto put = [&](int kk, const float (&o)[8]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) qop[ks][j] = (f16)o[j];
+        for (int j = 0; j < 8; j++) qop[kk][j] = (f16)o[j];
     };
 #pragma unroll
-    for (int ks = 0; ks < NKS; ks++) {
-        if (ks < OFF) {  // dims d < R/2 and their partners d + R/2
-            float lo[8], hi[8], cs[16];  // (cos, sin) of i = 16 ks + 8 half + j
-            y(ks, lo);
-            y(ks + OFF, hi);
+    for (int kk = 0; kk < NKS; kk++) {
+        if constexpr (OFF < 0) {  // R = 32: dims 0-15 (lanes g < 2) pair with dims 16-31 (lanes g + 2)
+            if (kk == 0) {
+                float o[8], p[8], cs[16];
+                y(0, o);
+                // (cos, sin) of i = 8 (g & 1) + j
+                load_vec<0, 16>(a.rope + (size_t)(a.pos + t) * a.R, 16 * (g & 1), cs);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[j]), __float_as_uint(o[j]), false, false);
+                    p[j] = __uint_as_float(lane < 32 ? sw[1] : sw[0]);
+                }
+                float r[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    r[j] = g < 2 ? o[j] * cs[2 * j] - p[j] * cs[2 * j + 1] : o[j] * cs[2 * j] + p[j] * cs[2 * j + 1];
+                put(0, r);
+            } else {
+                float o[8];
+                y(kk, o);
+                put(kk, o);
+            }
+        } else if (kk < OFF) {  // dims d < R/2 and their partners d + R/2
+            float lo[8], hi[8], cs[16];  // (cos, sin) of i = 32 kk + 8 g + j
+            y(kk, lo);
+            y(kk + OFF, hi);
             if constexpr (OFF <= kPfRopeEarly) {
 #pragma unroll
-                for (int k = 0; k < 16; k++) cs[k] = raw.cs[ks < kPfRopeEarly ? ks : 0][k >> 2][k & 3];
+                for (int k = 0; k < 16; k++) cs[k] = raw.cs[0][k >> 2][k & 3];
             } else {
-                load_vec<0, 16>(cs_row, 32 * ks, cs);
+                load_vec<0, 16>(cs_row, 64 * kk, cs);
             }
             float rl[8], rh[8];
 #pragma unroll
@@ -152,40 +177,46 @@ __device__ __forceinline__ void pf_query_finish(const PrefillArgs& a, const PfQR
                 rl[j] = lo[j] * cs[2 * j] - hi[j] * cs[2 * j + 1];
                 rh[j] = hi[j] * cs[2 * j] + lo[j] * cs[2 * j + 1];
             }
-            put(ks, rl);
-            put(ks + OFF, rh);
-        } else if (ks >= 2 * OFF) {
+            put(kk, rl);
+            put(kk + OFF, rh);
+        } else if (kk >= 2 * OFF) {
             float o[8];
-            y(ks, o);
-            put(ks, o);
+            y(kk, o);
+            put(kk, o);
         }
+        // k-step boundary: hoisted, the multiplier and rope reads of every k-step would be live at once
+        // beside the raw values and the operand
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 template <int D, int IN_DT>
 __device__ __forceinline__ void pf_query_fused(const PrefillArgs& a, const PfQRaw<D, IN_DT>& raw, const float* sW,
-                                               int t, int half, bool row_ok, f16x8 (&qop)[D / 16]) {
-    constexpr int NKS = D / 16;
+                                               int t, int g, int lane, bool row_ok, f16x8 (&qop)[D / 32]) {
+    constexpr int NKS = D / 32;
     // eight independent partial sums of squares (a single chain would be NKS * 8 instructions long)
     float s8[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) s8[j] = raw.at(0, j) * raw.at(0, j);
 #pragma unroll
-    for (int ks = 1; ks < NKS; ks++)
+    for (int kk = 1; kk < NKS; kk++)
 #pragma unroll
-        for (int j = 0; j < 8; j++) s8[j] = __builtin_fmaf(raw.at(ks, j), raw.at(ks, j), s8[j]);
+        for (int j = 0; j < 8; j++) s8[j] = __builtin_fmaf(raw.at(kk, j), raw.at(kk, j), s8[j]);
     float ss = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-    ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    // the row's four lanes (c, g): lanes 16 apart, then 32 apart
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    ss = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+    ss = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
     // the row factor with the score scale folded in (the rotation is linear, so it commutes); the raw
     // values of a row past the chunk are those of row 0 (finite), so a zero factor zeroes the row
     const float rs = row_ok ? 1.0f / sqrtf(ss / (float)D + a.eps) * a.q_scale : 0.f;
     // the multipliers 1 + qn come from LDS (sW, the same for every row: broadcast reads)
-    if (a.R == 0) pf_query_finish<D, IN_DT, 0>(a, raw, sW, rs, t, half, qop);
-    if constexpr (NKS >= 2) if (a.R == 32) pf_query_finish<D, IN_DT, 1>(a, raw, sW, rs, t, half, qop);
-    if constexpr (NKS >= 4) if (a.R == 64) pf_query_finish<D, IN_DT, 2>(a, raw, sW, rs, t, half, qop);
-    if constexpr (NKS >= 8) if (a.R == 128) pf_query_finish<D, IN_DT, 4>(a, raw, sW, rs, t, half, qop);
-    if constexpr (NKS >= 16) if (a.R == 256) pf_query_finish<D, IN_DT, 8>(a, raw, sW, rs, t, half, qop);
+    if (a.R == 0) pf_query_finish<D, IN_DT, 0>(a, raw, sW, rs, t, g, lane, qop);
+    if (a.R == 32) pf_query_finish<D, IN_DT, -1>(a, raw, sW, rs, t, g, lane, qop);
+    if constexpr (NKS >= 2) if (a.R == 64) pf_query_finish<D, IN_DT, 1>(a, raw, sW, rs, t, g, lane, qop);
+    if constexpr (NKS >= 4) if (a.R == 128) pf_query_finish<D, IN_DT, 2>(a, raw, sW, rs, t, g, lane, qop);
+    if constexpr (NKS >= 8) if (a.R == 256) pf_query_finish<D, IN_DT, 4>(a, raw, sW, rs, t, g, lane, qop);
 }
 
 // Key tiles of query tile qt: keys [0, pos + last token of the tile + 1) in 64-key tiles.
@@ -203,6 +234,7 @@ template <int D, int IN_DT, bool QF, bool QSA>
 __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot) {
     using C = PfCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, BLKE = C::BLKE, TILEE = C::TILEE, LOADS = C::LOADS;
+    constexpr int NQK = 4 * NKS, NPV = 2 * NDT;  // matrix instructions a tile: QK^T, P.V (D/8 each)
     constexpr float TAU = 8.f;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     // two K tile buffers, then two V tile buffers
@@ -215,18 +247,18 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     asm volatile("" : "+v"(tid_));
     const int tid = tid_, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: copy addresses stay scalar
-    const int col = lane & 31, half = lane >> 5;
+    const int col = lane & 15, g = lane >> 4;
     const int G = a.NH / a.NKV;
     const int tok_per_blk = PF_ROWS / G;
     const int t0 = qt * tok_per_blk;
 
     // this lane's query row (B-operand column) and its causal limit
-    const int r = wave * 32 + col;
+    const int r = wave * 16 + col;
     const int t = t0 + r / G, h = kvh * G + r % G;
     const bool row_ok = t < a.n;
     const int len = row_ok ? a.pos + t + 1 : 0;
     // the wave's first token: keys below its limit need no mask
-    const int t_wave_first = t0 + wave * 32 / G;
+    const int t_wave_first = t0 + wave * 16 / G;
     const int wave_nomask = a.pos + t_wave_first + 1;  // keys below this are visible to every row of the wave
     const int maxlen = a.pos + a.n;
     // QSA: the key bits of this lane's token for the current 64-key tile (two words), the next tile's
@@ -240,7 +272,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         }
     };
 
-    // ---- Q^T operand in registers: lane holds row `col`, dims 16*ks + 8*half .. +8 ----------------
+    // ---- Q^T operand in registers: lane (col, g) holds row `col`, dims 32*kk + 8*g .. +8 -------------
     // the loads are issued here, the operand finished once the first K tiles' copies are in flight.
     // In-kernel normalization: the norm multipliers 1 + qn go to LDS (after the four tile buffers), loaded
     // by wave 0 ahead of every other load of the segment
@@ -250,17 +282,17 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     f32x4 wq{};
     if constexpr (QF) {
         if (wave == 0 && lane < D / 4) wq = *reinterpret_cast<const f32x4*>(a.qn + 4 * lane);
-        qraw.load(a, row_ok ? t : 0, h, half);
+        qraw.load(a, row_ok ? t : 0, h, g);
     } else {
-        const size_t qoff = ((size_t)(row_ok ? t : 0) * a.NH + h) * D + 8 * half;
+        const size_t qoff = ((size_t)(row_ok ? t : 0) * a.NH + h) * D + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ks++) qop[ks] = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qoff + 16 * ks);
+        for (int ks = 0; ks < NKS; ks++) qop[ks] = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qoff + 32 * ks);
     }
     asm volatile("" ::: "memory");  // the query loads stay ahead of the copies
 
-    f32x16 acc[NDT];
+    f32x4 acc[NDT];
 #pragma unroll
-    for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x16{};
+    for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x4{};
     float m_run = kNegInf, l_run = 0.f;
 
     // ---- K/V staging: range-checked buffer loads of whole blocks of this KV head --------------------
@@ -271,10 +303,10 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.vc) + kv_part(0, kvh, a.cap, D), (short)0, nblk * bstride, 0x00020000);
     // direct-to-LDS copy, piece i of tile kt: 16 bytes per lane, lane-linear, one kilobyte per
-    // instruction; each wave copies every fourth kilobyte of the tile
+    // instruction; each wave copies every eighth kilobyte of the tile
     const int lane16 = lane * 16;
     auto copy_piece = [&](const __amdgpu_buffer_rsrc_t& rs, f16* dst, int kt, int i) {
-        const int ci = wave + 4 * i;  // kilobyte of the tile
+        const int ci = wave + kPfWaves * i;  // kilobyte of the tile
         const int blk = 2 * kt + ci / (BLKE / 512);
         // the whole offset in the per-lane operand, so the range check covers it
         const int off = blk * bstride + (ci % (BLKE / 512)) * 1024 + lane16;
@@ -288,7 +320,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     // V rows past the last written position: zeroed in LDS (each 16-byte chunk holds 8 consecutive keys
     // of one dim), so stale or unwritten cache memory never reaches the sum
     auto zero_tail = [&](f16* Vb, int kt) {
-        for (int idx = tid; idx < TILEE / 8; idx += 256) {
+        for (int idx = tid; idx < TILEE / 8; idx += 64 * kPfWaves) {
             const int q = idx % (BLKE / 8);
             const int key0 = (2 * kt + idx / (BLKE / 8)) * kBlk + 8 * ((q >> 4) & 3);
             if (key0 + 7 >= maxlen) {
@@ -301,48 +333,47 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         }
     };
 
-    // per-lane constant parts of the fragment addresses (elements within a block part)
-    // K: S^T row m = col <-> key sigma(col) = col with bits 2 and 3 swapped; dims 16*ks + 8*half
-    const int kq = (col & ~12) | ((col & 4) << 1) | ((col & 8) >> 1);
-    const int kc_ = ((kq >> 3) << 2) | (kq & 3), ks_ = (kq >> 2) & 1;
-    const int koff_lane = ks_ * 512 + half * 128 + kc_ * 8;
-    // V^T: dim 32*dt + col, keys 8*(2u + half) .. +7 of a block
-    const int voff_lane = (((col >> 4) * 4 + half) * 16 + (col & 15)) * 8;
-
-    // Operand fragments in the order the matrix instructions consume them. Slot i of a tile iteration:
-    // even i -> QK^T step i/2 (k-step (i/2)/2 of cache block (i/2)%2), odd i -> P.V step i/2 (block
-    // q/(2*NDT), 16-key half (q/NDT)%2, dim tile q%NDT with q = i/2).
-    constexpr int NSLOT = 2 * 2 * NKS;  // QK^T and P.V have D/8 steps each
-    constexpr int PF = 5;               // fragment reads run this many slots ahead
+    // Operand fragments: every one is the kilobyte of a block part at lane * 8 elements (the cache
+    // layout). QK^T step q (of NQK): chain cq = q % 4 = (block b, key set s) = (cq / 2, cq % 2), k-step q / 4:
+    // fragment (kk, s) of block b — lane (col, g) holding key 8*(col/4) + 4*s + col%4, dims 32*kk + 8*g ..
+    // +7. P.V step q (of NPV): block q / NDT, dim tile dt = q % NDT: V^T fragment dt — lane (col, g) holding
+    // dim 16*dt + col, keys 8*g .. +7 of the block. Slot i of a tile iteration: even i -> QK^T step i/2,
+    // odd i -> P.V step i/2.
+    constexpr int NSLOT = NQK + NPV;
+    constexpr int PF = 5;  // fragment reads run this many slots ahead
+    const int foff_lane = lane * 8;
     auto kfrag = [&](const f16* Kb, int q) -> f16x8 {
-        return *reinterpret_cast<const f16x8*>(Kb + (q & 1) * BLKE + ((q >> 1) >> 1) * 1024 + ((q >> 1) & 1) * 256);
+        return *reinterpret_cast<const f16x8*>(Kb + ((q % 4) >> 1) * BLKE + ((q / 4) * 2 + (q & 1)) * 512);
     };
     auto vfrag = [&](const f16* Vb, int q) -> f16x8 {
-        return *reinterpret_cast<const f16x8*>(Vb + (q / (2 * NDT)) * BLKE + ((q % NDT) * 8 + 2 * ((q / NDT) & 1)) * 16 * 8);
+        return *reinterpret_cast<const f16x8*>(Vb + (q / NDT) * BLKE + (q % NDT) * 512);
     };
 
-    f32x16 sc[2], sn[2];
-    f16x8 pcur[2][2], pprev[2][2];
+    // S^T of tile kt (sc) and kt+1 (sn): chain cq = 2 b + s, value i -> key 32 b + 8 g + 4 s + i of column col
+    f32x4 sc[4], sn[4];
+    // P^T operands of a tile: block b holds keys 32 b + 8 g + (0..7): {chain 2b value 0..3, chain 2b+1 value 0..3}
+    f16x8 pcur[2], pprev[2];
 
     // QK^T alone (the first tile) and P.V alone (the last tile), with the same fragment prefetch
     auto qk_only = [&](const f16* Kb) {
         f16x8 fr[PF + 1];
         static_for<0, PF>([&](auto ic) __attribute__((always_inline)) { fr[ic.value] = kfrag(Kb, ic.value); });
-        sn[0] = sn[1] = f32x16{};
-        static_for<0, 2 * NKS>([&](auto ic) __attribute__((always_inline)) {
+#pragma unroll
+        for (int cq = 0; cq < 4; cq++) sn[cq] = f32x4{};
+        static_for<0, NQK>([&](auto ic) __attribute__((always_inline)) {
             constexpr int q = decltype(ic)::value;
-            if constexpr (q + PF < 2 * NKS) fr[(q + PF) % (PF + 1)] = kfrag(Kb, q + PF);
-            sn[q & 1] = mfma32(fr[q % (PF + 1)], qop[q >> 1], sn[q & 1]);
+            if constexpr (q + PF < NQK) fr[(q + PF) % (PF + 1)] = kfrag(Kb, q + PF);
+            sn[q % 4] = mfma16(fr[q % (PF + 1)], qop[q / 4], sn[q % 4]);
             __builtin_amdgcn_sched_barrier(0);  // keep the reads PF slots ahead
         });
     };
     auto pv_only = [&](const f16* Vb) {
         f16x8 fr[PF + 1];
         static_for<0, PF>([&](auto ic) __attribute__((always_inline)) { fr[ic.value] = vfrag(Vb, ic.value); });
-        static_for<0, 4 * NDT>([&](auto ic) __attribute__((always_inline)) {
+        static_for<0, NPV>([&](auto ic) __attribute__((always_inline)) {
             constexpr int q = decltype(ic)::value;
-            if constexpr (q + PF < 4 * NDT) fr[(q + PF) % (PF + 1)] = vfrag(Vb, q + PF);
-            acc[q % NDT] = mfma32(fr[q % (PF + 1)], pprev[q / (2 * NDT)][(q / NDT) & 1], acc[q % NDT]);
+            if constexpr (q + PF < NPV) fr[(q + PF) % (PF + 1)] = vfrag(Vb, q + PF);
+            acc[q % NDT] = mfma16(fr[q % (PF + 1)], pprev[q / NDT], acc[q % NDT]);
             __builtin_amdgcn_sched_barrier(0);
         });
     };
@@ -350,15 +381,17 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     // One pipeline step, written in issue order: the softmax of tile kt (scores sc, weights into pc)
     // spread between the matrix instructions of QK^T(kt+1) (into sn, from K buffer Kb) and, when DO_PV,
     // P.V(kt-1) (weights pp, from V buffer Vb). The three are mutually independent, so the softmax
-    // arithmetic issues while the matrix pipe works (two QK^T chains and D/32 P.V chains, alternating).
-    // Softmax: row max over the first M1 slots, the rescale decision over the next three (one link of
-    // that dependent chain per slot), then the exponentials, half-precision weights and row sums.
+    // arithmetic issues while the matrix pipe works (four QK^T chains and D/16 P.V chains, alternating).
+    // Softmax: row max over the first M1 slots and the row's four lanes, the rescale decision over the next
+    // two (one link of that dependent chain per slot), then the exponentials, half-precision weights and
+    // the lane's part of the row sums.
     float corr = 1.f;
     bool any_rescale = false;
     auto step = [&](auto do_pv, const f16* Kb, const f16* Vb, int kt) __attribute__((always_inline)) {
         constexpr bool DO_PV = decltype(do_pv)::value;
         constexpr int M1 = NSLOT / 4;                   // max phase: slots [0, M1)
         constexpr int E0 = M1 + 4, NE = NSLOT - E0;  // exponentials: slots [E0, NSLOT)
+        static_assert(NE >= 1, "slots for the exponentials");
         auto frag = [&](int i) -> f16x8 {
             return slot_is_qk(NSLOT, i) ? kfrag(Kb, slot_qk(i)) : vfrag(Vb, slot_pv(NSLOT, i));
         };
@@ -366,7 +399,8 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         static_for<0, PF>([&](auto ic) __attribute__((always_inline)) {
             fr[ic.value] = frag(slot_nth(NSLOT, DO_PV, ic.value));
         });
-        sn[0] = sn[1] = f32x16{};
+#pragma unroll
+        for (int cq = 0; cq < 4; cq++) sn[cq] = f32x4{};
         float mx = kNegInf, m_use = 0.f, m_new = 0.f, ps[2] = {0.f, 0.f};
         bool grow = false;
         static_for<0, NSLOT>([&](auto ic) __attribute__((always_inline)) {
@@ -374,8 +408,8 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             // staging copies for the next iteration (K tile kt+2, V tile kt), one every third slot: issued
             // in one burst they would fill the vector-memory queue and stall the wave until it drains.
             // Past the last tile they read zeros (range-checked) or unused blocks into free buffers.
-            if constexpr (i % 3 == 0 && i / 3 < 2 * LOADS) {
-                constexpr int j = i / 3;
+            if constexpr (i % 6 == 0 && i / 6 < 2 * LOADS) {
+                constexpr int j = i / 6;
                 if constexpr (j < LOADS) copy_piece(rk, sK(kt & 1), kt + 2, j);
                 else copy_piece(rv, sV(kt & 1), kt, j - LOADS);
             }
@@ -385,18 +419,21 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
                 if constexpr (nx >= 0) fr[(u + PF) % (PF + 1)] = frag(nx);
                 if constexpr (slot_is_qk(NSLOT, i)) {
                     constexpr int qi = slot_qk(i);
-                    sn[qi & 1] = mfma32(fr[u % (PF + 1)], qop[qi >> 1], sn[qi & 1]);
+                    sn[qi % 4] = mfma16(fr[u % (PF + 1)], qop[qi / 4], sn[qi % 4]);
                 } else {
                     constexpr int pi = slot_pv(NSLOT, i);
-                    acc[pi % NDT] = mfma32(fr[u % (PF + 1)], pprev[pi / (2 * NDT)][(pi / NDT) & 1], acc[pi % NDT]);
+                    acc[pi % NDT] = mfma16(fr[u % (PF + 1)], pprev[pi / NDT], acc[pi % NDT]);
                 }
             }
             if constexpr (i < M1) {
 #pragma unroll
-                for (int v = i * 32 / M1; v < (i + 1) * 32 / M1; v++) mx = fmaxf(mx, sc[v >> 4][v & 15]);
+                for (int v = i * 16 / M1; v < (i + 1) * 16 / M1; v++) mx = fmaxf(mx, sc[v >> 2][v & 3]);
             } else if constexpr (i == M1) {
-                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                // the row's lanes (col, 0..3): 16 apart, then 32 apart
+                const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
                 mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+                const auto sx = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                mx = fmaxf(__uint_as_float(sx[0]), __uint_as_float(sx[1]));
             } else if constexpr (i == M1 + 1) {
                 // lazy rescale: the reference max moves only when a row's max passes it by more than TAU
                 // (log2 units), or on the row's first visible keys
@@ -412,14 +449,14 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             }
             if constexpr (i >= E0) {
 #pragma unroll
-                for (int e = (i - E0) * 16 / NE; e < (i - E0 + 1) * 16 / NE; e++) {
-                    const int sb = e >> 3, j = 2 * (e & 7);
-                    f16x2 pp = {(f16)exp2_fast(sc[sb][j] - m_use), (f16)exp2_fast(sc[sb][j + 1] - m_use)};
+                for (int e = (i - E0) * 8 / NE; e < (i - E0 + 1) * 8 / NE; e++) {
+                    const int cq = e >> 1, j = 2 * (e & 1);
+                    f16x2 pp = {(f16)exp2_fast(sc[cq][j] - m_use), (f16)exp2_fast(sc[cq][j + 1] - m_use)};
                     // consumed here: otherwise the exponentials are sunk below the rescale branch that
                     // follows the step and issue after the last matrix instruction instead of beside them
                     asm volatile("" : "+v"(pp));
-                    pcur[sb][j >> 3][j & 7] = pp[0];
-                    pcur[sb][j >> 3][(j & 7) + 1] = pp[1];
+                    pcur[cq >> 1][(cq & 1) * 4 + j] = pp[0];
+                    pcur[cq >> 1][(cq & 1) * 4 + j + 1] = pp[1];
                     // the row sum adds the same half-precision weights the P.V product uses
                     ps[e & 1] = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.f, (f16)1.f}, ps[e & 1], false);
                 }
@@ -449,26 +486,22 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            pf_query_fused<D, IN_DT>(a, qraw, sW, row_ok ? t : 0, half, row_ok, qop);
+            pf_query_fused<D, IN_DT>(a, qraw, sW, row_ok ? t : 0, g, lane, row_ok, qop);
         } else {
 #pragma unroll
             for (int ks = 0; ks < NKS; ks++) qop[ks] = row_ok ? qop[ks] : f16x8{};
         }
-        // the Q fragments are only ever matrix-instruction operands: keep them in accumulation registers,
-        // leaving the vector registers to the softmax and the operand staging
-#pragma unroll
-        for (int ks = 0; ks < NKS; ks++) asm volatile("" : "+a"(qop[ks]));
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    qk_only(sK(lo & 1) + koff_lane);
+    qk_only(sK(lo & 1) + foff_lane);
 
     // one tile iteration; the first (QK^T only, no P.V) is peeled off by hand so that the loop body is
     // the full step alone
     auto iter = [&](auto do_pv, int kt) __attribute__((always_inline)) {
         constexpr bool DO_PV = decltype(do_pv)::value;
-        sc[0] = sn[0];
-        sc[1] = sn[1];
+#pragma unroll
+        for (int cq = 0; cq < 4; cq++) sc[cq] = sn[cq];
         // this wave's copies are complete; after the barrier every wave's are, and every wave is done
         // with the buffers this iteration's copies overwrite (K tile kt, V tile kt-2)
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -479,37 +512,33 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         }
         const int k0 = kt * PF_KT;
         if constexpr (QSA) {
-            // register j of lane (col, half) in block sb holds key 32*sb + 16*(j/8) + 8*half + j%8 of the
-            // tile: bit 16*(j/8) + 8*half + j%8 of word sb
+            // value i of chain cq = 2 b + s holds key 32 b + 8 g + 4 s + i of the tile: bit 8 g + 4 s + i of
+            // word b
 #pragma unroll
-            for (int sb = 0; sb < 2; sb++)
+            for (int cq = 0; cq < 4; cq++)
 #pragma unroll
-                for (int j = 0; j < 16; j++)
-                    sc[sb][j] = (((sb ? qw1 : qw0) >> (16 * (j >> 3) + 8 * half + (j & 7))) & 1u) ? sc[sb][j] : kNegInf;
+                for (int j = 0; j < 4; j++)
+                    sc[cq][j] = ((((cq >> 1) ? qw1 : qw0) >> (8 * g + 4 * (cq & 1) + j)) & 1u) ? sc[cq][j] : kNegInf;
             qsa_words(kt + 1);
         }
         if (k0 + PF_KT > wave_nomask) {
-            // causal edge: register j of lane (col, half) in block sb holds key
-            // k0 + 32*sb + 16*(j/8) + 8*half + j%8, visible to this lane's row when below len
-            const int lim = len - k0 - 8 * half;
+            // causal edge: value i of chain cq = 2 b + s holds key k0 + 32 b + 8 g + 4 s + i, visible to
+            // this lane's row when below len
+            const int lim = len - k0 - 8 * g;
 #pragma unroll
-            for (int sb = 0; sb < 2; sb++)
+            for (int cq = 0; cq < 4; cq++)
 #pragma unroll
-                for (int j = 0; j < 16; j++)
-                    sc[sb][j] = (32 * sb + 16 * (j >> 3) + (j & 7)) < lim ? sc[sb][j] : kNegInf;
+                for (int j = 0; j < 4; j++) sc[cq][j] = (32 * (cq >> 1) + 4 * (cq & 1) + j) < lim ? sc[cq][j] : kNegInf;
         }
-        const f16* Kb = sK((kt + 1) & 1) + koff_lane;  // tile kt+1 (stale past the last tile: unused)
-        const f16* Vb = sV((kt + 1) & 1) + voff_lane;  // tile kt-1 (no P.V on the first tile)
+        const f16* Kb = sK((kt + 1) & 1) + foff_lane;  // tile kt+1 (stale past the last tile: unused)
+        const f16* Vb = sV((kt + 1) & 1) + foff_lane;  // tile kt-1 (no P.V on the first tile)
         step(do_pv, Kb, Vb, kt);
         if (any_rescale) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) acc[dt] *= corr;
         }
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++) {
-            pprev[sb][0] = pcur[sb][0];
-            pprev[sb][1] = pcur[sb][1];
-        }
+        pprev[0] = pcur[0];
+        pprev[1] = pcur[1];
     };
     qsa_words(lo);
     iter(std::false_type{}, lo);
@@ -523,43 +552,43 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     }
     // the gates of this wave's rows, kept as loaded (bf16 pairs or fp32). Bf16 gates of a whole tile are
     // in flight during the last P.V (fp32 ones would need twice the registers and are loaded after it);
-    // a split tile's merging wave loads them after the merge. Accumulator registers 4*q4 .. 4*q4+3 of
-    // lane (col, half) hold dims 32*dt + 8*q4 + 4*half + 0..3.
+    // a split tile's merging wave loads them after the merge. Accumulator register i of dim tile dt of
+    // lane (col, g) holds dim 16*dt + 4*g + i.
     using graw_t = typename std::conditional<IN_DT == 0, f32x4, u32x2_t>::type;
-    graw_t graw[NDT][4];
-    const size_t gb = ((size_t)(row_ok ? t : 0) * a.NH + h) * 2 * D + D + 4 * half;
+    graw_t graw[NDT];
+    const size_t gb = ((size_t)(row_ok ? t : 0) * a.NH + h) * 2 * D + D + 4 * g;
     auto load_gates = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                if constexpr (IN_DT == 0)
-                    graw[dt][q4] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.qg) + gb + dt * 32 + 8 * q4);
-                else
-                    graw[dt][q4] = *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(a.qg) + gb + dt * 32 + 8 * q4);
-            }
+        for (int dt = 0; dt < NDT; dt++) {
+            if constexpr (IN_DT == 0)
+                graw[dt] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.qg) + gb + dt * 16);
+            else
+                graw[dt] = *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(a.qg) + gb + dt * 16);
+        }
     };
-    auto gate = [&](int dt, int q4, int i) __attribute__((always_inline)) -> float {
-        if constexpr (IN_DT == 0) return graw[dt][q4][i];
-        else return __uint_as_float((i & 1) ? graw[dt][q4][i >> 1] & 0xffff0000u : graw[dt][q4][i >> 1] << 16);
+    auto gate = [&](int dt, int i) __attribute__((always_inline)) -> float {
+        if constexpr (IN_DT == 0) return graw[dt][i];
+        else return __uint_as_float((i & 1) ? graw[dt][i >> 1] & 0xffff0000u : graw[dt][i >> 1] << 16);
     };
     constexpr bool kGateEarly = IN_DT == 1;
     if (kGateEarly && slot < 0) load_gates();
-    pv_only(sV((hi - 1) & 1) + voff_lane);
+    pv_only(sV((hi - 1) & 1) + foff_lane);
 
-    // ---- epilogue: l across the two lane halves, merge of a split tile, normalize, gate, store ----
+    // ---- epilogue: l across the row's four lanes, merge of a split tile, normalize, gate, store ----
     {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
         l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        const auto sx = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+        l_run = __uint_as_float(sx[0]) + __uint_as_float(sx[1]);
     }
     if (slot >= 0) {
-        // a wave's partial: accumulator chunk (dt, q4) of every lane as 1 KB, then (max, sum) per lane;
+        // a wave's partial: accumulator dim tile dt of every lane as 1 KB, then (max, sum) per lane;
         // each half of the tile has its own region (half 1: keys from lo > 0) and reads the other's
         constexpr int PSTR = pf_part_floats(D);
         const int own = lo > 0 ? 1 : 0;
-        float* pw = a.part + (((size_t)slot * 2 + own) * 4 + wave) * PSTR;
-        float* pr = a.part + (((size_t)slot * 2 + (1 - own)) * 4 + wave) * PSTR;
-        int* cw = a.cnt + slot * 4 + wave;
+        float* pw = a.part + (((size_t)slot * 2 + own) * kPfWaves + wave) * PSTR;
+        float* pr = a.part + (((size_t)slot * 2 + (1 - own)) * kPfWaves + wave) * PSTR;
+        int* cw = a.cnt + slot * kPfWaves + wave;
         const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(pw, (short)0, PSTR * 4, 0x00020000);
         const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(pr, (short)0, PSTR * 4, 0x00020000);
         const float mu = m_run == kNegInf ? 0.f : m_run;  // the offset the weights were taken against
@@ -568,14 +597,9 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             // first (as far as this wave can tell): publish the partial (device-coherent stores,
             // acknowledged before the arrival is counted), then count
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    const f32x4 o = {acc[dt][4 * q4], acc[dt][4 * q4 + 1], acc[dt][4 * q4 + 2], acc[dt][4 * q4 + 3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(o, rp, ((dt * 4 + q4) * 64 + lane) * 16, 0, kScDevice);
-                }
+            for (int dt = 0; dt < NDT; dt++) __builtin_amdgcn_raw_buffer_store_b128(acc[dt], rp, (dt * 64 + lane) * 16, 0, kScDevice);
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, f32x2{mu, l_run}), rp,
-                                                  NDT * 4 * 64 * 16 + lane * 8, 0, kScDevice);
+                                                  NDT * 64 * 16 + lane * 8, 0, kScDevice);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             int old = 0;
             if (lane == 0) old = __hip_atomic_fetch_add(cw, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -586,13 +610,11 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         asm volatile("" ::: "memory");
         // second: the partner's partial (published before its count) merged into this wave's, one dim
         // tile at a time with two more in flight (the whole partial in registers at once would spill)
-        const f32x2 ml2 = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rq, NDT * 4 * 64 * 16 + lane * 8, 0, kScDevice));
-        constexpr int NB = NDT < 3 ? NDT : 3;
-        f32x4 o2[NB][4];
+        const f32x2 ml2 = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rq, NDT * 64 * 16 + lane * 8, 0, kScDevice));
+        constexpr int NB = NDT < 6 ? NDT : 6;
+        f32x4 o2[NB];
         auto load_dt = [&](int dt) __attribute__((always_inline)) {
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++)
-                o2[dt % NB][q4] = __builtin_amdgcn_raw_buffer_load_b128(rq, ((dt * 4 + q4) * 64 + lane) * 16, 0, kScDevice);
+            o2[dt % NB] = __builtin_amdgcn_raw_buffer_load_b128(rq, (dt * 64 + lane) * 16, 0, kScDevice);
         };
         static_for<0, NB - 1>([&](auto ic) __attribute__((always_inline)) { load_dt(ic.value); });
         if (lane == 0) __hip_atomic_store(cw, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -610,12 +632,10 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
             if constexpr (dt + NB - 1 < NDT) load_dt(dt + NB - 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int q4 = 0; q4 < 4; q4++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float x = acc[dt][4 * q4 + i], y = o2[dt % NB][q4][i];
-                    acc[dt][4 * q4 + i] = __builtin_fmaf(own_first ? y : x, cs, (own_first ? x : y) * cf);
-                }
+            for (int i = 0; i < 4; i++) {
+                const float x = acc[dt][i], y = o2[dt % NB][i];
+                acc[dt][i] = __builtin_fmaf(own_first ? y : x, cs, (own_first ? x : y) * cf);
+            }
             __builtin_amdgcn_sched_barrier(0);
         });
     }
@@ -624,14 +644,12 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
         const size_t ob = ((size_t)t * a.NH + h) * D;
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
+        for (int dt = 0; dt < NDT; dt++) {
+            f32x4 o;
 #pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                f32x4 o;
-#pragma unroll
-                for (int i = 0; i < 4; i++) o[i] = acc[dt][4 * q4 + i] * inv * sigmoid(gate(dt, q4, i));
-                *reinterpret_cast<f32x4*>(a.out + ob + dt * 32 + 8 * q4 + 4 * half) = o;
-            }
+            for (int i = 0; i < 4; i++) o[i] = acc[dt][i] * inv * sigmoid(gate(dt, i));
+            *reinterpret_cast<f32x4*>(a.out + ob + dt * 16 + 4 * g) = o;
+        }
     }
 }
 
@@ -640,7 +658,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
 // first x tiles, then the short tile, x = max(0, nl - ceil(T/2)). With n_qt odd the last workgroup
 // runs the middle tile alone.
 template <int D, int IN_DT, bool QF, bool QSA>
-__global__ __launch_bounds__(256, 1) void k_prefill(PrefillArgs a) {
+__global__ __launch_bounds__(64 * kPfWaves, 1) void k_prefill(PrefillArgs a) {
     const int G = a.NH / a.NKV;
     const int tok_per_blk = PF_ROWS / G;
     const int n_qt = (a.n + tok_per_blk - 1) / tok_per_blk;
@@ -682,7 +700,7 @@ static hipError_t launch_pf_d(const PrefillArgs& a, int q_dtype, int in_dtype, h
     // the split tiles' partial slots and counters are the caller's (sized for `slots` per KV head)
     if (a.n < 1 || a.slots != pf_split_slots(n_qt, a.split_all) || (a.slots > 0 && (!a.part || !a.cnt)))
         return hipErrorInvalidValue;
-    const dim3 grid((a.split_all ? 2 : 1) * n_qt * a.NKV), block(256);
+    const dim3 grid((a.split_all ? 2 : 1) * n_qt * a.NKV), block(64 * kPfWaves);
     // two buffers of a K and a V tile; with in-kernel query normalization, the D norm multipliers after them
     const size_t shm = 2 * 2 * (size_t)C::TILEE * 2 + (a.q ? 0 : D * sizeof(float));
     auto go = [&](auto kern) {

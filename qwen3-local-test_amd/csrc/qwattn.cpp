@@ -254,10 +254,10 @@ int qwattn_create(qwattn_ctx** out, int device, const qwattn_config* cfg) {
     const size_t qn = (size_t)cfg->max_tokens * NH * D;
     // prefill split slots per KV head: a pair of query tiles each (paired schedule) or a tile each (split
     // schedule, only while two workgroups per tile fit the CUs), at least one so the pointers are never
-    // null; 4 waves each, a partial region per half of the split tile
+    // null; kPfWaves waves each, a partial region per half of the split tile
     const int qt_max = qw::pf_query_tiles(cfg->max_tokens, NH / NKV);
     c->pf_slots_per_head = std::max(1, std::max(qt_max / 2, std::min(qt_max, c->n_cu / (2 * NKV))));
-    const size_t pf_slots = (size_t)NKV * c->pf_slots_per_head * 4;
+    const size_t pf_slots = (size_t)NKV * c->pf_slots_per_head * qw::kPfWaves;
     c->qsa_hist_n = std::min(cfg->max_tokens, qw::kQsaHistTokens);
     const size_t hist_tokens = (size_t)c->qsa_hist_n;
     bool ok = hipMalloc(&c->pf_part, sizeof(float) * 2 * pf_slots * qw::pf_part_floats(D)) == hipSuccess &&
