@@ -29,6 +29,8 @@
 //    its first x tiles and then the whole short tile, with x chosen so both get half the pair's tiles.
 //    The two halves of the long tile are merged by whichever wave finishes its half last (per-wave
 //    arrival counters, log-sum-exp merge of the stored partial), so no workgroup ever waits on another.
+//    The workgroup with two segments loads the short tile's query rows and first two K tiles during
+//    the long prefix's last P.V and merge, so its second segment starts without a load round trip.
 //    Launches small enough that two workgroups per tile fit the CUs split every tile's keys in two
 //    instead (same merge), so chunks of up to ~1,024 tokens still fill the chip.
 #include "common.hpp"
@@ -219,6 +221,10 @@ __device__ __forceinline__ void pf_query_fused(const PrefillArgs& a, const PfQRa
     if constexpr (NKS >= 8) if (a.R == 256) pf_query_finish<D, IN_DT, 4>(a, raw, sW, rs, t, g, lane, qop);
 }
 
+// Whether a workgroup's first segment hands the next one its query rows and first K tiles: for rows
+// normalized in the kernel from bf16 (the fp32 rows would need twice the registers through the hand-over).
+constexpr bool pf_handover(bool qf, int in_dt) { return qf && in_dt == 1; }
+
 // Key tiles of query tile qt: keys [0, pos + last token of the tile + 1) in 64-key tiles.
 __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, int qt) {
     return (a.pos + min(a.n - 1, (qt + 1) * tok_per_blk - 1) + 1 + PF_KT - 1) / PF_KT;
@@ -230,8 +236,15 @@ __device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int tok_per_blk, i
 // (accumulator, reference max, sum) in its half's region of the pair's slot and counts its arrival,
 // unless the partner wave has already arrived; the wave that arrives second merges the two (in a fixed
 // order) and writes the rows, then clears the counter for the next launch.
-template <int D, int IN_DT, bool QF, bool QSA>
-__device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot) {
+// Hand-over between a workgroup's two segments (bf16 rows normalized in the kernel): the first segment,
+// told the next one's query tile (next_qt >= 0), issues that tile's raw query loads (into `carry`) and
+// the copies of its first two K tiles right after its own loop, so they complete during its last P.V,
+// merge and stores; the second (PRE) starts from them, and from the norm multipliers already in LDS.
+template <int D, int IN_DT, bool QF, bool QSA, bool PRE>
+__device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt, int lo, int hi, int slot,
+                                           int next_qt, PfQRaw<D, IN_DT>& carry) {
+    constexpr bool NEXT = pf_handover(QF, IN_DT) && !PRE;
+    static_assert(!PRE || pf_handover(QF, IN_DT), "hand-over only for in-kernel bf16 rows");
     using C = PfCfg<D>;
     constexpr int NKS = C::NKS, NDT = C::NDT, BLKE = C::BLKE, TILEE = C::TILEE, LOADS = C::LOADS;
     constexpr int NQK = 4 * NKS, NPV = 2 * NDT;  // matrix instructions a tile: QK^T, P.V (D/8 each)
@@ -280,7 +293,9 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     PfQRaw<D, IN_DT> qraw;
     float* sW = reinterpret_cast<float*>(smem + (size_t)4 * C::TILEE * 2);
     f32x4 wq{};
-    if constexpr (QF) {
+    if constexpr (PRE) {
+        qraw = carry;  // loaded by the previous segment (lo = 0: tiles 0 and 1 are in the K buffers)
+    } else if constexpr (QF) {
         if (wave == 0 && lane < D / 4) wq = *reinterpret_cast<const f32x4*>(a.qn + 4 * lane);
         qraw.load(a, row_ok ? t : 0, h, g);
     } else {
@@ -473,12 +488,18 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     // one, in two buffers each (tile kt in buffer kt & 1), with one barrier per iteration. The buffers
     // are free here: the previous segment's last barrier follows its last K read, and its last V tile
     // is only overwritten after the first barrier of the loop below.
-    copy_tile(rk, sK(lo & 1), lo);
-    if (lo + 1 < hi) copy_tile(rk, sK((lo + 1) & 1), lo + 1);
+    // (tile lo + 1 even past hi: the buffer is free and the copy reads zeros or unused blocks, and a
+    // fixed number of copies lets the query's loads be waited for without waiting for any copy)
+    if constexpr (!PRE) {
+        copy_tile(rk, sK(lo & 1), lo);
+        copy_tile(rk, sK((lo + 1) & 1), lo + 1);
+    }
     {
         // the Q^T operand, while the copies fly (the query loads were issued before them). sW is free:
         // every wave finished the previous segment's reads of it many barriers ago
-        if constexpr (QF) {
+        if constexpr (PRE) {
+            pf_query_fused<D, IN_DT>(a, qraw, sW, row_ok ? t : 0, g, lane, row_ok, qop);
+        } else if constexpr (QF) {
             if (wave == 0 && lane < D / 4)
                 *reinterpret_cast<f32x4*>(sW + 4 * lane) = f32x4{1.0f + wq[0], 1.0f + wq[1], 1.0f + wq[2], 1.0f + wq[3]};
             // a barrier for the LDS write alone (__syncthreads would also wait for the copies in flight)
@@ -549,6 +570,16 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     if (hi * PF_KT > maxlen) {
         zero_tail(sV((hi - 1) & 1), hi - 1);
         __syncthreads();
+    }
+    if constexpr (NEXT) {
+        // the next segment's rows and K tiles 0 and 1 (both K buffers are free past the barrier above;
+        // nothing before the next segment's first barrier reads them)
+        if (next_qt >= 0) {
+            const int tn = next_qt * tok_per_blk + r / G;
+            carry.load(a, tn < a.n ? tn : 0, h, g);
+            copy_tile(rk, sK(0), 0);
+            copy_tile(rk, sK(1), 1);
+        }
     }
     // the gates of this wave's rows, kept as loaded (bf16 pairs or fp32). Bf16 gates of a whole tile are
     // in flight during the last P.V (fp32 ones would need twice the registers and are loaded after it);
@@ -686,9 +717,17 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void k_prefill(PrefillArgs a) {
             q0 = p, lo0 = 0, hi0 = ns;
         }
     }
-    // one call site, so the segment body exists once in the code object
-    for (int s = 0; s < nseg; s++)
-        pf_segment<D, IN_DT, QF, QSA>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0);
+    PfQRaw<D, IN_DT> carry;
+    if constexpr (pf_handover(QF, IN_DT)) {
+        // two call sites: the rows handed over are live only between the first segment's loop and the
+        // second's prologue (through one runtime segment loop they would stay live through every tile)
+        pf_segment<D, IN_DT, QF, QSA, false>(a, kvh, q0, lo0, hi0, slot0, nseg == 2 ? q1 : -1, carry);
+        if (nseg == 2) pf_segment<D, IN_DT, QF, QSA, true>(a, kvh, q1, 0, hi1, -1, -1, carry);
+    } else {
+        // one call site, so the segment body exists once in the code object
+        for (int s = 0; s < nseg; s++)
+            pf_segment<D, IN_DT, QF, QSA, false>(a, kvh, s ? q1 : q0, s ? 0 : lo0, s ? hi1 : hi0, s ? -1 : slot0, -1, carry);
+    }
 }
 
 template <int D>
