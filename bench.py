@@ -691,9 +691,12 @@ def main():
         "workloads": results,
     }
     if head:
+        # dim slices per combined row, as the library picks them (combine_slices in csrc/qwattn.cpp)
+        nds = next((k for k in (4, 2) if 2 * (NH // NKV) * k <= head["splits"]), 1)
         line["roofline"] = {"bound": "hbm",
                             "kernel": f"k_decode_ld<256,1,0> (one launch: {head['splits']}x{NKV} streaming "
-                                      f"workgroups, the last {NH // NKV} of each KV head combining one row each)",
+                                      f"workgroups, the last {NH // NKV * nds} of each KV head combining a "
+                                      f"{256 // nds}-dim slice of one output row each)",
                             "achieved": round(head["algorithmic_bytes"] / (head["us_main"] * 1e-6) / 1e9, 2),
                             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                             "frac": round(head["frac_hbm_kernel"], 4),
@@ -704,7 +707,8 @@ def main():
     if pf:
         line["prefill_roofline"] = {"bound": "mfma",
                                     "kernel": "k_prefill<256,1,true> (query rows normalized and rotated in the "
-                                              "kernel from bf16 projections, bf16 gate; paired schedule, grid 256)",
+                                              "kernel from bf16 projections, bf16 gate; 8 waves x 16 rows, two a SIMD, 16x16x32 "
+                                              "MFMAs; paired schedule, grid 256)",
                                     "achieved": round(pf["algorithmic_flops"] / (pf["us_main"] * 1e-6) / 1e12, 2),
                                     "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                                     "frac": round(pf["frac_mfma_kernel"], 4),
