@@ -288,7 +288,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
     // ---- Q^T operand in registers: lane (col, g) holds row `col`, dims 32*kk + 8*g .. +8 -------------
     // the loads are issued here, the operand finished once the first K tiles' copies are in flight.
     // In-kernel normalization: the norm multipliers 1 + qn go to LDS (after the four tile buffers), loaded
-    // by wave 0 ahead of every other load of the segment
+    // by wave 0 ahead of every other load of the first segment (a second segment finds them there)
     f16x8 qop[NKS];
     PfQRaw<D, IN_DT> qraw;
     float* sW = reinterpret_cast<float*>(smem + (size_t)4 * C::TILEE * 2);
@@ -420,7 +420,7 @@ __device__ __forceinline__ void pf_segment(const PrefillArgs& a, int kvh, int qt
         bool grow = false;
         static_for<0, NSLOT>([&](auto ic) __attribute__((always_inline)) {
             constexpr int i = decltype(ic)::value;
-            // staging copies for the next iteration (K tile kt+2, V tile kt), one every third slot: issued
+            // staging copies for the next iteration (K tile kt+2, V tile kt), one every sixth slot: issued
             // in one burst they would fill the vector-memory queue and stall the wave until it drains.
             // Past the last tile they read zeros (range-checked) or unused blocks into free buffers.
             if constexpr (i % 6 == 0 && i / 6 < 2 * LOADS) {
