@@ -585,6 +585,10 @@ CASES_PF_QG = [
     (Shape(16, 2, 256, 256), 64, 700, "bf16"),   # R = D = 256: eight k-steps away
     (Shape(16, 2, 256, 0), 100, 100, "bf16"),    # no rope
     (QWEN3_NEXT, 2048, 2048, "f32"),             # the bench shape with fp32 projections
+    # paired schedules with bf16 rows: the two-segment workgroups take their second segment's query rows
+    # and first K tiles from the first segment
+    (Shape(8, 2, 128, 64), 300, 2200, "bf16"),   # D = 128, (cos, sin) loaded with the rows; a middle tile
+    (Shape(4, 1, 64, 32), 100, 4200, "bf16"),    # D = 64, the R = 32 cross-lane partner
 ]
 
 
